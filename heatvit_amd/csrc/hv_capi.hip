@@ -1,0 +1,380 @@
+// hv_capi.hip -- extern "C" entry points of libheatvit_hip.so and the host
+// orchestration of the block, selector and full-model forwards.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "hv_device.h"
+#include "hv_internal.h"
+
+namespace hv {
+
+static thread_local char g_err[512];
+
+int fail(int status, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+int check_hip(hipError_t e, const char *what) {
+  if (e == hipSuccess) return HV_OK;
+  return fail(HV_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// ---------------------------------------------------------------- utilities
+
+__global__ void k_init_offsets(int32_t *offsets, uint8_t *pkg, int32_t *token_counts, int batch,
+                               int rows) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i <= batch) offsets[i] = i * rows;
+  if (i < batch) {
+    pkg[i] = 0;
+    if (token_counts)
+      for (int s = 0; s < 4; ++s) token_counts[(size_t)i * 4 + s] = rows;
+  }
+}
+
+int launch_init_offsets(int32_t *offsets, uint8_t *pkg, int32_t *token_counts, int batch,
+                        int rows, hipStream_t s) {
+  hipLaunchKernelGGL(k_init_offsets, dim3((batch + 256) / 256), dim3(256), 0, s, offsets, pkg,
+                     token_counts, batch, rows);
+  return check_hip(hipGetLastError(), "k_init_offsets launch");
+}
+
+__global__ void k_copy_ckpt(const int8_t *x, const int32_t *offsets, int8_t *ckpt,
+                            int32_t *ckpt_rows, int slot) {
+  const int b = blockIdx.x;
+  const int r0 = offsets[b], n = offsets[b + 1] - r0;
+  int8_t *dst = ckpt + ((size_t)b * 17 + slot) * 197 * 192;
+  for (int i = threadIdx.x; i < n * 12; i += blockDim.x)
+    reinterpret_cast<v4i *>(dst)[i] = reinterpret_cast<const v4i *>(x + (size_t)r0 * 192)[i];
+  if (threadIdx.x == 0 && ckpt_rows) ckpt_rows[(size_t)b * 17 + slot] = n;
+}
+
+int launch_copy_ckpt(const int8_t *x, const int32_t *offsets, int batch, int8_t *ckpt,
+                     int32_t *ckpt_rows, int slot, hipStream_t s) {
+  hipLaunchKernelGGL(k_copy_ckpt, dim3(batch), dim3(256), 0, s, x, offsets, ckpt, ckpt_rows,
+                     slot);
+  return check_hip(hipGetLastError(), "k_copy_ckpt launch");
+}
+
+// Bump allocator over the caller's workspace (256-byte aligned slices).
+struct Carve {
+  uint8_t *base;
+  size_t cap, used = 0;
+  bool ok = true;
+  template <class T>
+  T *take(size_t count) {
+    size_t off = (used + 255) & ~(size_t)255;
+    size_t bytes = count * sizeof(T);
+    if (base && off + bytes > cap) ok = false;
+    used = off + bytes;
+    return base && ok ? reinterpret_cast<T *>(base + off) : nullptr;
+  }
+};
+
+struct BlockWs {
+  int8_t *ln, *qkv, *ctx, *y, *hidden;
+};
+
+static BlockWs carve_block(Carve &cv, size_t rows) {
+  BlockWs w;
+  w.ln = cv.take<int8_t>(rows * 192);
+  w.qkv = cv.take<int8_t>(rows * 576);
+  w.ctx = cv.take<int8_t>(rows * 192);
+  w.y = cv.take<int8_t>(rows * 192);
+  w.hidden = cv.take<int8_t>(rows * 768);
+  return w;
+}
+
+// transformer_block (transformer.py:401-431) on rows [0, offsets[batch]).
+static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *offsets,
+                         int batch, int max_rows, int8_t *z, const hv_block_ckpt *ck,
+                         const BlockWs &w, hipStream_t s) {
+  const int32_t *rows_dev = offsets + batch;
+  int8_t *ln1 = ck && ck->ln1 ? ck->ln1 : w.ln;
+  int8_t *qkv = ck && ck->fused_qkv ? ck->fused_qkv : w.qkv;
+  int8_t *ctx = ck && ck->concat ? ck->concat : w.ctx;
+  int8_t *y = ck && ck->y ? ck->y : w.y;
+  int8_t *ln2 = ck && ck->ln2 ? ck->ln2 : w.ln;
+  int8_t *hidden = ck && ck->hidden ? ck->hidden : w.hidden;
+  int rc;
+
+  rc = launch_layernorm(x, p.ln1_gamma, p.ln1_beta, ln1, max_rows, rows_dev, p.x_exp,
+                        p.gamma1_exp, p.beta1_exp, p.ln1_out_exp, nullptr, s);
+  if (rc) return rc;
+  GemmArgs g{};
+  g.a = ln1; g.b = p.wqkv_p; g.bias = p.bqkv; g.c = qkv; g.m_dev = rows_dev;
+  g.m = max_rows; g.n = 576; g.k = 192; g.lda = 192; g.ldc = 576;
+  g.shift_a = p.qkv_out_exp - (p.ln1_out_exp + p.wqkv_exp);
+  if ((rc = launch_gemm(g, A_ROWS, HV_EPI_I8, s))) return rc;
+
+  AttnArgs a{};
+  a.qkv = qkv; a.offsets = offsets; a.ctx = ctx; a.batch = batch;
+  a.score = ck ? ck->score : nullptr;
+  a.prob = ck ? ck->prob : nullptr;
+  a.score_shift = p.score_exp - 2 * p.qkv_out_exp;
+  a.q16_shift = -(p.score_exp + 13);
+  a.ctx_shift = p.context_out_exp - (p.prob_exp + p.qkv_out_exp);
+  if ((rc = launch_attention(a, s))) return rc;
+
+  g = GemmArgs{};
+  g.a = ctx; g.b = p.wproj_p; g.bias = p.bproj; g.c = y; g.res = x; g.aux = ck ? ck->msa : nullptr;
+  g.m_dev = rows_dev; g.m = max_rows; g.n = 192; g.k = 192; g.lda = 192; g.ldc = 192; g.ldr = 192;
+  g.shift_a = p.msa_out_exp - (p.context_out_exp + p.wproj_exp);
+  g.mid_exp = p.msa_out_exp; g.res_exp = p.x_exp; g.out_exp = p.ffn_x_exp;
+  if ((rc = launch_gemm(g, A_ROWS, HV_EPI_RESIDUAL, s))) return rc;
+
+  rc = launch_layernorm(y, p.ln2_gamma, p.ln2_beta, ln2, max_rows, rows_dev, p.ffn_x_exp,
+                        p.gamma2_exp, p.beta2_exp, p.ln2_out_exp, nullptr, s);
+  if (rc) return rc;
+  g = GemmArgs{};
+  g.a = ln2; g.b = p.w1_p; g.bias = p.b1; g.c = hidden; g.m_dev = rows_dev;
+  g.m = max_rows; g.n = 768; g.k = 192; g.lda = 192; g.ldc = 768;
+  g.shift_a = -16 - (p.ln2_out_exp + p.w1_exp);
+  g.shift_b = p.hidden_out_exp + 16;
+  if ((rc = launch_gemm(g, A_ROWS, HV_EPI_GELU, s))) return rc;
+
+  g = GemmArgs{};
+  g.a = hidden; g.b = p.w2_p; g.bias = p.b2; g.c = z; g.res = y;
+  g.aux = ck ? ck->ffn_out : nullptr;
+  g.m_dev = rows_dev; g.m = max_rows; g.n = 192; g.k = 768; g.lda = 768; g.ldc = 192; g.ldr = 192;
+  g.shift_a = p.ffn_out_exp - (p.hidden_out_exp + p.w2_exp);
+  g.mid_exp = p.ffn_out_exp; g.res_exp = p.ffn_x_exp; g.out_exp = p.out_exp;
+  return launch_gemm(g, A_ROWS, HV_EPI_RESIDUAL, s);
+}
+
+static bool exp_ok(int e) { return e >= -32 && e <= 31; }
+
+static int check_block(const hv_block_dev &p) {
+  const int e[] = {p.x_exp, p.gamma1_exp, p.beta1_exp, p.ln1_out_exp, p.wqkv_exp,
+                   p.qkv_out_exp, p.score_exp, p.prob_exp, p.context_out_exp, p.wproj_exp,
+                   p.msa_out_exp, p.ffn_x_exp, p.gamma2_exp, p.beta2_exp, p.ln2_out_exp,
+                   p.w1_exp, p.hidden_out_exp, p.w2_exp, p.ffn_out_exp, p.out_exp};
+  for (int v : e)
+    if (!exp_ok(v)) return fail(HV_EVALUE, "block scale exponent %d outside [-32, 31]", v);
+  if (p.x_exp > 0 || p.ffn_x_exp > 0)
+    return fail(HV_EVALUE, "layernorm input scale must be in [-32, 0]");
+  return HV_OK;
+}
+
+}  // namespace hv
+
+using namespace hv;
+
+extern "C" {
+
+const char *hv_last_error(void) { return g_err; }
+
+int hv_abi_version(void) { return 1; }
+
+int hv_eval_primitive(int op, const int64_t *in, int64_t *out, int64_t n, int a, int b, int c,
+                      hv_stream_t stream) {
+  g_err[0] = 0;
+  return launch_primitive(op, in, out, n, a, b, c, (hipStream_t)stream);
+}
+
+int hv_softmax_rows(const int32_t *x, const int32_t *offsets, int rows, uint8_t *attention,
+                    int32_t *selector, hv_stream_t stream) {
+  g_err[0] = 0;
+  return launch_softmax_rows(x, offsets, rows, attention, selector, (hipStream_t)stream);
+}
+
+int hv_layernorm_i8(const int8_t *x, const int8_t *gamma, const int8_t *beta, int8_t *y,
+                    int rows, const int32_t *rows_dev, int x_exp, int gamma_exp, int beta_exp,
+                    int out_exp, uint8_t *neg_var, hv_stream_t stream) {
+  g_err[0] = 0;
+  return launch_layernorm(x, gamma, beta, y, rows, rows_dev, x_exp, gamma_exp, beta_exp,
+                          out_exp, neg_var, (hipStream_t)stream);
+}
+
+int hv_gemm_i8(const hv_gemm_desc *d, hv_stream_t stream) {
+  g_err[0] = 0;
+  if (!d) return fail(HV_EVALUE, "gemm: null descriptor");
+  GemmArgs g{};
+  g.a = d->a; g.a_rows = d->a_rows; g.b = d->b_packed; g.bias = d->bias; g.c = d->c;
+  g.res = d->residual; g.aux = d->aux; g.m_dev = d->m_dev;
+  g.m = d->m; g.n = d->n; g.k = d->k; g.lda = d->lda; g.ldc = d->ldc; g.ldr = d->ldr;
+  switch (d->epilogue) {
+    case HV_EPI_I8:
+    case HV_EPI_I32: g.shift_a = d->dst_exp - d->src_exp; break;
+    case HV_EPI_GELU:
+      g.shift_a = -16 - d->src_exp;
+      g.shift_b = d->dst_exp + 16;
+      break;
+    case HV_EPI_RESIDUAL:
+      if (!d->residual) return fail(HV_EVALUE, "gemm: residual epilogue needs a residual");
+      g.shift_a = d->mid_exp - d->src_exp;
+      g.mid_exp = d->mid_exp; g.res_exp = d->res_exp; g.out_exp = d->dst_exp;
+      break;
+    default: return fail(HV_EVALUE, "gemm: bad epilogue %d", d->epilogue);
+  }
+  if (d->a_mode == HV_A_GATHER && !d->a_rows) return fail(HV_EVALUE, "gemm: gather without rows");
+  return launch_gemm(g, d->a_mode, d->epilogue, (hipStream_t)stream);
+}
+
+size_t hv_block_workspace_bytes(int batch, int max_rows) {
+  (void)batch;
+  Carve cv{nullptr, 0};
+  carve_block(cv, (size_t)max_rows);
+  return cv.used + 256;
+}
+
+int hv_block_forward(const hv_block_dev *p, const int8_t *x, const int32_t *offsets, int batch,
+                     int max_rows, int8_t *z, const hv_block_ckpt *ck, void *workspace,
+                     size_t workspace_bytes, hv_stream_t stream) {
+  g_err[0] = 0;
+  if (!p || !x || !offsets || !z) return fail(HV_EVALUE, "block: null argument");
+  if (batch <= 0 || max_rows <= 0) return fail(HV_EVALUE, "block: empty batch");
+  int rc = check_block(*p);
+  if (rc) return rc;
+  Carve cv{(uint8_t *)workspace, workspace_bytes};
+  BlockWs w = carve_block(cv, (size_t)max_rows);
+  if (!cv.ok || !workspace) return fail(HV_EVALUE, "block: workspace too small");
+  return block_forward(*p, x, offsets, batch, max_rows, z, ck, w, (hipStream_t)stream);
+}
+
+size_t hv_selector_workspace_bytes(int batch) {
+  (void)batch;
+  return 0;
+}
+
+int hv_selector_forward(const hv_selector_dev *p, const int8_t *tokens, const int32_t *offsets,
+                        const uint8_t *pkg_in, int batch, int8_t *out_tokens,
+                        int32_t *out_offsets, uint8_t *pkg_out, int32_t *fused,
+                        int32_t *kept_index, int32_t *state, const hv_selector_ckpt *ck,
+                        void *workspace, size_t workspace_bytes, hv_stream_t stream) {
+  g_err[0] = 0;
+  (void)workspace;
+  (void)workspace_bytes;
+  if (!p || !tokens || !offsets || !out_tokens || !out_offsets || !pkg_out || !fused ||
+      !kept_index || !state)
+    return fail(HV_EVALUE, "selector: null argument");
+  SelectorArgs a{};
+  a.p = p; a.tokens = tokens; a.offsets = offsets; a.pkg_in = pkg_in; a.batch = batch;
+  a.out_tokens = out_tokens; a.out_offsets = out_offsets; a.pkg_out = pkg_out; a.fused = fused;
+  a.kept_index = kept_index; a.state = state;
+  if (ck) a.ck = *ck;
+  return launch_selector(a, (hipStream_t)stream);
+}
+
+int hv_selector_finalize(const int8_t *tokens, const int32_t *offsets, const uint8_t *pkg_in,
+                         const int32_t *fused, int batch, int8_t *out_tokens,
+                         int32_t *out_offsets, uint8_t *pkg_out, int32_t *kept_index,
+                         int32_t *state, hv_stream_t stream) {
+  g_err[0] = 0;
+  if (!tokens || !offsets || !fused || !out_tokens || !out_offsets || !pkg_out || !kept_index ||
+      !state)
+    return fail(HV_EVALUE, "finalize: null argument");
+  SelectorArgs a{};
+  a.p = nullptr; a.tokens = tokens; a.offsets = offsets; a.pkg_in = pkg_in; a.batch = batch;
+  a.out_tokens = out_tokens; a.out_offsets = out_offsets; a.pkg_out = pkg_out;
+  a.fused = const_cast<int32_t *>(fused); a.kept_index = kept_index; a.state = state;
+  return launch_selector(a, (hipStream_t)stream);
+}
+
+int hv_patch_embedding(const hv_patch_dev *p, const int8_t *images, int batch, int8_t *x,
+                       hv_stream_t stream) {
+  g_err[0] = 0;
+  if (!p || !images || !x) return fail(HV_EVALUE, "patch: null argument");
+  const int e[] = {p->image_exp, p->weight_exp, p->activation_exp, p->tokens_exp, p->cls_exp,
+                   p->pos_exp};
+  for (int v : e)
+    if (!exp_ok(v)) return fail(HV_EVALUE, "patch scale exponent %d outside [-32, 31]", v);
+  return launch_patch_embed(*p, images, batch, x, (hipStream_t)stream);
+}
+
+struct ModelWs {
+  int8_t *xa, *xb;
+  BlockWs blk;
+  int32_t *off_a, *off_b, *fused, *kept, *state;
+  uint8_t *pkg_a, *pkg_b;
+};
+
+static ModelWs carve_model(Carve &cv, int batch) {
+  const size_t rows = (size_t)batch * HV_MAX_TOKENS;
+  ModelWs w;
+  w.xa = cv.take<int8_t>(rows * 192);
+  w.xb = cv.take<int8_t>(rows * 192);
+  w.blk = carve_block(cv, rows);
+  w.off_a = cv.take<int32_t>(batch + 1);
+  w.off_b = cv.take<int32_t>(batch + 1);
+  w.fused = cv.take<int32_t>((size_t)batch * 196);
+  w.kept = cv.take<int32_t>((size_t)batch * 196);
+  w.state = cv.take<int32_t>((size_t)batch * 3 * 5);
+  w.pkg_a = cv.take<uint8_t>(batch);
+  w.pkg_b = cv.take<uint8_t>(batch);
+  return w;
+}
+
+size_t hv_model_workspace_bytes(int batch) {
+  Carve cv{nullptr, 0};
+  carve_model(cv, batch);
+  return cv.used + 256;
+}
+
+int hv_model_forward(const hv_model_dev *p, const int8_t *images, int batch, int32_t *logits,
+                     int32_t *token_counts, int32_t *state, int8_t *ckpt, int32_t *ckpt_rows,
+                     void *workspace, size_t workspace_bytes, hv_stream_t stream) {
+  g_err[0] = 0;
+  hipStream_t s = (hipStream_t)stream;
+  if (!p || !images || !logits) return fail(HV_EVALUE, "model: null argument");
+  if (batch <= 0) return fail(HV_EVALUE, "model: empty batch");
+  if ((long long)batch * HV_MAX_TOKENS * 768 > 0x7fffffffLL)
+    return fail(HV_EVALUE, "model: batch %d too large", batch);
+  if (p->n_selectors < 0 || p->n_selectors > 3) return fail(HV_EVALUE, "model: bad selector count");
+  for (int i = 0; i < 12; ++i) {
+    int rc = check_block(p->blocks[i]);
+    if (rc) return rc;
+  }
+  if (p->blocks[11].out_exp > 0) return fail(HV_EVALUE, "layernorm input scale must be in [-32, 0]");
+  Carve cv{(uint8_t *)workspace, workspace_bytes};
+  ModelWs w = carve_model(cv, batch);
+  if (!cv.ok || !workspace) return fail(HV_EVALUE, "model: workspace too small");
+  const int max_rows = batch * HV_MAX_TOKENS;
+  int32_t *st = state ? state : w.state;
+  int rc;
+
+  if ((rc = launch_init_offsets(w.off_a, w.pkg_a, token_counts, batch, HV_MAX_TOKENS, s))) return rc;
+  if ((rc = launch_patch_embed(p->patch, images, batch, w.xa, s))) return rc;
+  if (ckpt && (rc = launch_copy_ckpt(w.xa, w.off_a, batch, ckpt, ckpt_rows, 0, s))) return rc;
+
+  int sel = 0;
+  for (int blk = 1; blk <= 12; ++blk) {
+    if (sel < p->n_selectors && p->selector_blocks[sel] == blk) {
+      SelectorArgs a{};
+      a.p = &p->selectors[sel];
+      a.tokens = w.xa; a.offsets = w.off_a; a.pkg_in = w.pkg_a; a.batch = batch;
+      a.out_tokens = w.xb; a.out_offsets = w.off_b; a.pkg_out = w.pkg_b;
+      a.fused = w.fused; a.kept_index = w.kept; a.state = st + (size_t)sel * batch * 5;
+      a.token_counts = token_counts; a.stage = sel + 1;
+      if ((rc = launch_selector(a, s))) return rc;
+      std::swap(w.xa, w.xb);
+      std::swap(w.off_a, w.off_b);
+      std::swap(w.pkg_a, w.pkg_b);
+      ++sel;
+      if (ckpt && (rc = launch_copy_ckpt(w.xa, w.off_a, batch, ckpt, ckpt_rows, sel, s))) return rc;
+    }
+    if ((rc = block_forward(p->blocks[blk - 1], w.xa, w.off_a, batch, max_rows, w.xb, nullptr,
+                            w.blk, s)))
+      return rc;
+    std::swap(w.xa, w.xb);
+    if (ckpt && (rc = launch_copy_ckpt(w.xa, w.off_a, batch, ckpt, ckpt_rows, 3 + blk, s))) return rc;
+  }
+  // Final LayerNorm over every row (model.py:102-106), head on CLS rows.
+  if ((rc = launch_layernorm(w.xa, p->final_gamma, p->final_beta, w.blk.ln, max_rows,
+                             w.off_a + batch, p->blocks[11].out_exp, p->final_gamma_exp,
+                             p->final_beta_exp, p->final_ln_out_exp, nullptr, s)))
+    return rc;
+  if (ckpt && (rc = launch_copy_ckpt(w.blk.ln, w.off_a, batch, ckpt, ckpt_rows, 16, s))) return rc;
+  GemmArgs g{};
+  g.a = w.blk.ln; g.a_rows = w.off_a; g.b = p->head_w_p; g.bias = p->head_b; g.c = logits;
+  g.m = batch; g.n = 1000; g.k = 192; g.lda = 192; g.ldc = 1000;
+  g.shift_a = -14 - (p->final_ln_out_exp + p->head_w_exp);
+  return launch_gemm(g, A_GATHER, HV_EPI_I32, s);
+}
+
+}  // extern "C"

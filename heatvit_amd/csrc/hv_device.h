@@ -1,0 +1,200 @@
+// hv_device.h -- device-side integer primitives of HeatViT-T's golden model.
+//
+// Each helper restates one reference function bit for bit on the ranges
+// its call sites reach (noted per helper); the kernels use them in their
+// epilogues.  Exponent-dependent shifts are uniform per launch, so the
+// branches below do not diverge within a wavefront.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hv {
+
+typedef long long i64;
+typedef unsigned long long u64;
+typedef __int128 i128;
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// ---------------------------------------------------------------- fixed.py
+
+// round_shift_away (fixed.py:15-25) for shift >= 0 and |v| < 2^62.
+__device__ __forceinline__ i64 rsa_pos(i64 v, int s) {
+  if (s == 0) return v;
+  if (s >= 63) return 0;
+  u64 mag = v < 0 ? (u64)(-v) : (u64)v;
+  mag = (mag + (1ull << (s - 1))) >> s;
+  return v < 0 ? -(i64)mag : (i64)mag;
+}
+
+// sat_signed (fixed.py:28-34), bits <= 63.
+__device__ __forceinline__ i64 sat_bits(i64 v, int bits) {
+  const i64 hi = (1ll << (bits - 1)) - 1, lo = -hi - 1;
+  return v > hi ? hi : (v < lo ? lo : v);
+}
+
+// sat_signed(v << sl, bits) without forming an out-of-range value.
+__device__ __forceinline__ i64 sat_shl(i64 v, int sl, int bits) {
+  const i64 hi = (1ll << (bits - 1)) - 1, lo = -hi - 1;
+  if (v == 0) return 0;
+  if (sl >= bits) return v > 0 ? hi : lo;
+  if (v > (hi >> sl)) return hi;
+  if (v < (lo >> sl)) return lo;
+  return (i64)((u64)v << sl);
+}
+
+// requant (fixed.py:37-45) with shift = dst_exp - src_exp; |v| < 2^62.
+__device__ __forceinline__ i64 requant_shift(i64 v, int shift, int bits) {
+  return shift >= 0 ? sat_bits(rsa_pos(v, shift), bits) : sat_shl(v, -shift, bits);
+}
+
+// 128-bit variants for LayerNorm and exponent-aligned adds; |v| < 2^125.
+__device__ __forceinline__ i128 rsa128(i128 v, int s) {
+  if (s <= 0) return v * ((i128)1 << (-s));
+  if (s > 126) return 0;
+  i128 mag = v < 0 ? -v : v;
+  mag = (mag + ((i128)1 << (s - 1))) >> s;
+  return v < 0 ? -mag : mag;
+}
+
+__device__ __forceinline__ i64 sat128(i128 v, int bits) {
+  const i128 hi = ((i128)1 << (bits - 1)) - 1, lo = -hi - 1;
+  return (i64)(v > hi ? hi : (v < lo ? lo : v));
+}
+
+__device__ __forceinline__ i64 requant128(i128 v, int shift, int bits) {
+  if (shift >= 0) return sat128(rsa128(v, shift), bits);
+  const i128 hi = ((i128)1 << (bits - 1)) - 1, lo = -hi - 1;
+  const int sl = -shift;
+  if (v == 0) return 0;
+  if (sl >= bits) return v > 0 ? (i64)hi : (i64)lo;
+  if (v > (hi >> sl)) return (i64)hi;
+  if (v < (lo >> sl)) return (i64)lo;
+  return (i64)(v * ((i128)1 << sl));
+}
+
+// round_div (fixed.py:57-70) for den > 0: nearest, ties away from zero.
+__device__ __forceinline__ i64 round_div_pos(i64 num, i64 den) {
+  u64 mag = num < 0 ? (u64)(-num) : (u64)num;
+  u64 q = mag / (u64)den, r = mag - q * (u64)den;
+  if (2 * r >= (u64)den) q += 1;
+  return num < 0 ? -(i64)q : (i64)q;
+}
+
+// _align_add_requant (transformer.py:96-101): both operands int8.  The
+// aligned sum needs more than 64 bits only when the exponents differ by
+// more than 54; that case takes the 128-bit route.
+__device__ __forceinline__ int align_add_i8(int a, int a_exp, int b, int b_exp, int out_exp) {
+  const int c = a_exp < b_exp ? a_exp : b_exp;
+  const int da = a_exp - c, db = b_exp - c;
+  if (da <= 54 && db <= 54) {
+    i64 s = (i64)((u64)(i64)a << da) + (i64)((u64)(i64)b << db);
+    return (int)requant_shift(s, out_exp - c, 8);
+  }
+  i128 s = (i128)a * ((i128)1 << da) + (i128)b * ((i128)1 << db);
+  return (int)requant128(s, out_exp - c, 8);
+}
+
+// ---------------------------------------------------------------- nonlinear.py
+
+// floor(num / den) for num < 2^40 and 2^16 <= den < 2^24 with a quotient
+// below 2^17: single-precision reciprocal estimate (error well below one
+// unit) and one exact integer correction step.
+__device__ __forceinline__ unsigned udiv_q17(u64 num, unsigned den) {
+  float est = (float)num * __builtin_amdgcn_rcpf((float)den);
+  unsigned q = (unsigned)est;
+  i64 r = (i64)num - (i64)q * (i64)den;
+  if (r < 0) q -= 1;
+  else if (r >= (i64)den) q += 1;
+  return q;
+}
+
+// gelu (nonlinear.py:60-80), ShiftGELU on Q8.16.  Domain: the 24-bit signed
+// range, which every call site guarantees (requant(..., -16, 24) first).
+__device__ __forceinline__ int gelu_q16(int x) {
+  const int ip = x + (x >> 1) + (x >> 3) + (x >> 4);
+  const int ip2 = ip + (ip >> 1) - (ip >> 4);
+  const int a = ip2 < 0 ? -ip2 : ip2;
+  const int q = a >> 16, r = a & 0xFFFF;
+  const int frac = (r * 11 + 15) >> 4;
+  int e;
+  if (ip2 < 0) {
+    e = q <= 16 ? ((65536 - frac) >> q) : 0;
+  } else {
+    const int cap = (1 << 23) - 1;
+    if (q <= 7) {
+      e = (65536 + frac) << q;
+      e = e > cap ? cap : e;
+    } else {
+      e = cap;
+    }
+  }
+  const unsigned den = 65536u + (unsigned)e;
+  const u64 num = ((u64)(unsigned)e << 16) + (den >> 1);
+  const unsigned sig = udiv_q17(num, den);
+  return (int)sat_bits(rsa_pos((i64)x * (i64)sig, 16), 24);
+}
+
+// requant(gelu(requant(v, src, -16, 24)), -16, dst, 8): the GEMM+GELU
+// post-op of ffn (transformer.py:349-358) and selector._gemm_gelu
+// (selector.py:89-99).  shift_in = -16 - src_exp, shift_out = dst_exp + 16.
+__device__ __forceinline__ int gelu_post(i64 v, int shift_in, int shift_out) {
+  const int q = (int)requant_shift(v, shift_in, 24);
+  return (int)requant_shift(gelu_q16(q), shift_out, 8);
+}
+
+// plan_sigmoid (nonlinear.py:83-95).
+__device__ __forceinline__ int plan_sigmoid(int x) {
+  const int ax = x < 0 ? -x : x;
+  int y;
+  if (ax >= 327680) y = 65536;
+  else if (ax >= 155648) y = (ax >> 5) + 55296;
+  else if (ax >= 65536) y = (ax >> 3) + 40960;
+  else y = (ax >> 2) + 32768;
+  return x < 0 ? 65536 - y : y;
+}
+
+// _softmax_exp (nonlinear.py:98-106) for x_tilde in [-(2^31 - 1), 0].
+__device__ __forceinline__ unsigned softmax_exp(int xt) {
+  const unsigned nx = (unsigned)(-xt);
+  const unsigned z = nx / 45426u;
+  const int p = xt + (int)(z * 45426u);
+  const unsigned s = (unsigned)(p + 88670);          // (43244, 88670]
+  const unsigned square = (unsigned)(((u64)s * s + 32768u) >> 16);   // <= 119971
+  const unsigned e = (unsigned)(((u64)23495u * square + 32768u) >> 16) + 22544u;
+  return z >= 32 ? 0u : (e >> z);
+}
+
+// round_div(2^32, sum) for sum > 0 (nonlinear.py:119).
+__device__ __forceinline__ u64 softmax_recip(u64 sum) {
+  const u64 num = 1ull << 32;
+  u64 q = num / sum, r = num - q * sum;
+  if (2 * r >= sum) q += 1;
+  return q;
+}
+
+// ratio = rsa(e * recip, 16); with delta2 = 65536 the scaled value equals
+// the ratio (nonlinear.py:120-121).
+__device__ __forceinline__ unsigned softmax_ratio(unsigned e, u64 recip) {
+  return (unsigned)(((u64)e * recip + 32768u) >> 16);
+}
+
+// softmax_attention narrowing (nonlinear.py:133): min(rsa(scaled, 8), 255).
+__device__ __forceinline__ unsigned prob_u8(unsigned ratio) {
+  const unsigned p = (ratio + 128u) >> 8;
+  return p > 255u ? 255u : p;
+}
+
+// floor square root over u64 (fixed.isqrt, fixed.py:73-80): double estimate
+// and exact integer correction.
+__device__ __forceinline__ u64 isqrt_u64(u64 x) {
+  u64 r = (u64)__builtin_sqrt((double)x);
+  while (r > 0 && r * r > x) --r;
+  while ((r + 1) * (r + 1) <= x) ++r;
+  return r;
+}
+
+__device__ __forceinline__ int sat_q016(i64 v) { return v < 0 ? 0 : (v > 65536 ? 65536 : (int)v); }
+
+}  // namespace hv

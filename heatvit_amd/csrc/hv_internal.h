@@ -1,0 +1,89 @@
+// hv_internal.h -- launchers shared between the kernel files and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/heatvit_hip.h"
+
+namespace hv {
+
+// Error reporting (thread-local message, see hv_capi.hip).
+int fail(int status, const char *fmt, ...);
+int check_hip(hipError_t e, const char *what);
+
+// A-operand sources of the GEMM.
+enum { A_ROWS = HV_A_ROWS, A_GATHER = HV_A_GATHER, A_PATCH = 2 };
+
+struct GemmArgs {
+  const int8_t *a;
+  const int32_t *a_rows;
+  const int8_t *b;  // mfma32-packed weights
+  const int32_t *bias;
+  void *c;
+  const int8_t *res;
+  int8_t *aux;
+  const int32_t *m_dev;
+  const int8_t *pos;  // patch mode: [197][192] position table
+  int m, n, k, lda, ldc, ldr;
+  int shift_a;  // epilogue shifts, see k_gemm
+  int shift_b;
+  int res_exp, mid_exp, out_exp;
+};
+
+int launch_gemm(const GemmArgs &g, int a_mode, int epilogue, hipStream_t s);
+
+// Patch embedding (transformer.patch_embedding): A rows are gathered
+// patches of NHWC 224x224x3 images, epilogue adds the position rows, and the
+// CLS rows are written by a second small kernel.
+int launch_patch_embed(const hv_patch_dev &p, const int8_t *images, int batch, int8_t *x,
+                       hipStream_t s);
+
+int launch_layernorm(const int8_t *x, const int8_t *g, const int8_t *b, int8_t *y, int rows,
+                     const int32_t *rows_dev, int x_exp, int g_exp, int b_exp, int out_exp,
+                     uint8_t *neg_var, hipStream_t s);
+
+struct AttnArgs {
+  const int8_t *qkv;  // [T][576]
+  const int32_t *offsets;
+  int8_t *ctx;        // [T][192]
+  int32_t *score;     // optional [B][3][197][197]
+  uint8_t *prob;      // optional
+  int batch;
+  int score_shift;    // score_exp - 2*qkv_out_exp (requant to int32)
+  int q16_shift;      // -(score_exp + 13)
+  int ctx_shift;      // context_out_exp - (prob_exp + qkv_out_exp)
+};
+int launch_attention(const AttnArgs &a, hipStream_t s);
+
+int launch_softmax_rows(const int32_t *x, const int32_t *offsets, int rows, uint8_t *att,
+                        int32_t *sel, hipStream_t s);
+int launch_primitive(int op, const int64_t *in, int64_t *out, int64_t n, int a, int b, int c,
+                     hipStream_t s);
+
+struct SelectorArgs {
+  const hv_selector_dev *p;  // host copy passed by value; NULL: fused is an input
+  const int8_t *tokens;
+  const int32_t *offsets;
+  const uint8_t *pkg_in;
+  int batch;
+  int8_t *out_tokens;
+  int32_t *out_offsets;
+  uint8_t *pkg_out;
+  int32_t *fused;       // [B][196]
+  int32_t *kept_index;  // [B][196]
+  int32_t *state;       // [B][5]
+  int32_t *token_counts;  // optional [B][4] column `stage`
+  int stage;
+  hv_selector_ckpt ck;    // optional intermediate outputs (null pointers skip)
+};
+int launch_selector(const SelectorArgs &a, hipStream_t s);
+
+// Small utility kernels.
+int launch_init_offsets(int32_t *offsets, uint8_t *pkg, int32_t *token_counts, int batch,
+                        int rows_per_image, hipStream_t s);
+int launch_copy_ckpt(const int8_t *x, const int32_t *offsets, int batch, int8_t *ckpt,
+                     int32_t *ckpt_rows, int slot, hipStream_t s);
+int launch_cls_rows(const int32_t *offsets, int batch, int32_t *rows_out, hipStream_t s);
+
+}  // namespace hv

@@ -1,0 +1,143 @@
+"""Full HeatViT-T inference on the GPU.
+
+HeatViTModel.infer keeps the golden model's signature and result
+(model.py:49-123): logits (1000 int32 at LOGIT_SCALE_EXP = -14), the
+18 checkpoints (patch, selector_NN, block_NN, final_ln, logits) and the
+selector summary.  HeatViTModel.infer_batch and Engine run many images per
+launch sequence; pruned images keep ragged token counts on the device.
+"""
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _lib
+from .device import DeviceModel
+from .params import HeatViTParams
+
+LOGIT_SCALE_EXP = -14
+IMAGE_BYTES = 224 * 224 * 3
+CKPT_NAMES = (["patch"] + [f"selector_{i:02d}" for i in range(1, 4)] +
+              [f"block_{i:02d}" for i in range(1, 13)] + ["final_ln"])
+
+
+@dataclass(frozen=True)
+class ModelResult:
+    logits: tuple
+    output_scale_exp: int
+    checkpoints: dict
+    selector_summary: tuple
+
+
+@dataclass(frozen=True)
+class BatchResult:
+    logits: np.ndarray         # [B][1000] int32 at output_scale_exp
+    output_scale_exp: int
+    token_counts: np.ndarray   # [B][4]: rows entering block 1 and after each selector
+    selector_state: np.ndarray  # [n_selectors][B][5]: count, package, kept, pruned, warnings
+    checkpoints: list = None   # per image dict when requested
+
+
+class Engine:
+    """Device-resident model plus a reusable workspace for batches of up to
+    `max_batch` images.  `forward(images)` takes a device int8 tensor
+    [B][150528] and enqueues the whole forward on the current stream."""
+
+    def __init__(self, params, max_batch, device="cuda"):
+        self.model = params if isinstance(params, DeviceModel) else DeviceModel(params, device)
+        self.max_batch = int(max_batch)
+        L = _lib.lib()
+        dev = self.model.device
+        self.workspace = torch.empty(L.hv_model_workspace_bytes(self.max_batch),
+                                     dtype=torch.uint8, device=dev)
+        self.logits = torch.empty((self.max_batch, 1000), dtype=torch.int32, device=dev)
+        self.token_counts = torch.empty((self.max_batch, 4), dtype=torch.int32, device=dev)
+        self.state = torch.zeros((3, self.max_batch, 5), dtype=torch.int32, device=dev)
+
+    def forward(self, images, ckpt=None, ckpt_rows=None):
+        b = images.shape[0]
+        if b > self.max_batch:
+            raise ValueError(f"batch {b} exceeds the engine's {self.max_batch}")
+        if images.dtype != torch.int8 or not images.is_contiguous() or \
+                images.numel() != b * IMAGE_BYTES:
+            raise ValueError("images must be a contiguous int8 device tensor [B][150528]")
+        state = self.state[:, :b] if b == self.max_batch else \
+            torch.zeros((3, b, 5), dtype=torch.int32, device=images.device)
+        _lib.check(_lib.lib().hv_model_forward(
+            self.model.struct, images.data_ptr(), b, self.logits.data_ptr(),
+            self.token_counts.data_ptr(), state.data_ptr(),
+            None if ckpt is None else ckpt.data_ptr(),
+            None if ckpt_rows is None else ckpt_rows.data_ptr(),
+            self.workspace.data_ptr(), self.workspace.numel(),
+            torch.cuda.current_stream(images.device).cuda_stream), "model forward")
+        return self.logits[:b], self.token_counts[:b], state
+
+
+def _images(images):
+    a = np.asarray(images.cpu().numpy() if isinstance(images, torch.Tensor) else images)
+    if a.dtype.kind == "f":
+        raise TypeError("images must hold integers")
+    a = a.reshape(-1, IMAGE_BYTES)
+    if a.size and (a.min() < -128 or a.max() > 127):
+        raise ValueError("image outside int8")
+    return np.ascontiguousarray(a, np.int8)
+
+
+class HeatViTModel:
+    """Integer HeatViT-T inference (model.py:70) on one MI355X."""
+
+    def __init__(self):
+        self._cache = None
+
+    def _engine(self, params, batch):
+        if not isinstance(params, HeatViTParams):
+            raise TypeError("params must be HeatViTParams")
+        if (self._cache is None or self._cache[0] is not params or
+                self._cache[1].max_batch < batch):
+            self._cache = (params, Engine(params, batch))
+        return self._cache[1]
+
+    def infer_batch(self, images, params, checkpoints=False):
+        imgs = _images(images)
+        b = len(imgs)
+        eng = self._engine(params, b)
+        dev = torch.from_numpy(imgs).cuda()
+        ck = ck_rows = None
+        if checkpoints:
+            ck = torch.zeros((b, 17, 197, 192), dtype=torch.int8, device="cuda")
+            ck_rows = torch.zeros((b, 17), dtype=torch.int32, device="cuda")
+        logits, counts, state = eng.forward(dev, ck, ck_rows)
+        n_sel = len(params.selectors)
+        state = state.cpu().numpy()[:n_sel]
+        if (state[:, :, 0] < 0).any():
+            raise ValueError("selector input invalid for some image (too few tokens)")
+        cks = None
+        if checkpoints:
+            ck, ck_rows = ck.cpu().numpy(), ck_rows.cpu().numpy()
+            lg = logits.cpu().numpy()
+            cks = []
+            for i in range(b):
+                d = {name: ck[i, s, :ck_rows[i, s]].copy()
+                     for s, name in enumerate(CKPT_NAMES) if ck_rows[i, s]}
+                d["logits"] = lg[i].copy()
+                cks.append(d)
+        return BatchResult(logits=logits.cpu().numpy().copy(), output_scale_exp=LOGIT_SCALE_EXP,
+                           token_counts=counts.cpu().numpy().copy(), selector_state=state.copy(),
+                           checkpoints=cks)
+
+    def infer(self, image, params):
+        """HeatViTModel.infer (model.py:73): one image, all checkpoints."""
+        res = self.infer_batch(_images(image)[:1], params, checkpoints=True)
+        summary = []
+        counts = res.token_counts[0]
+        prev = 197
+        for s in range(len(params.selectors)):
+            st = res.selector_state[s, 0]
+            summary.append({"input_tokens": int(prev), "output_tokens": int(st[0]),
+                            "kept_normal": int(st[2]), "pruned_normal": int(st[3]),
+                            "package_present": int(st[1])})
+            prev = int(counts[s + 1])
+        return ModelResult(logits=tuple(int(v) for v in res.logits[0]),
+                           output_scale_exp=LOGIT_SCALE_EXP, checkpoints=res.checkpoints[0],
+                           selector_summary=tuple(summary))

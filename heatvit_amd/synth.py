@@ -28,6 +28,12 @@ Distributions (integer only, no floating point):
                    inputs equal the producing tensor's output exponent,
                    selector concat_out = local_out and stats_out = in
                    (the selector relabels these without rescaling).
+  selectors        the calibration (tests/golden/calibrate.py, stored in
+                   data/calibration.json) picks, per selector, one of 16
+                   independent uniform exponent draws -- the one whose fused
+                   keep scores are most diverse on the calibration inputs,
+                   since saturated draws leave every candidate on one score
+                   level -- and then the keep-logit biases.
 """
 
 import json
@@ -179,14 +185,16 @@ def make_block(seed, index, x_exp):
     return BlockParams(mhsa=mhsa, ffn=ffn)
 
 
-def make_selector(seed, index, in_exp, keep_bias=0):
-    """Selector `index` with every head's keep-logit bias b3[h][1] set to
-    `keep_bias` (b3[h][0] keeps its drawn value)."""
+def make_selector(seed, index, in_exp, keep_bias=0, exp_draw=0):
+    """Selector `index` with the keep-logit biases b3[h][1] set to `keep_bias`
+    (one int for every head, or three per-head ints); b3[h][0] keeps its
+    drawn value.  `exp_draw` selects one of several independent uniform
+    draws of the selector's scale exponents (draw 0 is the default)."""
     p = f"selector{index}"
-    e = _Exps(seed, p)
+    e = _Exps(seed, p if exp_draw == 0 else f"{p}.draw{exp_draw}")
     local_out = e("local_out")
     b3 = normal_i32(seed, f"{p}.score.b3", (3, 2)).copy()
-    b3[:, 1] = keep_bias
+    b3[:, 1] = np.broadcast_to(np.asarray(keep_bias, np.int64), (3,))
     return SelectorParams(
         local=SelectorLocalParams(w=normal_i8(seed, f"{p}.local.w", (3, 64, 32)),
                                   b=normal_i32(seed, f"{p}.local.b", (3, 32))),
@@ -212,14 +220,16 @@ def make_selector(seed, index, in_exp, keep_bias=0):
     )
 
 
-def make_model(seed, selector_blocks=(4, 7, 10), keep_biases=(0, 0, 0)):
+def make_model(seed, selector_blocks=(4, 7, 10), keep_biases=(0, 0, 0), exp_draws=(0, 0, 0)):
+    """Full model; keep_biases[s] is selector s's keep bias (int or 3 ints)
+    and exp_draws[s] its exponent draw."""
     patch = make_patch(seed)
     blocks, selectors = [], []
     x_exp = patch.tokens_scale_exp
     for b in range(1, 13):
         if b in selector_blocks:
             s = len(selectors)
-            selectors.append(make_selector(seed, s + 1, x_exp, keep_biases[s]))
+            selectors.append(make_selector(seed, s + 1, x_exp, keep_biases[s], exp_draws[s]))
         blk = make_block(seed, b, x_exp)
         blocks.append(blk)
         x_exp = blk.ffn.out_scale_exp
@@ -265,20 +275,22 @@ def full_workload():
     return images(seed, 1), make_model(seed, selector_blocks=())
 
 
-def selector_workload(keep_bias=None):
+def selector_workload(keep_bias=None, exp_draw=None):
     seed = WORKLOAD_SEED["selector"]
-    if keep_bias is None:
-        keep_bias = load_calibration().get("selector", {}).get("keep_bias", 0)
+    cal = load_calibration().get("selector", {})
+    keep_bias = cal.get("keep_bias", 0) if keep_bias is None else keep_bias
+    exp_draw = cal.get("exp_draw", 0) if exp_draw is None else exp_draw
     in_exp = _Exps(seed, "input")("tokens")
     return token_batch(seed, WORKLOAD_BATCH["selector"]), make_selector(seed, 1, in_exp,
-                                                                        keep_bias)
+                                                                        keep_bias, exp_draw)
 
 
-def pruned_params(keep_biases=None):
+def pruned_params(keep_biases=None, exp_draws=None):
     seed = WORKLOAD_SEED["pruned"]
-    if keep_biases is None:
-        keep_biases = load_calibration().get("pruned", {}).get("keep_biases", (0, 0, 0))
-    return make_model(seed, (4, 7, 10), tuple(keep_biases))
+    cal = load_calibration().get("pruned", {})
+    keep_biases = cal.get("keep_biases", (0, 0, 0)) if keep_biases is None else keep_biases
+    exp_draws = cal.get("exp_draws", (0, 0, 0)) if exp_draws is None else exp_draws
+    return make_model(seed, (4, 7, 10), tuple(keep_biases), tuple(exp_draws))
 
 
 def unpruned_control(params):

@@ -1,0 +1,239 @@
+/*
+ * heatvit_hip.h -- C ABI of libheatvit_hip.so, the gfx950 (MI355X) HIP
+ * implementation of HeatViT-T's integer inference path.
+ *
+ * The reference (YOUXINYANG/HeatViT) has no FFI: its golden model is plain
+ * Python that callers import (verification/heatvit_ref).  Each entry point
+ * below replaces one golden-model function; the Python package heatvit_amd
+ * binds them with ctypes and keeps the reference's Python signatures.
+ *
+ * Conventions
+ *  - All tensor pointers are device pointers (hipMalloc'd or torch-owned);
+ *    the library never allocates or frees caller memory.  Scratch space is
+ *    passed in as `workspace` (size from the matching *_workspace_bytes).
+ *  - All work is enqueued on the caller's stream; nothing synchronises the
+ *    device.  Ragged row counts stay on the device (offset arrays).
+ *  - Weights are passed in the packed layouts documented per struct; the
+ *    host package produces them (heatvit_amd/device.py).
+ *  - Return value: HV_OK or a negative status; hv_last_error() describes it.
+ *    Status classes mirror the golden model's exceptions: HV_EVALUE is
+ *    ValueError, HV_EOVERFLOW is OverflowError.
+ *
+ * Packed GEMM weight layout ("mfma32"): a logical int8 matrix W[K][N]
+ * (row-major, the reference's layout) with K % 32 == 0 is padded to
+ * N32 = ceil(N/32)*32 columns and stored as [N32/32][K/32][64][16] bytes:
+ * element (k, n) lives at tile (n/32, k/32), lane (n%32) + 32*((k%32)/16),
+ * byte k%16.  Each 1 KiB tile is the B operand of one 32x32x32 int8 MFMA.
+ */
+#ifndef HEATVIT_HIP_H
+#define HEATVIT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HV_OK 0
+#define HV_EVALUE (-2)    /* invalid shape / range / exponent (ValueError) */
+#define HV_EOVERFLOW (-3) /* accumulator outside int32 (OverflowError)    */
+#define HV_EHIP (-4)      /* HIP runtime error                           */
+
+#define HV_MAX_TOKENS 197 /* rows per image; attention tiles assume <= 208 */
+
+/* hipStream_t without pulling in the HIP headers. */
+typedef void *hv_stream_t;
+
+/* Last error message of the calling thread ("" when none). */
+const char *hv_last_error(void);
+/* ABI version, bumped on any incompatible change. */
+int hv_abi_version(void);
+
+/* ------------------------------------------------------------------ */
+/* Primitive evaluators (device implementations of fixed.py and         */
+/* nonlinear.py, exposed so they can be checked element by element).    */
+/* ------------------------------------------------------------------ */
+
+#define HV_PRIM_REQUANT 0 /* out = requant(in, a, b, c)          fixed.py:37  */
+#define HV_PRIM_GELU 1    /* out = gelu(in)                      nonlinear.py:60 */
+#define HV_PRIM_PLAN 2    /* out = plan_sigmoid(in)              nonlinear.py:83 */
+#define HV_PRIM_RSA 3     /* out = round_shift_away(in, a)       fixed.py:15  */
+
+/* Element-wise: out[i] = op(in[i]; a, b, c) over n int64 values. */
+int hv_eval_primitive(int op, const int64_t *in, int64_t *out, int64_t n, int a, int b,
+                      int c, hv_stream_t stream);
+
+/* Softmax over ragged rows (nonlinear.py:109-133): row r is
+ * x[offsets[r] .. offsets[r+1]); writes the attention UQ0.8 bytes and the
+ * selector Q0.16 values.  Row length <= 256. */
+int hv_softmax_rows(const int32_t *x, const int32_t *offsets, int rows, uint8_t *attention,
+                    int32_t *selector, hv_stream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* LayerNorm (nonlinear.layernorm, nonlinear.py:136-186)                */
+/* ------------------------------------------------------------------ */
+
+/* y[r] = layernorm(x[r]) for r < rows (rows_dev, when non-NULL, holds the
+ * live row count on the device and `rows` is the capacity).  neg_var, when
+ * non-NULL, receives one byte per row (negative-variance flag). */
+int hv_layernorm_i8(const int8_t *x, const int8_t *gamma, const int8_t *beta, int8_t *y,
+                    int rows, const int32_t *rows_dev, int x_exp, int gamma_exp,
+                    int beta_exp, int out_exp, uint8_t *neg_var, hv_stream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* int8 GEMM with fused epilogues (gemm.gemm_numpy + gemm_writeback,    */
+/* gemm.py:93-139; transformer.py:349-358 GELU; transformer.py:96-101   */
+/* residual align-add)                                                  */
+/* ------------------------------------------------------------------ */
+
+#define HV_EPI_I8 0       /* c = requant(acc + bias, src, dst, 8)                    */
+#define HV_EPI_I32 1      /* c = requant(acc + bias, src, dst, 32) (int32 output)    */
+#define HV_EPI_GELU 2     /* c = requant(gelu(requant(acc+bias, src, -16, 24)), -16, dst, 8) */
+#define HV_EPI_RESIDUAL 3 /* t = requant(acc+bias, src, mid, 8); c = align_add(res@res_exp, t@mid -> dst) */
+
+#define HV_A_ROWS 0   /* A row r at a + r*lda                                         */
+#define HV_A_GATHER 1 /* A row r at a + a_rows[r]*lda                                 */
+
+typedef struct {
+  const int8_t *a;         /* [M][lda] int8                                  */
+  const int32_t *a_rows;   /* HV_A_GATHER row indices [M]                     */
+  const int8_t *b_packed;  /* "mfma32" packed weights for W[K][N]             */
+  const int32_t *bias;     /* [N] or NULL                                    */
+  void *c;                 /* [M][ldc] int8, or int32 for HV_EPI_I32          */
+  const int8_t *residual;  /* [M][ldr] for HV_EPI_RESIDUAL                    */
+  int8_t *aux;             /* optional [M][ldc]: t of HV_EPI_RESIDUAL        */
+  const int32_t *m_dev;    /* optional device-side live M (<= m)             */
+  int32_t m, n, k, lda, ldc, ldr;
+  int32_t a_mode, epilogue;
+  int32_t src_exp, dst_exp, mid_exp, res_exp;
+} hv_gemm_desc;
+
+int hv_gemm_i8(const hv_gemm_desc *d, hv_stream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* Parameter views (device pointers) for the fused stages                */
+/* ------------------------------------------------------------------ */
+
+/* PatchParams (transformer.py:51-93); weight packed mfma32 from [768][192]. */
+typedef struct {
+  const int8_t *weight_p;
+  const int32_t *bias;
+  const int8_t *cls, *pos; /* [192], [197][192] */
+  int32_t image_exp, weight_exp, activation_exp, tokens_exp, cls_exp, pos_exp;
+} hv_patch_dev;
+
+/* BlockParams = MhsaParams + FfnParams (transformer.py:148-198, 287-325);
+ * wqkv_p/wproj_p/w1_p/w2_p packed mfma32 from the [K][N] matrices. */
+typedef struct {
+  const int8_t *ln1_gamma, *ln1_beta, *wqkv_p, *wproj_p;
+  const int8_t *ln2_gamma, *ln2_beta, *w1_p, *w2_p;
+  const int32_t *bqkv, *bproj, *b1, *b2;
+  int32_t x_exp, gamma1_exp, beta1_exp, ln1_out_exp, wqkv_exp, qkv_out_exp, score_exp,
+      prob_exp, context_out_exp, wproj_exp, msa_out_exp;
+  int32_t ffn_x_exp, gamma2_exp, beta2_exp, ln2_out_exp, w1_exp, hidden_out_exp, w2_exp,
+      ffn_out_exp, out_exp;
+} hv_block_dev;
+
+/* SelectorParams (selector.py:111-222).  Weight matrices are stored
+ * output-major ("transposed"): local_wt [3][32][64], w1t [3][32][64],
+ * w2t [3][16][32], w3t [3][2][16], hw_w1t [3][3], hw_w2t [3][3], i.e.
+ * wt[h][j][k] = w[h][k][j]. */
+typedef struct {
+  const int8_t *local_wt, *w1t, *w2t, *w3t, *hw_w1t, *hw_w2t;
+  const int32_t *local_b, *b1, *b2, *b3, *hw_b1, *hw_b2;
+  int32_t in_exp, local_w_exp, local_out_exp, concat_out_exp, score_w1_exp, score_w2_exp,
+      score_w3_exp, h1_out_exp, h2_out_exp, logits_out_exp, stats_out_exp, hw_w1_exp,
+      hw_hidden_out_exp, hw_w2_exp;
+} hv_selector_dev;
+
+/* HeatViTParams (model.py:24-47); head_w packed mfma32 from [192][1000]. */
+typedef struct {
+  hv_patch_dev patch;
+  hv_block_dev blocks[12];
+  hv_selector_dev selectors[3];
+  int32_t n_selectors;
+  int32_t selector_blocks[3];
+  const int8_t *final_gamma, *final_beta, *head_w_p;
+  const int32_t *head_b;
+  int32_t final_gamma_exp, final_beta_exp, final_ln_out_exp, head_w_exp;
+} hv_model_dev;
+
+/* ------------------------------------------------------------------ */
+/* transformer.transformer_block (transformer.py:401-431) over a ragged  */
+/* batch: image b owns rows offsets[b] .. offsets[b+1] of x.             */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+  int8_t *ln1, *fused_qkv, *concat, *msa, *y, *ln2, *hidden, *ffn_out; /* [T][..] */
+  int32_t *score; /* [B][3][197][197] (row/col stride 197) */
+  uint8_t *prob;  /* [B][3][197][197] */
+} hv_block_ckpt;
+
+size_t hv_block_workspace_bytes(int batch, int max_rows);
+int hv_block_forward(const hv_block_dev *p, const int8_t *x, const int32_t *offsets, int batch,
+                     int max_rows, int8_t *z, const hv_block_ckpt *ck, void *workspace,
+                     size_t workspace_bytes, hv_stream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* selector.token_selector (selector.py:503-563) over a ragged batch.    */
+/* Image b: rows offsets[b]..offsets[b+1] of tokens, package flag        */
+/* pkg_in[b].  Outputs: out_tokens (compacted), out_offsets [B+1],       */
+/* pkg_out [B], fused [B][196] (Q0.16 per candidate), kept_index         */
+/* [B][196] (candidate index of each kept normal, -1 padded),            */
+/* state [B][5] = {token_count, package_present, kept, pruned, warnings}. */
+/* ------------------------------------------------------------------ */
+
+/* Optional selector checkpoints (SelectorResult fields, selector.py:235-250);
+ * candidate axes are padded to 196. */
+typedef struct {
+  int8_t *local;         /* [B][3][196][32] */
+  int8_t *global;        /* [B][3][32]      */
+  int32_t *head_scores;  /* [B][3][196]     */
+  int8_t *head_stats;    /* [B][196][3]     */
+  int32_t *head_weights; /* [B][196][3]     */
+} hv_selector_ckpt;
+
+size_t hv_selector_workspace_bytes(int batch);
+int hv_selector_forward(const hv_selector_dev *p, const int8_t *tokens, const int32_t *offsets,
+                        const uint8_t *pkg_in, int batch, int8_t *out_tokens,
+                        int32_t *out_offsets, uint8_t *pkg_out, int32_t *fused,
+                        int32_t *kept_index, int32_t *state, const hv_selector_ckpt *ck,
+                        void *workspace, size_t workspace_bytes, hv_stream_t stream);
+
+/* selector.finalize_tokens (selector.py:421-500) from given fused scores
+ * fused [B][196] (Q0.16, candidate c of image b at b*196 + c; the last
+ * candidate is the incoming package when pkg_in[b]); outputs as in
+ * hv_selector_forward. */
+int hv_selector_finalize(const int8_t *tokens, const int32_t *offsets, const uint8_t *pkg_in,
+                         const int32_t *fused, int batch, int8_t *out_tokens,
+                         int32_t *out_offsets, uint8_t *pkg_out, int32_t *kept_index,
+                         int32_t *state, hv_stream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* transformer.patch_embedding (transformer.py:104-145) over a batch of  */
+/* NHWC 224x224x3 int8 images: x [B][197][192] int8 at tokens_exp.       */
+/* ------------------------------------------------------------------ */
+
+int hv_patch_embedding(const hv_patch_dev *p, const int8_t *images, int batch, int8_t *x,
+                       hv_stream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* model.HeatViTModel.infer (model.py:73-123) over a batch of images.    */
+/* images [B][224*224*3] NHWC int8; logits [B][1000] int32 at exp -14;   */
+/* token_counts [B][4]: rows entering block 1, and after each selector;  */
+/* state [3][B][5] per-selector state as in hv_selector_forward.         */
+/* ckpt (optional): [B][17][197][192] int8 in the slot order patch,      */
+/* selector_01..03, block_01..12, final_ln, rows per slot in ckpt_rows   */
+/* [B][17].                                                              */
+/* ------------------------------------------------------------------ */
+
+size_t hv_model_workspace_bytes(int batch);
+int hv_model_forward(const hv_model_dev *p, const int8_t *images, int batch, int32_t *logits,
+                     int32_t *token_counts, int32_t *state, int8_t *ckpt, int32_t *ckpt_rows,
+                     void *workspace, size_t workspace_bytes, hv_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
