@@ -44,7 +44,7 @@ class _Holder:
         self.tensors = []
 
     def put(self, arr, dtype):
-        t = torch.from_numpy(np.ascontiguousarray(arr, dtype=dtype)).to(self.device)
+        t = torch.from_numpy(np.array(arr, dtype=dtype, copy=True, order="C")).to(self.device)
         self.tensors.append(t)
         return t.data_ptr()
 

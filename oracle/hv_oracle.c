@@ -69,6 +69,11 @@ static int64_t requant128(i128 v, int src_exp, int dst_exp, int bits) {
   return sat_shl(v, -shift, bits);
 }
 
+void hvo_requant_array(const int64_t *v, int64_t *out, int64_t n, int src_exp, int dst_exp,
+                       int bits) {
+  for (int64_t i = 0; i < n; i++) out[i] = requant128(v[i], src_exp, dst_exp, bits);
+}
+
 int64_t hvo_round_shift_away(int64_t value, int shift) {
   return (int64_t)rsa128(value, shift);
 }
@@ -151,6 +156,10 @@ int32_t hvo_gelu(int32_t x32) {
   int64_t den = 65536 + e;
   int64_t sig = ((e << 16) + (den >> 1)) / den;
   return (int32_t)sat128(rsa128((i128)x * sig, 16), 24);
+}
+
+void hvo_gelu_array(const int32_t *x, int32_t *out, int64_t n) {
+  for (int64_t i = 0; i < n; i++) out[i] = hvo_gelu(x[i]);
 }
 
 /* nonlinear.plan_sigmoid (nonlinear.py:83-95). */

@@ -37,11 +37,14 @@ extern "C" {
 int64_t hvo_round_shift_away(int64_t value, int shift);
 int64_t hvo_sat_signed(int64_t value, int bits);
 int64_t hvo_requant(int64_t value, int src_exp, int dst_exp, int bits);
+void hvo_requant_array(const int64_t *v, int64_t *out, int64_t n, int src_exp, int dst_exp,
+                       int bits);
 int hvo_round_div(int64_t num, int64_t den, int64_t *out);
 int hvo_udiv(uint64_t num, uint64_t den, uint64_t *quot, uint64_t *rem);
 uint64_t hvo_isqrt(uint64_t radicand, uint64_t *rem);
 int32_t hvo_gelu(int32_t x);
 int32_t hvo_plan_sigmoid(int32_t x);
+void hvo_gelu_array(const int32_t *x, int32_t *out, int64_t n);
 int hvo_softmax_scaled(const int32_t *x, int n, int32_t delta2, int32_t *out);
 int hvo_softmax_attention(const int32_t *x, int n, uint8_t *out);
 int hvo_softmax_selector(const int32_t *x, int n, int32_t *out);

@@ -106,6 +106,8 @@ def lib():
         L.hvo_sat_signed.argtypes = [C.c_int64, C.c_int]
         L.hvo_requant.restype = C.c_int64
         L.hvo_requant.argtypes = [C.c_int64, C.c_int, C.c_int, C.c_int]
+        L.hvo_requant_array.restype = None
+        L.hvo_requant_array.argtypes = [_p64, _p64, C.c_int64, C.c_int, C.c_int, C.c_int]
         L.hvo_round_div.argtypes = [C.c_int64, C.c_int64, _p64]
         L.hvo_udiv.argtypes = [C.c_uint64, C.c_uint64, C.POINTER(C.c_uint64),
                                C.POINTER(C.c_uint64)]
@@ -113,6 +115,8 @@ def lib():
         L.hvo_isqrt.argtypes = [C.c_uint64, C.POINTER(C.c_uint64)]
         L.hvo_gelu.restype = C.c_int32
         L.hvo_gelu.argtypes = [C.c_int32]
+        L.hvo_gelu_array.restype = None
+        L.hvo_gelu_array.argtypes = [_p32, _p32, C.c_int64]
         L.hvo_plan_sigmoid.restype = C.c_int32
         L.hvo_plan_sigmoid.argtypes = [C.c_int32]
         L.hvo_softmax_attention.argtypes = [_p32, C.c_int, _pu8]
@@ -171,6 +175,13 @@ def requant(v, src, dst, bits):
     return lib().hvo_requant(int(v), int(src), int(dst), int(bits))
 
 
+def requant_array(values, src, dst, bits):
+    v = np.ascontiguousarray(values, np.int64)
+    out = np.empty_like(v)
+    lib().hvo_requant_array(_ptr(v, _p64), _ptr(out, _p64), v.size, src, dst, bits)
+    return out
+
+
 def round_div(n, d):
     out = C.c_int64()
     _check(lib().hvo_round_div(int(n), int(d), C.byref(out)), "round_div")
@@ -191,6 +202,13 @@ def isqrt(x):
 
 def gelu(x):
     return lib().hvo_gelu(int(x))
+
+
+def gelu_array(xs):
+    x = np.ascontiguousarray(xs, np.int32)
+    out = np.empty_like(x)
+    lib().hvo_gelu_array(_ptr(x, _p32), _ptr(out, _p32), x.size)
+    return out
 
 
 def plan_sigmoid(x):

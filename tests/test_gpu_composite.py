@@ -1,0 +1,164 @@
+"""GPU parity of the composite stages: the HIP transformer block, token
+selector, patch embedding and full model against the reference golden
+model's fixtures (tests/golden) and the CPU oracle, bit-exact."""
+
+import numpy as np
+import pytest
+
+import golden_io as gio
+from heatvit_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _block_ck_digests(ck):
+    return {k: gio.digest(v, gio.BLOCK_DTYPES[k]) for k, v in ck.items()
+            if k in gio.BLOCK_DTYPES}
+
+
+def test_block_matches_golden():
+    from heatvit_amd.transformer import transformer_block
+    meta, arrays = gio.load("block")
+    x, bp = synth.block_workload()
+    z, ck = transformer_block(x, bp)
+    assert np.array_equal(z, arrays["z"])
+    got = _block_ck_digests(ck)
+    bad = [k for k, v in meta["checkpoints"].items() if got.get(k) != v]
+    assert not bad, bad
+
+
+def test_block_ragged_batch_vs_oracle(oracle):
+    from heatvit_amd.transformer import transformer_block_batch
+    x, bp = synth.block_workload()
+    rng = np.random.default_rng(3)
+    lens = [197, 100, 17, 1, 64, 2, 197, 45]
+    xs = [rng.integers(-128, 128, (n, 192)).astype(np.int8) for n in lens]
+    xs[0] = x
+    zs, cks = transformer_block_batch(xs, bp, checkpoints=True)
+    for i, xi in enumerate(xs):
+        z, ck = oracle.transformer_block(xi, bp)
+        assert np.array_equal(zs[i], z), i
+        for k in ("ln1", "fused_qkv", "score", "prob", "msa", "y", "ln2", "hidden", "ffn_out",
+                  "qkv", "context", "concat"):
+            assert np.array_equal(cks[i][k], ck[k]), (i, k)
+
+
+def test_selector_matches_golden():
+    from heatvit_amd.selector import token_selector_batch
+    meta, arrays = gio.load("selector")
+    tokens, sp = synth.selector_workload()
+    res = token_selector_batch(list(tokens), [False] * len(tokens), sp)
+    for i, (r, want) in enumerate(zip(res, meta["results"])):
+        assert r.token_count == want["token_count"], i
+        assert r.kept_normal_count == want["kept_normal_count"], i
+        assert r.pruned_normal_count == want["pruned_normal_count"], i
+        assert r.warnings == want["warnings"], i
+        assert int(r.package_present) == want["package_present"], i
+        assert gio.digest(r.tokens, np.int8) == want["tokens_sha256"], i
+        assert gio.digest(r.local, np.int8) == want["local_sha256"], i
+        assert gio.digest(r.global_features, np.int8) == want["global_sha256"], i
+        assert gio.digest(r.head_scores, "<i4") == want["head_scores_sha256"], i
+        assert gio.digest(r.head_stats, np.int8) == want["head_stats_sha256"], i
+        assert gio.digest(r.head_weights, "<i4") == want["head_weights_sha256"], i
+        assert np.array_equal(r.fused_scores, arrays["fused"][i]), i
+        if r.package_present:
+            assert np.array_equal(r.tokens[-1], arrays["package"][i]), i
+        assert np.array_equal(r.kept_index, np.nonzero(arrays["fused"][i] >= 32768)[0])
+
+
+def test_selector_ragged_with_packages_vs_oracle(oracle):
+    from heatvit_amd.selector import token_selector_batch
+    tokens, sp = synth.selector_workload()
+    rng = np.random.default_rng(4)
+    lens = [197, 3, 2, 90, 45, 150, 33]
+    flags = [False, True, False, True, True, False, True]
+    sets = [tokens[i][:n] if i % 2 == 0 else rng.integers(-128, 128, (n, 192)).astype(np.int8)
+            for i, n in enumerate(lens)]
+    res = token_selector_batch(sets, flags, sp)
+    for i, (t, f) in enumerate(zip(sets, flags)):
+        want = oracle.token_selector(t, f, sp)
+        r = res[i]
+        assert np.array_equal(r.tokens, want["tokens"]), i
+        assert np.array_equal(r.fused_scores, want["fused_scores"]), i
+        assert np.array_equal(r.kept_index, want["kept_index"]), i
+        assert (r.token_count, r.warnings, r.pruned_normal_count) == \
+            (want["token_count"], want["warnings"], want["pruned_normal_count"]), i
+
+
+def test_patch_embedding_vs_golden_and_oracle(oracle):
+    from heatvit_amd.transformer import patch_embedding
+    meta, _ = gio.load("full")
+    img, params = synth.full_workload()
+    x = patch_embedding(img[0], params.patch)
+    assert gio.digest(x, np.int8) == meta["checkpoints"][0]["patch"]
+    imgs, pp = synth.pruned_workload(5)
+    xb = patch_embedding(imgs, pp.patch, batch=True)
+    for i in range(5):
+        assert np.array_equal(xb[i], oracle.patch_embedding(imgs[i], pp.patch))
+
+
+def _check_model_golden(which, images, params, count):
+    from heatvit_amd.model import HeatViTModel
+    meta, arrays = gio.load(which)
+    m = HeatViTModel()
+    res = m.infer_batch(images[:count], params, checkpoints=True)
+    for i in range(count):
+        assert np.array_equal(res.logits[i], arrays["logits"][i]), i
+        got = gio.model_checkpoint_digests(res.checkpoints[i])
+        bad = [k for k, v in meta["checkpoints"][i].items() if got.get(k) != v]
+        assert not bad, (i, bad)
+        rows = meta["rows"][i]
+        if params.selectors:
+            want = [rows["block_01"], rows["block_04"], rows["block_07"], rows["block_10"]]
+            assert res.token_counts[i].tolist() == want, i
+    return res
+
+
+def test_full_model_matches_golden():
+    img, params = synth.full_workload()
+    _check_model_golden("full", img, params, 1)
+
+
+def test_infer_single_image_api():
+    from heatvit_amd.model import HeatViTModel
+    meta, arrays = gio.load("pruned")
+    imgs, params = synth.pruned_workload(2)
+    r = HeatViTModel().infer(imgs[1].reshape(-1), params)
+    assert list(r.logits) == arrays["logits"][1].tolist()
+    assert r.output_scale_exp == -14
+    assert gio.model_checkpoint_digests(r.checkpoints) == meta["checkpoints"][1]
+    for s, want in zip(r.selector_summary, meta["selector_summary"][1]):
+        assert s == want
+
+
+def test_pruned_model_matches_golden():
+    imgs, params = synth.pruned_workload()
+    _check_model_golden("pruned", imgs, params, len(imgs))
+
+
+def test_throughput_batch_vs_oracle_and_deterministic(oracle):
+    from heatvit_amd.model import HeatViTModel
+    imgs, params = synth.throughput_workload()
+    m = HeatViTModel()
+    r1 = m.infer_batch(imgs, params)
+    r2 = m.infer_batch(imgs, params)
+    assert np.array_equal(r1.logits, r2.logits) and np.array_equal(r1.token_counts,
+                                                                   r2.token_counts)
+    logits, counts, status = oracle.model_infer_batch(imgs, params)
+    assert not status.any()
+    assert np.array_equal(r1.logits, logits)
+    assert np.array_equal(r1.token_counts, counts)
+    # batch invariance: a sub-batch reproduces the same rows
+    r3 = m.infer_batch(imgs[100:103], params)
+    assert np.array_equal(r3.logits, r1.logits[100:103])
+
+
+def test_unpruned_control_vs_oracle(oracle):
+    from heatvit_amd.model import HeatViTModel
+    imgs, params = synth.throughput_workload(64)
+    ctrl = synth.unpruned_control(params)
+    r = HeatViTModel().infer_batch(imgs, ctrl)
+    logits, counts, status = oracle.model_infer_batch(imgs, ctrl)
+    assert not status.any()
+    assert np.array_equal(r.logits, logits)
+    assert (r.token_counts == 197).all()

@@ -1,0 +1,159 @@
+"""GPU parity of the HIP primitives and single kernels against the
+reference's committed vectors and the CPU oracle (bit-exact)."""
+
+import numpy as np
+import pytest
+
+import fixture_io as fx
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from heatvit_amd import ops as o
+    return o
+
+
+@pytest.mark.parametrize("suite", ["fixed", "requant"])
+def test_requant_vectors(ops, suite):
+    recs = fx.requant_records(suite)
+    for src in range(-32, 32):
+        for dst in range(-32, 32):
+            sel = [(v, e) for v, s, d, e in recs if s == src and d == dst]
+            if sel:
+                got = ops.requant([v for v, _ in sel], src, dst, 8)
+                assert got.tolist() == [e for _, e in sel], (src, dst)
+
+
+def test_gelu_plan_vectors(ops):
+    recs = fx.nonlinear_records()
+    xs = np.array([r[0] for r in recs])
+    assert ops.gelu(xs).tolist() == [r[1] for r in recs]
+    assert ops.plan_sigmoid(xs).tolist() == [r[2] for r in recs]
+
+
+def test_gelu_exhaustive_24bit(ops, oracle):
+    # Every Q8.16 input the call sites can produce (requant to 24 bits
+    # precedes every gelu), against the oracle's exact integer division.
+    xs = np.arange(-(1 << 23), 1 << 23, dtype=np.int64)
+    got = ops.gelu(xs)
+    want = oracle.gelu_array(xs)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, [(int(xs[i]), int(got[i]), int(want[i])) for i in bad[:5]]
+
+
+def test_softmax_vectors(ops):
+    rows = fx.softmax_rows()
+    att, sel = ops.softmax_rows([r[0] for r in rows])
+    for (x, want_att, want_sel), a, s in zip(rows, att, sel):
+        assert np.array_equal(a, want_att), x[:4]
+        assert np.array_equal(s, want_sel), x[:4]
+
+
+def test_layernorm_vectors(ops):
+    for x, g, b, exps, warn, expected in fx.layernorm_rows():
+        out, neg = ops.layernorm_rows(x[None], g, b, *exps)
+        assert np.array_equal(out[0], expected), exps
+        assert bool(neg[0]) == warn
+
+
+def test_layernorm_random_rows_vs_oracle(ops, oracle):
+    rng = np.random.default_rng(11)
+    for _ in range(24):
+        exps = (int(rng.integers(-32, 1)), int(rng.integers(-32, 32)),
+                int(rng.integers(-32, 32)), int(rng.integers(-32, 32)))
+        x = rng.integers(-128, 128, (300, 192))
+        g = rng.integers(-128, 128, 192)
+        b = rng.integers(-128, 128, 192)
+        out, _ = ops.layernorm_rows(x, g, b, *exps)
+        assert np.array_equal(out, oracle.layernorm_rows(x, g, b, *exps)), exps
+
+
+def test_gemm_scenarios(ops):
+    for sc in fx.gemm_scenarios():
+        if sc["unsigned"]:
+            continue  # unsigned A runs only inside the attention kernel (P V)
+        s0, s1, dst = sc["scales"]
+        for h in range(sc["heads"]):
+            w = sc["b"][h].T if sc["transpose"] else sc["b"][h]
+            bias = None if sc["bias"] is None else sc["bias"][h * sc["n"]:(h + 1) * sc["n"]]
+            got = ops.gemm_writeback(sc["a"][h], w, bias, s0 + s1, dst, sc["bits"])
+            assert np.array_equal(got, sc["expected"][h]), (sc["name"], h)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1000, 192), (197, 576, 192), (1000, 768, 192),
+                                   (333, 192, 768), (64, 100, 64), (4099, 192, 192)])
+def test_gemm_epilogues_vs_oracle(ops, oracle, m, n, k):
+    rng = np.random.default_rng(m * 7 + n)
+    a = rng.integers(-128, 128, (m, k))
+    w = rng.integers(-128, 128, (k, n))
+    bias = rng.integers(-(1 << 20), 1 << 20, n)
+    acc = oracle.gemm(a, w, bias)
+    for src, dst in ((-14, -7), (-20, -4), (-8, -12), (-30, 5)):
+        assert np.array_equal(ops.gemm_writeback(a, w, bias, src, dst, 8),
+                              oracle.gemm_writeback(acc, src, dst, 8)), (src, dst)
+    assert np.array_equal(ops.gemm_writeback(a, w, bias, -14, -14, 32),
+                          oracle.gemm_writeback(acc, -14, -14, 32))
+    rows = slice(0, 96)  # the element-wise oracle checks below are scalar
+    # GELU post-op (transformer.py:349-358)
+    for src, dst in ((-14, -7), (-22, -5)):
+        q = oracle.requant_array(acc[rows], src, -16, 24)
+        want = oracle.requant_array(oracle.gelu_array(q).astype(np.int64), -16, dst, 8)
+        got = ops.gemm_writeback(a, w, bias, src, dst, 8, epilogue="gelu")
+        assert np.array_equal(got[rows], want), (src, dst)
+    # residual align-add (transformer.py:96-101)
+    res = rng.integers(-128, 128, (m, n))
+    for mid, rexp, out in ((-7, -6, -7), (-9, -4, -5), (-30, 20, -3)):
+        t = oracle.gemm_writeback(acc[rows], -14, mid, 8).astype(np.int64)
+        c = min(rexp, mid)
+        want = np.vectorize(lambda r, tt: oracle.requant(
+            (int(r) << (rexp - c)) + (int(tt) << (mid - c)), c, out, 8))(res[rows], t)
+        got = ops.gemm_writeback(a, w, bias, -14, out, 8, epilogue="residual", mid_exp=mid,
+                                 residual=res, res_exp=rexp)
+        assert np.array_equal(got[rows], want), (mid, rexp, out)
+
+
+def test_gemm_gather_rows(ops, oracle):
+    rng = np.random.default_rng(5)
+    a = rng.integers(-128, 128, (500, 192))
+    w = rng.integers(-128, 128, (192, 1000))
+    rows = np.array([0, 197, 7, 499, 3], np.int32)
+    got = ops.gemm_writeback(a, w, None, -14, -14, 32, a_rows=rows)
+    want = oracle.gemm_writeback(oracle.gemm(a[rows], w, None), -14, -14, 32)
+    assert np.array_equal(got, want)
+
+
+def test_finalize_vectors():
+    from heatvit_amd.selector import finalize_tokens
+    for name, meta, tokens, scores, expected in fx.selector_cases():
+        pkg = bool(meta["input_package_present"])
+        r = finalize_tokens(tokens[0], tokens[1:-1] if pkg else tokens[1:],
+                            tokens[-1] if pkg else None, scores)
+        assert np.array_equal(r.tokens, expected), name
+        assert len(r.tokens) == meta["next_token_count"]
+        assert int(r.package_present) == meta["next_package_present"]
+        assert r.warnings == meta["warning_flags"]
+
+
+def test_finalize_random_vs_oracle(oracle):
+    from heatvit_amd.selector import finalize_tokens
+    rng = np.random.default_rng(9)
+    for trial in range(30):
+        n = int(rng.integers(2, 198))
+        toks = rng.integers(-128, 128, (n, 192))
+        pkg = bool(trial % 2) and n >= 3
+        c = n - 1
+        scores = rng.integers(0, 65537, c)
+        if trial % 5 == 0:
+            scores[:] = 0  # zero denominator fallback
+        if trial % 7 == 0:
+            scores[rng.integers(0, c, c // 2)] = 32768  # threshold ties
+        normal = toks[1:-1] if pkg else toks[1:]
+        inc = toks[-1] if pkg else None
+        r = finalize_tokens(toks[0], normal, inc, scores)
+        want, kept, st = oracle.finalize_tokens(toks[0], normal, inc, scores)
+        assert np.array_equal(r.tokens, want), trial
+        assert np.array_equal(r.kept_index, kept)
+        assert (r.kept_normal_count, r.pruned_normal_count, r.warnings, int(r.package_present)) \
+            == (st.kept_normal_count, st.pruned_normal_count, st.warnings, st.package_present)
