@@ -15,6 +15,8 @@ HV_PRIM_REQUANT, HV_PRIM_GELU, HV_PRIM_PLAN, HV_PRIM_RSA = 0, 1, 2, 3
 HV_EPI_I8, HV_EPI_I32, HV_EPI_GELU, HV_EPI_RESIDUAL = 0, 1, 2, 3
 HV_A_ROWS, HV_A_GATHER = 0, 1
 ABI_VERSION = 1
+PROF_CLASSES = ("patch", "layernorm", "gemm_qkv", "attention", "gemm_proj", "gemm_ffn1",
+                "gemm_ffn2", "selector", "head", "other")
 
 _vp = C.c_void_p
 _i32 = C.c_int32
@@ -109,6 +111,8 @@ def lib():
     L.hv_model_workspace_bytes.argtypes = [C.c_int]
     L.hv_model_forward.argtypes = [C.POINTER(ModelDev), _vp, C.c_int, _vp, _vp, _vp, _vp, _vp,
                                    _vp, C.c_size_t, _vp]
+    L.hv_profile_enable.argtypes = [C.c_int]
+    L.hv_profile_read.argtypes = [_vp, _vp, C.c_int]
     if L.hv_abi_version() != ABI_VERSION:
         raise RuntimeError("libheatvit_hip.so ABI version mismatch; rebuild it")
     _LIB = L
@@ -131,5 +135,5 @@ def exported_symbols():
     return ("hv_last_error", "hv_abi_version", "hv_eval_primitive", "hv_softmax_rows",
             "hv_layernorm_i8", "hv_gemm_i8", "hv_block_workspace_bytes", "hv_block_forward",
             "hv_selector_workspace_bytes", "hv_selector_forward", "hv_selector_finalize",
-            "hv_patch_embedding",
+            "hv_patch_embedding", "hv_profile_enable", "hv_profile_read",
             "hv_model_workspace_bytes", "hv_model_forward")

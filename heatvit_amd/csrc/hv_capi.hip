@@ -4,6 +4,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <vector>
+
 #include "hv_device.h"
 #include "hv_internal.h"
 
@@ -22,6 +24,45 @@ int fail(int status, const char *fmt, ...) {
 int check_hip(hipError_t e, const char *what) {
   if (e == hipSuccess) return HV_OK;
   return fail(HV_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// ---------------------------------------------------------------- profiling
+// With profiling on, every launch of the forwards is bracketed by two HIP
+// events recorded on the launch stream; hv_profile_read() sums the elapsed
+// time per kernel class.  Host-side state: one profiling client at a time.
+
+struct ProfEvent {
+  int cls;
+  hipEvent_t a, b;
+};
+static bool g_prof_on = false;
+static std::vector<ProfEvent> g_prof;
+
+struct ProfScope {
+  int cls;
+  hipStream_t s;
+  hipEvent_t a = nullptr;
+  ProfScope(int c, hipStream_t st) : cls(c), s(st) {
+    if (g_prof_on && hipEventCreate(&a) == hipSuccess) (void)hipEventRecord(a, s);
+  }
+  ~ProfScope() {
+    if (!a) return;
+    hipEvent_t b;
+    if (hipEventCreate(&b) == hipSuccess) {
+      (void)hipEventRecord(b, s);
+      g_prof.push_back({cls, a, b});
+    } else {
+      (void)hipEventDestroy(a);
+    }
+  }
+};
+
+static void prof_clear() {
+  for (auto &e : g_prof) {
+    (void)hipEventDestroy(e.a);
+    (void)hipEventDestroy(e.b);
+  }
+  g_prof.clear();
 }
 
 // ---------------------------------------------------------------- utilities
@@ -103,14 +144,21 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   int8_t *hidden = ck && ck->hidden ? ck->hidden : w.hidden;
   int rc;
 
-  rc = launch_layernorm(x, p.ln1_gamma, p.ln1_beta, ln1, max_rows, rows_dev, p.x_exp,
-                        p.gamma1_exp, p.beta1_exp, p.ln1_out_exp, nullptr, s);
+  {
+    ProfScope ps(HV_PROF_LAYERNORM, s);
+    rc = launch_layernorm(x, p.ln1_gamma, p.ln1_beta, ln1, max_rows, rows_dev, p.x_exp,
+                          p.gamma1_exp, p.beta1_exp, p.ln1_out_exp, nullptr, s);
+  }
   if (rc) return rc;
   GemmArgs g{};
   g.a = ln1; g.b = p.wqkv_p; g.bias = p.bqkv; g.c = qkv; g.m_dev = rows_dev;
   g.m = max_rows; g.n = 576; g.k = 192; g.lda = 192; g.ldc = 576;
   g.shift_a = p.qkv_out_exp - (p.ln1_out_exp + p.wqkv_exp);
-  if ((rc = launch_gemm(g, A_ROWS, HV_EPI_I8, s))) return rc;
+  {
+    ProfScope ps(HV_PROF_GEMM_QKV, s);
+    rc = launch_gemm(g, A_ROWS, HV_EPI_I8, s);
+  }
+  if (rc) return rc;
 
   AttnArgs a{};
   a.qkv = qkv; a.offsets = offsets; a.ctx = ctx; a.batch = batch;
@@ -119,24 +167,39 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   a.score_shift = p.score_exp - 2 * p.qkv_out_exp;
   a.q16_shift = -(p.score_exp + 13);
   a.ctx_shift = p.context_out_exp - (p.prob_exp + p.qkv_out_exp);
-  if ((rc = launch_attention(a, s))) return rc;
+  {
+    ProfScope ps(HV_PROF_ATTENTION, s);
+    rc = launch_attention(a, s);
+  }
+  if (rc) return rc;
 
   g = GemmArgs{};
   g.a = ctx; g.b = p.wproj_p; g.bias = p.bproj; g.c = y; g.res = x; g.aux = ck ? ck->msa : nullptr;
   g.m_dev = rows_dev; g.m = max_rows; g.n = 192; g.k = 192; g.lda = 192; g.ldc = 192; g.ldr = 192;
   g.shift_a = p.msa_out_exp - (p.context_out_exp + p.wproj_exp);
   g.mid_exp = p.msa_out_exp; g.res_exp = p.x_exp; g.out_exp = p.ffn_x_exp;
-  if ((rc = launch_gemm(g, A_ROWS, HV_EPI_RESIDUAL, s))) return rc;
+  {
+    ProfScope ps(HV_PROF_GEMM_PROJ, s);
+    rc = launch_gemm(g, A_ROWS, HV_EPI_RESIDUAL, s);
+  }
+  if (rc) return rc;
 
-  rc = launch_layernorm(y, p.ln2_gamma, p.ln2_beta, ln2, max_rows, rows_dev, p.ffn_x_exp,
-                        p.gamma2_exp, p.beta2_exp, p.ln2_out_exp, nullptr, s);
+  {
+    ProfScope ps(HV_PROF_LAYERNORM, s);
+    rc = launch_layernorm(y, p.ln2_gamma, p.ln2_beta, ln2, max_rows, rows_dev, p.ffn_x_exp,
+                          p.gamma2_exp, p.beta2_exp, p.ln2_out_exp, nullptr, s);
+  }
   if (rc) return rc;
   g = GemmArgs{};
   g.a = ln2; g.b = p.w1_p; g.bias = p.b1; g.c = hidden; g.m_dev = rows_dev;
   g.m = max_rows; g.n = 768; g.k = 192; g.lda = 192; g.ldc = 768;
   g.shift_a = -16 - (p.ln2_out_exp + p.w1_exp);
   g.shift_b = p.hidden_out_exp + 16;
-  if ((rc = launch_gemm(g, A_ROWS, HV_EPI_GELU, s))) return rc;
+  {
+    ProfScope ps(HV_PROF_GEMM_FFN1, s);
+    rc = launch_gemm(g, A_ROWS, HV_EPI_GELU, s);
+  }
+  if (rc) return rc;
 
   g = GemmArgs{};
   g.a = hidden; g.b = p.w2_p; g.bias = p.b2; g.c = z; g.res = y;
@@ -144,6 +207,7 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   g.m_dev = rows_dev; g.m = max_rows; g.n = 192; g.k = 768; g.lda = 768; g.ldc = 192; g.ldr = 192;
   g.shift_a = p.ffn_out_exp - (p.hidden_out_exp + p.w2_exp);
   g.mid_exp = p.ffn_out_exp; g.res_exp = p.ffn_x_exp; g.out_exp = p.out_exp;
+  ProfScope ps(HV_PROF_GEMM_FFN2, s);
   return launch_gemm(g, A_ROWS, HV_EPI_RESIDUAL, s);
 }
 
@@ -338,8 +402,16 @@ int hv_model_forward(const hv_model_dev *p, const int8_t *images, int batch, int
   int32_t *st = state ? state : w.state;
   int rc;
 
-  if ((rc = launch_init_offsets(w.off_a, w.pkg_a, token_counts, batch, HV_MAX_TOKENS, s))) return rc;
-  if ((rc = launch_patch_embed(p->patch, images, batch, w.xa, s))) return rc;
+  {
+    ProfScope ps(HV_PROF_OTHER, s);
+    rc = launch_init_offsets(w.off_a, w.pkg_a, token_counts, batch, HV_MAX_TOKENS, s);
+  }
+  if (rc) return rc;
+  {
+    ProfScope ps(HV_PROF_PATCH, s);
+    rc = launch_patch_embed(p->patch, images, batch, w.xa, s);
+  }
+  if (rc) return rc;
   if (ckpt && (rc = launch_copy_ckpt(w.xa, w.off_a, batch, ckpt, ckpt_rows, 0, s))) return rc;
 
   int sel = 0;
@@ -351,7 +423,11 @@ int hv_model_forward(const hv_model_dev *p, const int8_t *images, int batch, int
       a.out_tokens = w.xb; a.out_offsets = w.off_b; a.pkg_out = w.pkg_b;
       a.fused = w.fused; a.kept_index = w.kept; a.state = st + (size_t)sel * batch * 5;
       a.token_counts = token_counts; a.stage = sel + 1;
-      if ((rc = launch_selector(a, s))) return rc;
+      {
+        ProfScope ps(HV_PROF_SELECTOR, s);
+        rc = launch_selector(a, s);
+      }
+      if (rc) return rc;
       std::swap(w.xa, w.xb);
       std::swap(w.off_a, w.off_b);
       std::swap(w.pkg_a, w.pkg_b);
@@ -365,16 +441,46 @@ int hv_model_forward(const hv_model_dev *p, const int8_t *images, int batch, int
     if (ckpt && (rc = launch_copy_ckpt(w.xa, w.off_a, batch, ckpt, ckpt_rows, 3 + blk, s))) return rc;
   }
   // Final LayerNorm over every row (model.py:102-106), head on CLS rows.
-  if ((rc = launch_layernorm(w.xa, p->final_gamma, p->final_beta, w.blk.ln, max_rows,
-                             w.off_a + batch, p->blocks[11].out_exp, p->final_gamma_exp,
-                             p->final_beta_exp, p->final_ln_out_exp, nullptr, s)))
-    return rc;
+  {
+    ProfScope ps(HV_PROF_LAYERNORM, s);
+    rc = launch_layernorm(w.xa, p->final_gamma, p->final_beta, w.blk.ln, max_rows,
+                          w.off_a + batch, p->blocks[11].out_exp, p->final_gamma_exp,
+                          p->final_beta_exp, p->final_ln_out_exp, nullptr, s);
+  }
+  if (rc) return rc;
   if (ckpt && (rc = launch_copy_ckpt(w.blk.ln, w.off_a, batch, ckpt, ckpt_rows, 16, s))) return rc;
   GemmArgs g{};
   g.a = w.blk.ln; g.a_rows = w.off_a; g.b = p->head_w_p; g.bias = p->head_b; g.c = logits;
   g.m = batch; g.n = 1000; g.k = 192; g.lda = 192; g.ldc = 1000;
   g.shift_a = -14 - (p->final_ln_out_exp + p->head_w_exp);
+  ProfScope ps(HV_PROF_HEAD, s);
   return launch_gemm(g, A_GATHER, HV_EPI_I32, s);
+}
+
+int hv_profile_enable(int on) {
+  prof_clear();
+  g_prof_on = on != 0;
+  return HV_OK;
+}
+
+int hv_profile_read(float *ms, int32_t *launches, int n) {
+  g_err[0] = 0;
+  for (int i = 0; i < n; ++i) {
+    if (ms) ms[i] = 0.f;
+    if (launches) launches[i] = 0;
+  }
+  int rc = HV_OK;
+  for (auto &e : g_prof) {
+    float t = 0.f;
+    if (rc == HV_OK) rc = check_hip(hipEventSynchronize(e.b), "profile sync");
+    if (rc == HV_OK) rc = check_hip(hipEventElapsedTime(&t, e.a, e.b), "profile elapsed");
+    if (rc == HV_OK && e.cls >= 0 && e.cls < n) {
+      if (ms) ms[e.cls] += t;
+      if (launches) launches[e.cls] += 1;
+    }
+  }
+  prof_clear();
+  return rc;
 }
 
 }  // extern "C"

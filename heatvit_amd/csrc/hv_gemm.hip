@@ -47,7 +47,7 @@ __device__ __forceinline__ const int8_t *patch_ptr(const int8_t *images, int r, 
   return images + (size_t)b * kImageBytes + ((pr * 16 + in_row) * 224 + pc * 16) * 3 + rem;
 }
 
-template <int MT, int NT, int EPI, int AMODE>
+template <int MT, int NT, int EPI, int AMODE, int KTC>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -58,7 +58,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
   const int m0 = mb * BM + wm * 32 * MT;
   const int n32t = (g.n + 31) >> 5;
   const int ntile0 = (nb * BN >> 5) + wn * NT;
-  const int KT = g.k >> 5;
+  const int KT = KTC ? KTC : (g.k >> 5);  // K/32 steps; compile-time for K = 192, 768
   const int khalf = (lane >> 5) * 16;
 
   int arow[MT];
@@ -97,6 +97,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
     for (int nt = 0; nt < NT; ++nt) bv[nt] = *reinterpret_cast<const v4i *>(bp[nt] + kt * 1024);
   };
   load(0, a_cur, b_cur);
+#pragma unroll(KTC ? 6 : 1)
   for (int kt = 0; kt < KT; ++kt) {
     if (kt + 1 < KT) load(kt + 1, a_nxt, b_nxt);
 #pragma unroll
@@ -155,7 +156,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
   }
 }
 
-template <int MT, int NT, int EPI, int AMODE>
+template <int MT, int NT, int EPI, int AMODE, int KTC = 0>
 static int run(const GemmArgs &g, hipStream_t s) {
   constexpr int BM = 64 * MT, BN = 64 * NT;
   const int n_blocks = (g.n + BN - 1) / BN;
@@ -163,8 +164,8 @@ static int run(const GemmArgs &g, hipStream_t s) {
   const long long grid = m_blocks * n_blocks;
   if (grid <= 0) return HV_OK;
   if (grid > 0x7fffffff) return fail(HV_EVALUE, "gemm grid too large");
-  hipLaunchKernelGGL((k_gemm<MT, NT, EPI, AMODE>), dim3((unsigned)grid), dim3(256), 0, s, g,
-                     n_blocks);
+  hipLaunchKernelGGL((k_gemm<MT, NT, EPI, AMODE, KTC>), dim3((unsigned)grid), dim3(256), 0, s,
+                     g, n_blocks);
   return check_hip(hipGetLastError(), "k_gemm launch");
 }
 
@@ -172,15 +173,26 @@ static int run(const GemmArgs &g, hipStream_t s) {
 // 192) uses 192-wide column blocks; other N (head 1000, tests) 128-wide.
 // Large-N GEMMs use 128-row tiles, N = 192 GEMMs 64-row tiles so the grid
 // still fills 256 CUs.
-template <int EPI, int AMODE>
+template <int EPI, int AMODE, int KTC>
 static int dispatch_tiles(const GemmArgs &g, hipStream_t s) {
   // The GELU epilogue needs more registers; 128x128 tiles keep it spill-free.
-  if (EPI == EPI_GELU && g.n > 192) return run<2, 2, EPI, AMODE>(g, s);
+  if (EPI == EPI_GELU && g.n > 192) return run<2, 2, EPI, AMODE, KTC>(g, s);
   if (g.n % 192 == 0) {
-    if (g.n > 192) return run<2, 3, EPI, AMODE>(g, s);
-    return run<1, 3, EPI, AMODE>(g, s);
+    if (g.n > 192) return run<2, 3, EPI, AMODE, KTC>(g, s);
+    return run<1, 3, EPI, AMODE, KTC>(g, s);
   }
-  return run<1, 2, EPI, AMODE>(g, s);
+  return run<1, 2, EPI, AMODE, KTC>(g, s);
+}
+
+// K = 192 (every GEMM but FFN2) and K = 768 (FFN2) get compile-time trip
+// counts; other K (tests, tails) take the runtime loop.
+template <int EPI>
+static int dispatch_k(const GemmArgs &g, int a_mode, hipStream_t s) {
+  if (a_mode == A_GATHER) return dispatch_tiles<EPI, A_GATHER, 0>(g, s);
+  if (a_mode != A_ROWS) return fail(HV_EVALUE, "gemm: bad A mode %d", a_mode);
+  if (g.k == 192) return dispatch_tiles<EPI, A_ROWS, 6>(g, s);
+  if (g.k == 768) return dispatch_tiles<EPI, A_ROWS, 24>(g, s);
+  return dispatch_tiles<EPI, A_ROWS, 0>(g, s);
 }
 
 int launch_gemm(const GemmArgs &g, int a_mode, int epi, hipStream_t s) {
@@ -190,21 +202,13 @@ int launch_gemm(const GemmArgs &g, int a_mode, int epi, hipStream_t s) {
   if (a_mode != A_PATCH && (g.lda % 16 || ((uintptr_t)g.a & 15)))
     return fail(HV_EVALUE, "gemm: A must be 16-byte aligned with lda %% 16 == 0");
   if (g.k > 131071) return fail(HV_EOVERFLOW, "gemm: K=%d may overflow int32", g.k);
-#define HV_EPI_CASE(E)                                                          \
-  case E:                                                                       \
-    switch (a_mode) {                                                           \
-      case A_ROWS: return dispatch_tiles<E, A_ROWS>(g, s);                      \
-      case A_GATHER: return dispatch_tiles<E, A_GATHER>(g, s);                  \
-      default: return fail(HV_EVALUE, "gemm: bad A mode %d", a_mode);            \
-    }
   switch (epi) {
-    HV_EPI_CASE(EPI_I8)
-    HV_EPI_CASE(EPI_I32)
-    HV_EPI_CASE(EPI_GELU)
-    HV_EPI_CASE(EPI_RES)
+    case EPI_I8: return dispatch_k<EPI_I8>(g, a_mode, s);
+    case EPI_I32: return dispatch_k<EPI_I32>(g, a_mode, s);
+    case EPI_GELU: return dispatch_k<EPI_GELU>(g, a_mode, s);
+    case EPI_RES: return dispatch_k<EPI_RES>(g, a_mode, s);
     default: return fail(HV_EVALUE, "gemm: bad epilogue %d", epi);
   }
-#undef HV_EPI_CASE
 }
 
 // CLS rows: row b*197 = align_add(cls @ cls_exp, pos[0] @ pos_exp -> tokens)
@@ -235,7 +239,7 @@ int launch_patch_embed(const hv_patch_dev &p, const int8_t *images, int batch, i
   g.mid_exp = p.activation_exp;
   g.res_exp = p.pos_exp;
   g.out_exp = p.tokens_exp;
-  int rc = run<1, 3, EPI_PATCH, A_PATCH>(g, s);
+  int rc = run<1, 3, EPI_PATCH, A_PATCH, 24>(g, s);
   if (rc) return rc;
   hipLaunchKernelGGL(k_cls_rows, dim3(batch), dim3(192), 0, s, p.cls, p.pos, x, p.cls_exp,
                      p.pos_exp, p.tokens_exp);

@@ -233,6 +233,29 @@ int hv_model_forward(const hv_model_dev *p, const int8_t *images, int batch, int
                      int32_t *token_counts, int32_t *state, int8_t *ckpt, int32_t *ckpt_rows,
                      void *workspace, size_t workspace_bytes, hv_stream_t stream);
 
+/* ------------------------------------------------------------------ */
+/* Kernel-class timing with HIP events (for benchmarks).  While enabled, */
+/* the forwards bracket every launch with two events on the launch       */
+/* stream; hv_profile_read() waits for them and returns the summed       */
+/* milliseconds and launch counts per class (arrays of n entries), then  */
+/* clears the record.  Not thread-safe: one profiling client at a time.  */
+/* ------------------------------------------------------------------ */
+
+#define HV_PROF_PATCH 0
+#define HV_PROF_LAYERNORM 1
+#define HV_PROF_GEMM_QKV 2
+#define HV_PROF_ATTENTION 3
+#define HV_PROF_GEMM_PROJ 4
+#define HV_PROF_GEMM_FFN1 5
+#define HV_PROF_GEMM_FFN2 6
+#define HV_PROF_SELECTOR 7
+#define HV_PROF_HEAD 8
+#define HV_PROF_OTHER 9
+#define HV_PROF_CLASSES 10
+
+int hv_profile_enable(int on);
+int hv_profile_read(float *ms, int32_t *launches, int n);
+
 #ifdef __cplusplus
 }
 #endif
