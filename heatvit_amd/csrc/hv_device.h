@@ -96,6 +96,34 @@ __device__ __forceinline__ int align_add_i8(int a, int a_exp, int b, int b_exp, 
   return (int)requant128(s, out_exp - c, 8);
 }
 
+// requant (fixed.py:37-45) in int32 arithmetic for |v| < 2^30; lo/hi are
+// the saturation bounds of the target width.  rsa for negative v uses
+// (v + 2^(s-1) - 1) >> s, the floor form of -((-v + 2^(s-1)) >> s).
+__device__ __forceinline__ int requant_i32(int v, int shift, int lo, int hi) {
+  int r;
+  if (shift > 0) {
+    r = shift >= 31 ? 0 : (v + (1 << (shift - 1)) - (v < 0 ? 1 : 0)) >> shift;
+  } else if (shift == 0) {
+    r = v;
+  } else {
+    const int sl = -shift;
+    if (sl >= 31) return v > 0 ? hi : (v < 0 ? lo : 0);
+    const i64 w = (i64)v * (1ll << sl);
+    return w > hi ? hi : (w < lo ? lo : (int)w);
+  }
+  return r > hi ? hi : (r < lo ? lo : r);
+}
+
+// _align_add_requant with host-precomputed shifts da = a_exp - c,
+// db = b_exp - c, os = out_exp - c (c = min(a_exp, b_exp)); int32 when
+// da, db <= 21 (then |sum| <= 2^29).
+__device__ __forceinline__ int align_add_pre(int a, int b, int da, int db, int os, bool narrow) {
+  if (narrow) return requant_i32(a * (1 << da) + b * (1 << db), os, -128, 127);
+  if (da <= 54 && db <= 54)
+    return (int)requant_shift((i64)((u64)(i64)a << da) + (i64)((u64)(i64)b << db), os, 8);
+  return (int)requant128((i128)a * ((i128)1 << da) + (i128)b * ((i128)1 << db), os, 8);
+}
+
 // ---------------------------------------------------------------- nonlinear.py
 
 // floor(num / den) for num < 2^40 and 2^16 <= den < 2^24 with a quotient

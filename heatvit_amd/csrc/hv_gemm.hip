@@ -96,9 +96,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) bv[nt] = *reinterpret_cast<const v4i *>(bp[nt] + kt * 1024);
   };
-  load(0, a_cur, b_cur);
-#pragma unroll(KTC ? 6 : 1)
-  for (int kt = 0; kt < KT; ++kt) {
+  auto step = [&](int kt) {
     if (kt + 1 < KT) load(kt + 1, a_nxt, b_nxt);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -112,47 +110,153 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) b_cur[nt] = b_nxt[nt];
     }
+  };
+  load(0, a_cur, b_cur);
+  if constexpr (KTC > 0) {
+#pragma unroll
+    for (int kt = 0; kt < KTC; ++kt) step(kt);
+  } else {
+    for (int kt = 0; kt < KT; ++kt) step(kt);
   }
 
-  // 32x32 accumulator layout: lane l holds column l%32 and, in element i,
-  // row 8*(i/4) + 4*(l/32) + i%4 of the tile.
+  // Epilogue.  Each wavefront stages one 32x32 int32 accumulator tile at a
+  // time in its LDS slice (MFMA layout: lane l holds column l%32 and, in
+  // element i, row 8*(i/4) + 4*(l/32) + i%4), then lane l finishes row l/2,
+  // columns 16*(l%2) + 4*g .. +3 for g = 0..3: four outputs per group with
+  // one bias/residual vector load and one packed store.  With |acc| <=
+  // K*2^14 and |bias| <= acc_lim, v = acc + bias stays below 2^30 and the
+  // epilogue's requants are exact in int32 (requant_i32); other columns take
+  // the 64-bit forms.
+  __shared__ int stage[4][32 * 36];
+  int *T = stage[wave];
+  const int er = lane >> 1, ec0 = (lane & 1) * 16;
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    if (!nvalid[nt]) continue;
-    const int col = (ntile0 + nt) * 32 + (lane & 31);
-    if (col >= g.n) continue;
-    const i64 bias = g.bias ? (i64)g.bias[col] : 0;
+  for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
+    for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int row = m0 + mt * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        if (row >= M) continue;
-        const i64 v = (i64)acc[mt][nt][i] + bias;
-        if (EPI == EPI_I32) {
-          reinterpret_cast<int32_t *>(g.c)[(size_t)row * g.ldc + col] =
-              (int32_t)requant_shift(v, g.shift_a, 32);
-        } else if (EPI == EPI_I8) {
-          reinterpret_cast<int8_t *>(g.c)[(size_t)row * g.ldc + col] =
-              (int8_t)requant_shift(v, g.shift_a, 8);
-        } else if (EPI == EPI_GELU) {
-          reinterpret_cast<int8_t *>(g.c)[(size_t)row * g.ldc + col] =
-              (int8_t)gelu_post(v, g.shift_a, g.shift_b);
-        } else if (EPI == EPI_RES) {
-          const int t = (int)requant_shift(v, g.shift_a, 8);
-          if (g.aux) g.aux[(size_t)row * g.ldc + col] = (int8_t)t;
-          const int r = g.res[(size_t)row * g.ldr + col];
-          reinterpret_cast<int8_t *>(g.c)[(size_t)row * g.ldc + col] =
-              (int8_t)align_add_i8(r, g.res_exp, t, g.mid_exp, g.out_exp);
-        } else {  // EPI_PATCH
-          const int t = (int)requant_shift(v, g.shift_a, 8);
-          const int b = row / kPatchesPerImage, p = row - b * kPatchesPerImage;
-          const int pos = g.pos[(size_t)(p + 1) * 192 + col];
-          reinterpret_cast<int8_t *>(g.c)[((size_t)b * kTokens + 1 + p) * g.ldc + col] =
-              (int8_t)align_add_i8(t, g.mid_exp, pos, g.res_exp, g.out_exp);
+      for (int i = 0; i < 16; ++i)
+        T[(8 * (i >> 2) + 4 * (lane >> 5) + (i & 3)) * 36 + (lane & 31)] = acc[mt][nt][i];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int row = m0 + mt * 32 + er;
+      if (nvalid[nt] && row < M) {
+#pragma unroll 1
+        for (int grp = 0; grp < 4; ++grp) {
+          const int cl = ec0 + 4 * grp;
+          const int col = (ntile0 + nt) * 32 + cl;
+          if (col >= g.n) break;
+          const v4i a4 = *reinterpret_cast<const v4i *>(&T[er * 36 + cl]);
+          const bool full = col + 3 < g.n;
+          int bias[4] = {0, 0, 0, 0};
+          if (g.bias) {
+            if (full && (g.n & 3) == 0) {
+              const v4i b4 = *reinterpret_cast<const v4i *>(g.bias + col);
+              bias[0] = b4[0]; bias[1] = b4[1]; bias[2] = b4[2]; bias[3] = b4[3];
+            } else {
+#pragma unroll
+              for (int j = 0; j < 4; ++j) bias[j] = col + j < g.n ? g.bias[col + j] : 0;
+            }
+          }
+          int rv[4] = {0, 0, 0, 0};
+          if (EPI == EPI_RES) {
+            const int8_t *rp = g.res + (size_t)row * g.ldr + col;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) rv[j] = col + j < g.n ? rp[j] : 0;
+          }
+          size_t orow = (size_t)row;
+          if (EPI == EPI_PATCH) {
+            const int b = row / kPatchesPerImage, p = row - b * kPatchesPerImage;
+            orow = (size_t)b * kTokens + 1 + p;
+            const int8_t *pp = g.pos + (size_t)(p + 1) * 192 + col;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) rv[j] = pp[j];
+          }
+          int out[4], aux[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const bool n32 = g.narrow_ok && bias[j] <= g.acc_lim && bias[j] >= -g.acc_lim;
+            const int v32 = a4[j] + (n32 ? bias[j] : 0);
+            const i64 v = (i64)a4[j] + bias[j];
+            if (EPI == EPI_I32) {
+              out[j] = (int)requant_shift(v, g.shift_a, 32);
+            } else if (EPI == EPI_I8) {
+              out[j] = n32 ? requant_i32(v32, g.shift_a, -128, 127)
+                           : (int)requant_shift(v, g.shift_a, 8);
+            } else if (EPI == EPI_GELU) {
+              if (n32) {
+                const int q = requant_i32(v32, g.shift_a, -(1 << 23), (1 << 23) - 1);
+                out[j] = requant_i32(gelu_q16(q), g.shift_b, -128, 127);
+              } else {
+                out[j] = gelu_post(v, g.shift_a, g.shift_b);
+              }
+            } else {  // EPI_RES, EPI_PATCH
+              const int t = n32 ? requant_i32(v32, g.shift_a, -128, 127)
+                                : (int)requant_shift(v, g.shift_a, 8);
+              aux[j] = t;
+              out[j] = EPI == EPI_RES ? align_add_pre(rv[j], t, g.da, g.db, g.os, n32)
+                                      : align_add_pre(t, rv[j], g.da, g.db, g.os, n32);
+            }
+          }
+          if (EPI == EPI_I32) {
+            int32_t *cp = reinterpret_cast<int32_t *>(g.c) + orow * g.ldc + col;
+            if (full && ((g.ldc & 3) == 0)) {
+              *reinterpret_cast<v4i *>(cp) = v4i{out[0], out[1], out[2], out[3]};
+            } else {
+#pragma unroll
+              for (int j = 0; j < 4; ++j)
+                if (col + j < g.n) cp[j] = out[j];
+            }
+          } else {
+            int8_t *cp = reinterpret_cast<int8_t *>(g.c) + orow * g.ldc + col;
+            const int word = (out[0] & 0xFF) | ((out[1] & 0xFF) << 8) | ((out[2] & 0xFF) << 16) |
+                             ((out[3] & 0xFF) << 24);
+            if (full && ((g.ldc & 3) == 0)) {
+              *reinterpret_cast<int *>(cp) = word;
+            } else {
+#pragma unroll
+              for (int j = 0; j < 4; ++j)
+                if (col + j < g.n) cp[j] = (int8_t)out[j];
+            }
+            if (EPI == EPI_RES && g.aux) {
+              int8_t *xp = g.aux + (size_t)row * g.ldc + col;
+              const int aw = (aux[0] & 0xFF) | ((aux[1] & 0xFF) << 8) | ((aux[2] & 0xFF) << 16) |
+                             ((aux[3] & 0xFF) << 24);
+              if (full && ((g.ldc & 3) == 0)) {
+                *reinterpret_cast<int *>(xp) = aw;
+              } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                  if (col + j < g.n) xp[j] = (int8_t)aux[j];
+              }
+            }
+          }
         }
       }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
+  }
+}
+
+// Shared host-side set-up of the int32 epilogue preconditions.
+static void epilogue_limits(GemmArgs &g, int epi) {
+  const long long acc_max = (long long)g.k * 128 * 128;  // |A W| bound (int8 x int8)
+  const long long lim = (1ll << 30) - 1 - acc_max;
+  g.acc_lim = lim > 0 ? (int)lim : -1;
+  g.narrow_ok = 1;
+  if (epi == EPI_RES || epi == EPI_PATCH) {
+    // residual: align_add(res @ res_exp, t @ mid_exp -> out_exp);
+    // patch:    align_add(t @ mid_exp, pos @ res_exp -> out_exp)
+    const int a_exp = epi == EPI_RES ? g.res_exp : g.mid_exp;
+    const int b_exp = epi == EPI_RES ? g.mid_exp : g.res_exp;
+    const int c = a_exp < b_exp ? a_exp : b_exp;
+    g.da = a_exp - c;
+    g.db = b_exp - c;
+    g.os = g.out_exp - c;
+    g.narrow_ok = g.da <= 21 && g.db <= 21;
   }
 }
 
@@ -195,7 +299,9 @@ static int dispatch_k(const GemmArgs &g, int a_mode, hipStream_t s) {
   return dispatch_tiles<EPI, A_ROWS, 0>(g, s);
 }
 
-int launch_gemm(const GemmArgs &g, int a_mode, int epi, hipStream_t s) {
+int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
+  GemmArgs g = g_in;
+  epilogue_limits(g, epi);
   if (g.k <= 0 || g.k % 32) return fail(HV_EVALUE, "gemm: K=%d must be a positive multiple of 32", g.k);
   if (g.n <= 0) return fail(HV_EVALUE, "gemm: N=%d must be positive", g.n);
   if (g.m < 0) return fail(HV_EVALUE, "gemm: M=%d must be non-negative", g.m);
@@ -239,6 +345,7 @@ int launch_patch_embed(const hv_patch_dev &p, const int8_t *images, int batch, i
   g.mid_exp = p.activation_exp;
   g.res_exp = p.pos_exp;
   g.out_exp = p.tokens_exp;
+  epilogue_limits(g, EPI_PATCH);
   int rc = run<1, 3, EPI_PATCH, A_PATCH, 24>(g, s);
   if (rc) return rc;
   hipLaunchKernelGGL(k_cls_rows, dim3(batch), dim3(192), 0, s, p.cls, p.pos, x, p.cls_exp,

@@ -29,6 +29,10 @@ struct GemmArgs {
   int shift_a;  // epilogue shifts, see k_gemm
   int shift_b;
   int res_exp, mid_exp, out_exp;
+  // Filled by launch_gemm: int32 epilogue preconditions.
+  int acc_lim;     // a column takes the int32 path when |bias| <= acc_lim
+  int narrow_ok;   // epilogue shifts allow int32 (residual: da, db <= 21)
+  int da, db, os;  // residual / patch align-add shifts
 };
 
 int launch_gemm(const GemmArgs &g, int a_mode, int epilogue, hipStream_t s);
@@ -53,6 +57,7 @@ struct AttnArgs {
   int score_shift;    // score_exp - 2*qkv_out_exp (requant to int32)
   int q16_shift;      // -(score_exp + 13)
   int ctx_shift;      // context_out_exp - (prob_exp + qkv_out_exp)
+  int q16_mode, q16_s;  // int32 fast path for the score -> Q8.16 conversion
 };
 int launch_attention(const AttnArgs &a, hipStream_t s);
 

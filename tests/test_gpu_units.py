@@ -157,3 +157,23 @@ def test_finalize_random_vs_oracle(oracle):
         assert np.array_equal(r.kept_index, kept)
         assert (r.kept_normal_count, r.pruned_normal_count, r.warnings, int(r.package_present)) \
             == (st.kept_normal_count, st.pruned_normal_count, st.warnings, st.package_present)
+
+
+def test_gemm_wide_bias_columns_take_exact_fallback(ops, oracle):
+    # Columns whose bias is too large for the int32 epilogue path must still
+    # match (they run the 64-bit requant), next to int32-path columns.
+    rng = np.random.default_rng(21)
+    m, k, n = 130, 192, 576
+    a = rng.integers(-128, 128, (m, k))
+    w = rng.integers(-128, 128, (k, n))
+    bias = rng.integers(-(1 << 20), 1 << 20, n)
+    bias[::3] = rng.integers(-(1 << 31), 1 << 31, len(bias[::3]))
+    bias[1] = (1 << 31) - 1
+    bias[2] = -(1 << 31)
+    acc = oracle.gemm(a, w, bias)
+    for src, dst in ((-14, -7), (-40, -8), (-3, 10)):
+        assert np.array_equal(ops.gemm_writeback(a, w, bias, src, dst, 8),
+                              oracle.gemm_writeback(acc, src, dst, 8)), (src, dst)
+    q = oracle.requant_array(acc, -22, -16, 24)
+    want = oracle.requant_array(oracle.gelu_array(q).astype(np.int64), -16, -9, 8)
+    assert np.array_equal(ops.gemm_writeback(a, w, bias, -22, -9, 8, epilogue="gelu"), want)
