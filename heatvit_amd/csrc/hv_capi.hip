@@ -131,19 +131,20 @@ static BlockWs carve_block(Carve &cv, size_t rows) {
   return w;
 }
 
-// transformer_block (transformer.py:401-431) on rows [0, offsets[batch]).
+// transformer_block (transformer.py:401-431) on rows [0, offsets[batch]):
+// LN1, QKV, attention, proj + residual, LN2, FFN1 + GELU, FFN2 + residual.
 static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *offsets,
                          int batch, int max_rows, int8_t *z, const hv_block_ckpt *ck,
                          const BlockWs &w, hipStream_t s) {
   const int32_t *rows_dev = offsets + batch;
-  int8_t *ln1 = ck && ck->ln1 ? ck->ln1 : w.ln;
   int8_t *qkv = ck && ck->fused_qkv ? ck->fused_qkv : w.qkv;
   int8_t *ctx = ck && ck->concat ? ck->concat : w.ctx;
   int8_t *y = ck && ck->y ? ck->y : w.y;
-  int8_t *ln2 = ck && ck->ln2 ? ck->ln2 : w.ln;
   int8_t *hidden = ck && ck->hidden ? ck->hidden : w.hidden;
   int rc;
 
+  int8_t *ln1 = ck && ck->ln1 ? ck->ln1 : w.ln;
+  int8_t *ln2 = ck && ck->ln2 ? ck->ln2 : w.ln;
   {
     ProfScope ps(HV_PROF_LAYERNORM, s);
     rc = launch_layernorm(x, p.ln1_gamma, p.ln1_beta, ln1, max_rows, rows_dev, p.x_exp,
@@ -180,7 +181,7 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   g.mid_exp = p.msa_out_exp; g.res_exp = p.x_exp; g.out_exp = p.ffn_x_exp;
   {
     ProfScope ps(HV_PROF_GEMM_PROJ, s);
-    rc = launch_gemm(g, A_ROWS, HV_EPI_RESIDUAL, s);
+    rc = launch_block_gemm(BG_PROJ, g, nullptr, s);
   }
   if (rc) return rc;
 
@@ -208,7 +209,7 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   g.shift_a = p.ffn_out_exp - (p.hidden_out_exp + p.w2_exp);
   g.mid_exp = p.ffn_out_exp; g.res_exp = p.ffn_x_exp; g.out_exp = p.out_exp;
   ProfScope ps(HV_PROF_GEMM_FFN2, s);
-  return launch_gemm(g, A_ROWS, HV_EPI_RESIDUAL, s);
+  return launch_block_gemm(BG_FFN2, g, nullptr, s);
 }
 
 static bool exp_ok(int e) { return e >= -32 && e <= 31; }

@@ -27,6 +27,7 @@ enum { EPI_I8 = HV_EPI_I8, EPI_I32 = HV_EPI_I32, EPI_GELU = HV_EPI_GELU,
        EPI_RES = HV_EPI_RESIDUAL, EPI_PATCH = 4 };
 
 static constexpr int kPatchesPerImage = 196;
+static constexpr long long kGridCap = 256 * 8;  // workgroups: 256 CUs x 8 resident
 static constexpr int kTokens = 197;
 static constexpr int kImageBytes = 224 * 224 * 3;
 
@@ -52,9 +53,12 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int M = g.m_dev ? min(*g.m_dev, g.m) : g.m;
-  const int nb = blockIdx.x % n_blocks, mb = blockIdx.x / n_blocks;
   constexpr int BM = 64 * MT, BN = 64 * NT;
-  if (M <= 0 || mb * BM >= M) return;
+  const int live_tiles = ((M + BM - 1) / BM) * n_blocks;
+  // Grid-stride over output tiles: the grid is sized for the chip, not for
+  // the largest possible M, so pruned batches launch no idle workgroups.
+  for (int tile_id = blockIdx.x; tile_id < live_tiles; tile_id += gridDim.x) {
+  const int nb = tile_id % n_blocks, mb = tile_id / n_blocks;
   const int m0 = mb * BM + wm * 32 * MT;
   const int n32t = (g.n + 31) >> 5;
   const int ntile0 = (nb * BN >> 5) + wn * NT;
@@ -239,10 +243,11 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   }
+  }  // tile loop
 }
 
 // Shared host-side set-up of the int32 epilogue preconditions.
-static void epilogue_limits(GemmArgs &g, int epi) {
+void epilogue_limits_pub(GemmArgs &g, int epi) {
   const long long acc_max = (long long)g.k * 128 * 128;  // |A W| bound (int8 x int8)
   const long long lim = (1ll << 30) - 1 - acc_max;
   g.acc_lim = lim > 0 ? (int)lim : -1;
@@ -265,9 +270,9 @@ static int run(const GemmArgs &g, hipStream_t s) {
   constexpr int BM = 64 * MT, BN = 64 * NT;
   const int n_blocks = (g.n + BN - 1) / BN;
   const long long m_blocks = (g.m + BM - 1) / BM;
-  const long long grid = m_blocks * n_blocks;
+  long long grid = m_blocks * n_blocks;
   if (grid <= 0) return HV_OK;
-  if (grid > 0x7fffffff) return fail(HV_EVALUE, "gemm grid too large");
+  if (grid > kGridCap) grid = kGridCap;
   hipLaunchKernelGGL((k_gemm<MT, NT, EPI, AMODE, KTC>), dim3((unsigned)grid), dim3(256), 0, s,
                      g, n_blocks);
   return check_hip(hipGetLastError(), "k_gemm launch");
@@ -301,7 +306,7 @@ static int dispatch_k(const GemmArgs &g, int a_mode, hipStream_t s) {
 
 int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
   GemmArgs g = g_in;
-  epilogue_limits(g, epi);
+  epilogue_limits_pub(g, epi);
   if (g.k <= 0 || g.k % 32) return fail(HV_EVALUE, "gemm: K=%d must be a positive multiple of 32", g.k);
   if (g.n <= 0) return fail(HV_EVALUE, "gemm: N=%d must be positive", g.n);
   if (g.m < 0) return fail(HV_EVALUE, "gemm: M=%d must be non-negative", g.m);
@@ -345,8 +350,8 @@ int launch_patch_embed(const hv_patch_dev &p, const int8_t *images, int batch, i
   g.mid_exp = p.activation_exp;
   g.res_exp = p.pos_exp;
   g.out_exp = p.tokens_exp;
-  epilogue_limits(g, EPI_PATCH);
-  int rc = run<1, 3, EPI_PATCH, A_PATCH, 24>(g, s);
+  g.lda = 0;
+  int rc = launch_block_gemm(BG_PATCH, g, nullptr, s);
   if (rc) return rc;
   hipLaunchKernelGGL(k_cls_rows, dim3(batch), dim3(192), 0, s, p.cls, p.pos, x, p.cls_exp,
                      p.pos_exp, p.tokens_exp);

@@ -36,6 +36,20 @@ struct GemmArgs {
 };
 
 int launch_gemm(const GemmArgs &g, int a_mode, int epilogue, hipStream_t s);
+// Fills acc_lim / narrow_ok / da / db / os of the int32 epilogue paths.
+void epilogue_limits_pub(GemmArgs &g, int epilogue);
+
+// LayerNorm parameters for the fused prologue of the persistent GEMM.
+struct LnArgs {
+  const int8_t *gamma, *beta;
+  int8_t *out;  // optional copy of the normalised rows (checkpoints)
+  int x_exp, g_exp, b_exp, out_exp;
+  int gs, bs, os, fast_norm, fast_align;  // derived by the launcher
+};
+
+// Per-token GEMMs of the block on the persistent kernel (hv_gemm_p.hip).
+enum { BG_QKV = 0, BG_PROJ = 1, BG_FFN1 = 2, BG_FFN2 = 3, BG_PATCH = 4 };
+int launch_block_gemm(int which, const GemmArgs &g, const LnArgs *ln, hipStream_t s);
 
 // Patch embedding (transformer.patch_embedding): A rows are gathered
 // patches of NHWC 224x224x3 images, epilogue adds the position rows, and the

@@ -25,9 +25,10 @@ __global__ __launch_bounds__(256) void k_layernorm(const int8_t *__restrict__ x,
                                                    int g_exp, int b_exp, int out_exp,
                                                    uint8_t *neg_var) {
   const int sub = threadIdx.x & 15;  // lane within the row group
-  const int row = blockIdx.x * 16 + (threadIdx.x >> 4);
   const int R = rows_dev ? min(*rows_dev, rows) : rows;
-  if (row >= R) return;
+  // Grid-stride over rows: the grid is sized for the chip, not for the
+  // largest possible row count.
+  for (int row = blockIdx.x * 16 + (threadIdx.x >> 4); row < R; row += gridDim.x * 16) {
   const int *xr = reinterpret_cast<const int *>(x + (size_t)row * 192) + sub * 3;
   int w[3] = {xr[0], xr[1], xr[2]};
   int xv[12];
@@ -89,6 +90,7 @@ __global__ __launch_bounds__(256) void k_layernorm(const int8_t *__restrict__ x,
   yr[1] = out[1];
   yr[2] = out[2];
   if (neg_var && sub == 0) neg_var[row] = neg ? 1 : 0;
+  }  // row loop
 }
 
 int launch_layernorm(const int8_t *x, const int8_t *g, const int8_t *b, int8_t *y, int rows,
@@ -102,7 +104,8 @@ int launch_layernorm(const int8_t *x, const int8_t *g, const int8_t *b, int8_t *
   const int common = (g_exp - 16) < b_exp ? (g_exp - 16) : b_exp;
   const bool fast_norm = x_exp <= -1;
   const bool fast_align = (g_exp - 16 - common) <= 30 && (b_exp - common) <= 54;
-  const dim3 grid((rows + 15) / 16), block(256);
+  const int blocks = (rows + 15) / 16;
+  const dim3 grid(blocks < 256 * 8 ? blocks : 256 * 8), block(256);
   if (fast_norm && fast_align)
     hipLaunchKernelGGL((k_layernorm<true, true>), grid, block, 0, s, x, g, b, y, rows, rows_dev,
                        x_exp, g_exp, b_exp, out_exp, neg_var);
