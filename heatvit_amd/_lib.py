@@ -14,7 +14,7 @@ HV_OK, HV_EVALUE, HV_EOVERFLOW, HV_EHIP = 0, -2, -3, -4
 HV_PRIM_REQUANT, HV_PRIM_GELU, HV_PRIM_PLAN, HV_PRIM_RSA = 0, 1, 2, 3
 HV_EPI_I8, HV_EPI_I32, HV_EPI_GELU, HV_EPI_RESIDUAL = 0, 1, 2, 3
 HV_A_ROWS, HV_A_GATHER = 0, 1
-ABI_VERSION = 1
+ABI_VERSION = 2
 PROF_CLASSES = ("patch", "layernorm", "gemm_qkv", "attention", "gemm_proj", "gemm_ffn1",
                 "gemm_ffn2", "selector", "head", "other")
 

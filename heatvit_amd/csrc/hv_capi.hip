@@ -181,7 +181,7 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   g.mid_exp = p.msa_out_exp; g.res_exp = p.x_exp; g.out_exp = p.ffn_x_exp;
   {
     ProfScope ps(HV_PROF_GEMM_PROJ, s);
-    rc = launch_block_gemm(BG_PROJ, g, nullptr, s);
+    rc = launch_gemm(g, A_ROWS, HV_EPI_RESIDUAL, s);
   }
   if (rc) return rc;
 
@@ -209,7 +209,7 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   g.shift_a = p.ffn_out_exp - (p.hidden_out_exp + p.w2_exp);
   g.mid_exp = p.ffn_out_exp; g.res_exp = p.ffn_x_exp; g.out_exp = p.out_exp;
   ProfScope ps(HV_PROF_GEMM_FFN2, s);
-  return launch_block_gemm(BG_FFN2, g, nullptr, s);
+  return launch_gemm(g, A_ROWS, HV_EPI_RESIDUAL, s);
 }
 
 static bool exp_ok(int e) { return e >= -32 && e <= 31; }
@@ -234,7 +234,7 @@ extern "C" {
 
 const char *hv_last_error(void) { return g_err; }
 
-int hv_abi_version(void) { return 1; }
+int hv_abi_version(void) { return 2; }
 
 int hv_eval_primitive(int op, const int64_t *in, int64_t *out, int64_t n, int a, int b, int c,
                       hv_stream_t stream) {

@@ -126,42 +126,41 @@ __device__ __forceinline__ int align_add_pre(int a, int b, int da, int db, int o
 
 // ---------------------------------------------------------------- nonlinear.py
 
-// floor(num / den) for num < 2^40 and 2^16 <= den < 2^24 with a quotient
-// below 2^17: single-precision reciprocal estimate (error well below one
-// unit) and one exact integer correction step.
-__device__ __forceinline__ unsigned udiv_q17(u64 num, unsigned den) {
-  float est = (float)num * __builtin_amdgcn_rcpf((float)den);
-  unsigned q = (unsigned)est;
-  i64 r = (i64)num - (i64)q * (i64)den;
-  if (r < 0) q -= 1;
-  else if (r >= (i64)den) q += 1;
-  return q;
-}
-
 // gelu (nonlinear.py:60-80), ShiftGELU on Q8.16.  Domain: the 24-bit signed
 // range, which every call site guarantees (requant(..., -16, 24) first).
+// Everything stays in 32-bit lanes:
+//  * |ip2| < 2^25, so q = |ip2| >> 16 < 2^9; ib < 2^17 makes ib >> min(q, 31)
+//    zero for every q > 16, and ib << min(q, 8) >= 2^24 exceeds the cap for
+//    every q > 7, so both branch conditions become clamps;
+//  * e <= 2^23 - 1 gives den < 2^24 and sig < 2^16 - 500 (sig -> 2^16 only
+//    as e -> inf); the quotient estimate from the float reciprocal is within
+//    one of sig, and its remainder, below 2^25 in magnitude, is exact in
+//    wrapping 32-bit arithmetic, so one correction step finishes the division;
+//  * |x| * sig < 2^39: with |x| = ah * 2^16 + al (ah < 2^7) the rounded shift
+//    is ah * sig + ((al * sig + 2^15) >> 16), two 24-bit products, and its
+//    magnitude stays below |x| < 2^23, so the 24-bit saturation never acts.
 __device__ __forceinline__ int gelu_q16(int x) {
   const int ip = x + (x >> 1) + (x >> 3) + (x >> 4);
   const int ip2 = ip + (ip >> 1) - (ip >> 4);
-  const int a = ip2 < 0 ? -ip2 : ip2;
-  const int q = a >> 16, r = a & 0xFFFF;
-  const int frac = (r * 11 + 15) >> 4;
-  int e;
+  const unsigned a = (unsigned)(ip2 < 0 ? -ip2 : ip2);
+  const unsigned q = a >> 16, r = a & 0xFFFFu;
+  const unsigned frac = (__umul24(r, 11u) + 15u) >> 4;
+  unsigned e;
   if (ip2 < 0) {
-    e = q <= 16 ? ((65536 - frac) >> q) : 0;
+    e = (65536u - frac) >> (q < 31u ? q : 31u);
   } else {
-    const int cap = (1 << 23) - 1;
-    if (q <= 7) {
-      e = (65536 + frac) << q;
-      e = e > cap ? cap : e;
-    } else {
-      e = cap;
-    }
+    const unsigned sh = (65536u + frac) << (q < 8u ? q : 8u);
+    e = sh < (1u << 23) - 1 ? sh : (1u << 23) - 1;
   }
-  const unsigned den = 65536u + (unsigned)e;
-  const u64 num = ((u64)(unsigned)e << 16) + (den >> 1);
-  const unsigned sig = udiv_q17(num, den);
-  return (int)sat_bits(rsa_pos((i64)x * (i64)sig, 16), 24);
+  const unsigned den = 65536u + e;
+  const float est = (float)e * 65536.0f * __builtin_amdgcn_rcpf((float)den) + 0.5f;
+  unsigned sig = (unsigned)est;
+  const int rem = (int)((e << 16) + (den >> 1) - __umul24(sig, den));
+  sig = rem < 0 ? sig - 1 : (rem >= (int)den ? sig + 1 : sig);
+  const unsigned ax = (unsigned)(x < 0 ? -x : x);
+  const unsigned y = __umul24(ax >> 16, sig) +
+                     ((__umul24(ax & 0xFFFFu, sig) + 32768u) >> 16);
+  return x < 0 ? -(int)y : (int)y;
 }
 
 // requant(gelu(requant(v, src, -16, 24)), -16, dst, 8): the GEMM+GELU

@@ -1,16 +1,27 @@
 // hv_gemm.hip -- int8 GEMM on CDNA4 MFMA with the golden model's fused
 // writebacks (gemm.gemm_numpy + gemm.gemm_writeback, gemm.py:93-139).
 //
-// Tiling: a 256-thread workgroup owns a (64*MT) x (64*NT) output tile; its
-// four wavefronts form a 2x2 grid, each computing MT x NT tiles of 32x32
-// with v_mfma_i32_32x32x32_i8 (int32 accumulation is exact: |acc| <=
-// K*128*128 < 2^31 for K <= 131071, so gemm_numpy's overflow check cannot
-// fire).  A rows are read straight from HBM/L2 as 16-byte lane fragments;
-// weights come pre-packed in MFMA operand order ("mfma32", see
-// include/heatvit_hip.h) so every B fragment load is one coalesced 1 KiB
-// wavefront read.  The K loop is software-pipelined one step deep.
+// Orientation: every wavefront computes C^T tiles, W^T A^T, with
+// v_mfma_i32_32x32x32_i8 taking the packed weight fragment as its first
+// operand and the activation rows as its second.  The "mfma32" packing
+// (include/heatvit_hip.h) permutes the 32 columns of each weight tile so
+// that result lane l holds, for token row l%32, the 16 contiguous output
+// channels 16*(l/32) .. +15 of the tile.  The whole epilogue therefore runs
+// in registers: one 16-byte residual load and one 16-byte store per lane
+// and tile, four 16-byte bias loads per column tile, no LDS round trip.
+// int32 accumulation is exact: |acc| <= K*128*128 < 2^31 for K <= 131071,
+// so gemm_numpy's overflow check cannot fire.
 //
-// Epilogues (per output element v = acc + bias, int64):
+// Tiling: a 256-thread workgroup is a WM x (4/WM) grid of wavefronts, each
+// owning MT x NT 32x32 tiles.  Workgroups stride over the output tiles of
+// the live rows (row count read on the device); consecutive tiles of one
+// row block (its column blocks) go to the same XCD, so the row block's A
+// bytes are fetched into one L2.  For K = 192 all operand fragments of a
+// tile are loaded before the first MFMA (one memory latency per tile); for
+// K = 768 the loads run in double-buffered chunks of four K steps, and the
+// epilogue's bias and residual loads are issued with the first chunk.
+//
+// Epilogues (per output element v = acc + bias):
 //   EPI_I8/I32   requant(v, src, dst, 8|32)                     gemm.py:123-139
 //   EPI_GELU     requant(gelu(requant(v, src, -16, 24)), -16, dst, 8)
 //                                                    transformer.py:349-358
@@ -18,6 +29,11 @@
 //                                                    transformer.py:96-101
 //   EPI_PATCH    t = requant(v, img+w, act, 8); out = align_add(t, pos[p+1])
 //                into row b*197 + 1 + p                transformer.py:120-145
+// The int32 form of each epilogue is taken when the launch's shifts lie in
+// [1, 30], the align-add shifts are at most 21, and every bias of the
+// wavefront's columns satisfies |bias| <= 2^30 - 1 - K*2^14 (so v, the
+// aligned sums and every rounding addend stay below 2^31); the other cases
+// call the exact 64/128-bit form, kept out of line.
 #include "hv_device.h"
 #include "hv_internal.h"
 
@@ -27,9 +43,9 @@ enum { EPI_I8 = HV_EPI_I8, EPI_I32 = HV_EPI_I32, EPI_GELU = HV_EPI_GELU,
        EPI_RES = HV_EPI_RESIDUAL, EPI_PATCH = 4 };
 
 static constexpr int kPatchesPerImage = 196;
-static constexpr long long kGridCap = 256 * 8;  // workgroups: 256 CUs x 8 resident
 static constexpr int kTokens = 197;
 static constexpr int kImageBytes = 224 * 224 * 3;
+static constexpr int kGridCap = 256 * 8;  // workgroups: 256 CUs x 8 resident
 
 template <int AMODE>
 __device__ __forceinline__ const int8_t *a_row(const GemmArgs &g, int r) {
@@ -48,210 +64,305 @@ __device__ __forceinline__ const int8_t *patch_ptr(const int8_t *images, int r, 
   return images + (size_t)b * kImageBytes + ((pr * 16 + in_row) * 224 + pc * 16) * 3 + rem;
 }
 
-template <int MT, int NT, int EPI, int AMODE, int KTC>
+// requant for |v| < 2^30 and shift s in [1, 30] with rnd = 2^(s-1):
+// round_shift_away is (v + rnd - (v < 0)) >> s, then saturate.
+__device__ __forceinline__ int rq(int v, int rnd, int s, int lo, int hi) {
+  const int r = (v + rnd + (v >> 31)) >> s;
+  return min(max(r, lo), hi);
+}
+
+// Exact epilogue of one element (64/128-bit), out of line.  Returns
+// {output, requantised product (residual forms)}.
+typedef int v2i __attribute__((ext_vector_type(2)));
+__device__ __noinline__ v2i epi_exact(int epi, int acc, int bias, int res, int shift_a,
+                                      int shift_b, int da, int db, int os) {
+  const i64 v = (i64)acc + bias;
+  if (epi == EPI_I8) return v2i{(int)requant_shift(v, shift_a, 8), 0};
+  if (epi == EPI_I32) return v2i{(int)requant_shift(v, shift_a, 32), 0};
+  if (epi == EPI_GELU) return v2i{gelu_post(v, shift_a, shift_b), 0};
+  const int t = (int)requant_shift(v, shift_a, 8);
+  return v2i{epi == EPI_RES ? align_add_pre(res, t, da, db, os, false)
+                            : align_add_pre(t, res, da, db, os, false),
+             t};
+}
+
+__device__ __forceinline__ int pack4(int a, int b, int c, int d) {
+  return (int)((unsigned)(a & 0xFF) | ((unsigned)(b & 0xFF) << 8) | ((unsigned)(c & 0xFF) << 16) |
+               ((unsigned)d << 24));
+}
+
+template <int MT, int NT, int WM, int EPI, int AMODE, int KTC, bool FAST>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
+  constexpr int WN = 4 / WM;
+  constexpr int BM = 32 * MT * WM;  // rows per tile
+  constexpr int BT = NT * WN;       // 32-column weight tiles per tile
+  constexpr bool RESLIKE = EPI == EPI_RES || EPI == EPI_PATCH;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave - wm * WN;
+  const int h = lane >> 5, l32 = lane & 31;
   const int M = g.m_dev ? min(*g.m_dev, g.m) : g.m;
-  constexpr int BM = 64 * MT, BN = 64 * NT;
-  const int live_tiles = ((M + BM - 1) / BM) * n_blocks;
-  // Grid-stride over output tiles: the grid is sized for the chip, not for
-  // the largest possible M, so pruned batches launch no idle workgroups.
-  for (int tile_id = blockIdx.x; tile_id < live_tiles; tile_id += gridDim.x) {
-  const int nb = tile_id % n_blocks, mb = tile_id / n_blocks;
-  const int m0 = mb * BM + wm * 32 * MT;
+  if (M <= 0) return;
+  const int T = ((M + BM - 1) / BM) * n_blocks;
+  const int T8 = (T + 7) >> 3;
+  const int KT = KTC ? KTC : (g.k >> 5);
   const int n32t = (g.n + 31) >> 5;
-  const int ntile0 = (nb * BN >> 5) + wn * NT;
-  const int KT = KTC ? KTC : (g.k >> 5);  // K/32 steps; compile-time for K = 192, 768
-  const int khalf = (lane >> 5) * 16;
+  const int rnd_a = FAST ? 1 << (g.shift_a - 1) : 0;
+  const int rnd_b = FAST && EPI == EPI_GELU ? 1 << (g.shift_b - 1) : 0;
+  const int rnd_o = FAST && RESLIKE ? 1 << (g.os - 1) : 0;
 
-  int arow[MT];
-  const int8_t *ap[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    int r = m0 + mt * 32 + (lane & 31);
-    r = r < M ? r : M - 1;
-    arow[mt] = r;
-    if (AMODE != A_PATCH) ap[mt] = a_row<AMODE>(g, r) + khalf;
-  }
-  const int8_t *bp[NT];
-  bool nvalid[NT];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int t = ntile0 + nt;
-    nvalid[nt] = t < n32t;
-    bp[nt] = g.b + ((size_t)(t < n32t ? t : n32t - 1) * KT) * 1024 + lane * 16;
-  }
+  // The grid is a multiple of 8, so t & 7 (the XCD) is fixed per workgroup
+  // and XCD x works through logical tiles [x*T8, (x+1)*T8).
+  for (int t = blockIdx.x; t < 8 * T8; t += gridDim.x) {
+    const int L = (t & 7) * T8 + (t >> 3);
+    if (L >= T) continue;
+    const int mb = L / n_blocks, nb = L - mb * n_blocks;
+    const int r0 = mb * BM + wm * 32 * MT;
+    const int ct0 = nb * BT + wn * NT;
 
-  v16i acc[MT][NT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v16i{0};
-
-  v4i a_cur[MT], b_cur[NT], a_nxt[MT], b_nxt[NT];
-  auto load = [&](int kt, v4i *av, v4i *bv) {
+    int arow[MT];
+    const int8_t *ap[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const int8_t *p = AMODE == A_PATCH ? patch_ptr(g.a, arow[mt], kt * 32 + khalf)
-                                         : ap[mt] + kt * 32;
-      av[mt] = *reinterpret_cast<const v4i *>(p);
+      const int r = min(r0 + mt * 32 + l32, M - 1);
+      arow[mt] = r;
+      if (AMODE != A_PATCH) ap[mt] = a_row<AMODE>(g, r) + 16 * h;
     }
+    const int8_t *bp[NT];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) bv[nt] = *reinterpret_cast<const v4i *>(bp[nt] + kt * 1024);
-  };
-  auto step = [&](int kt) {
-    if (kt + 1 < KT) load(kt + 1, a_nxt, b_nxt);
+    for (int nt = 0; nt < NT; ++nt)
+      bp[nt] = g.b + (size_t)min(ct0 + nt, n32t - 1) * KT * 1024 + lane * 16;
+
+    auto load_a = [&](int mt, int kt) -> v4i {
+      const int8_t *p = AMODE == A_PATCH ? patch_ptr(g.a, arow[mt], kt * 32 + 16 * h)
+                                         : ap[mt] + kt * 32;
+      return *reinterpret_cast<const v4i *>(p);
+    };
+    auto load_b = [&](int nt, int kt) -> v4i {
+      return *reinterpret_cast<const v4i *>(bp[nt] + kt * 1024);
+    };
+
+    // Epilogue operands that do not depend on the product.
+    v4i bias4[NT][4];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int c0 = (ct0 + nt) * 32 + 16 * h;
+      if (g.bias && c0 + 16 <= g.n) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bias4[nt][q] = *reinterpret_cast<const v4i *>(g.bias + c0 + 4 * q);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          bias4[nt][j >> 2][j & 3] = g.bias && c0 + j < g.n ? g.bias[c0 + j] : 0;
+      }
+    }
+    v4i res4[MT][NT];
+    if constexpr (RESLIKE) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const int c0 = (ct0 + nt) * 32 + 16 * h;
+          const int8_t *rp;
+          if (EPI == EPI_RES) {
+            rp = g.res + (size_t)arow[mt] * g.ldr + c0;
+          } else {
+            const int p = arow[mt] % kPatchesPerImage;
+            rp = g.pos + (size_t)(p + 1) * 192 + c0;
+          }
+          if (g.vec_res && c0 + 16 <= g.n) {
+            res4[mt][nt] = *reinterpret_cast<const v4i *>(rp);
+          } else {
+            int w[4] = {0, 0, 0, 0};
+            for (int j = 0; j < 16 && c0 + j < g.n; ++j) w[j >> 2] |= ((int)rp[j] & 0xFF) << (8 * (j & 3));
+            res4[mt][nt] = v4i{w[0], w[1], w[2], w[3]};
+          }
+        }
+    }
+
+    v16i acc[MT][NT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-        acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_cur[mt], b_cur[nt], acc[mt][nt],
-                                                             0, 0, 0);
-    if (kt + 1 < KT) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) a_cur[mt] = a_nxt[mt];
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) b_cur[nt] = b_nxt[nt];
-    }
-  };
-  load(0, a_cur, b_cur);
-  if constexpr (KTC > 0) {
-#pragma unroll
-    for (int kt = 0; kt < KTC; ++kt) step(kt);
-  } else {
-    for (int kt = 0; kt < KT; ++kt) step(kt);
-  }
+      for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v16i{0};
 
-  // Epilogue.  Each wavefront stages one 32x32 int32 accumulator tile at a
-  // time in its LDS slice (MFMA layout: lane l holds column l%32 and, in
-  // element i, row 8*(i/4) + 4*(l/32) + i%4), then lane l finishes row l/2,
-  // columns 16*(l%2) + 4*g .. +3 for g = 0..3: four outputs per group with
-  // one bias/residual vector load and one packed store.  With |acc| <=
-  // K*2^14 and |bias| <= acc_lim, v = acc + bias stays below 2^30 and the
-  // epilogue's requants are exact in int32 (requant_i32); other columns take
-  // the 64-bit forms.
-  __shared__ int stage[4][32 * 36];
-  int *T = stage[wave];
-  const int er = lane >> 1, ec0 = (lane & 1) * 16;
+    if constexpr (KTC > 0 && KTC <= 8) {
+      // Every fragment of the tile in flight at once.
+      v4i af[MT][KTC], bf[NT][KTC];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
+      for (int kt = 0; kt < KTC; ++kt) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) af[mt][kt] = load_a(mt, kt);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) bf[nt][kt] = load_b(nt, kt);
+      }
+#pragma unroll
+      for (int kt = 0; kt < KTC; ++kt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[nt][kt], af[mt][kt],
+                                                                 acc[mt][nt], 0, 0, 0);
+    } else if constexpr (KTC > 8) {
+      // Double-buffered chunks of KC steps.
+      constexpr int KC = 4, NC = KTC / KC;
+      static_assert(KTC % (2 * KC) == 0, "K steps must split into chunk pairs");
+      v4i a0[MT][KC], b0[NT][KC], a1[MT][KC], b1[NT][KC];
+      auto load_chunk = [&](int c, v4i (*av)[KC], v4i (*bv)[KC]) {
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) av[mt][j] = load_a(mt, c * KC + j);
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) bv[nt][j] = load_b(nt, c * KC + j);
+        }
+      };
+      auto mma_chunk = [&](v4i (*av)[KC], v4i (*bv)[KC]) {
+#pragma unroll
+        for (int j = 0; j < KC; ++j)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+              acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bv[nt][j], av[mt][j],
+                                                                   acc[mt][nt], 0, 0, 0);
+      };
+      load_chunk(0, a0, b0);
+#pragma unroll
+      for (int c = 0; c < NC; c += 2) {
+        load_chunk(c + 1, a1, b1);
+        mma_chunk(a0, b0);
+        if (c + 2 < NC) load_chunk(c + 2, a0, b0);
+        mma_chunk(a1, b1);
+      }
+    } else {
+      // Runtime K: one step of prefetch.
+      v4i ac[MT], bc[NT], an[MT], bn[NT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) ac[mt] = load_a(mt, 0);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) bc[nt] = load_b(nt, 0);
+      for (int kt = 0; kt < KT; ++kt) {
+        if (kt + 1 < KT) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) an[mt] = load_a(mt, kt + 1);
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) bn[nt] = load_b(nt, kt + 1);
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bc[nt], ac[mt], acc[mt][nt], 0, 0, 0);
+        if (kt + 1 < KT) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) ac[mt] = an[mt];
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) bc[nt] = bn[nt];
+        }
+      }
+    }
+
+    // Epilogue: lane l finishes row r0 + 32*mt + l%32, channels c0 .. c0+15.
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
+      const int c0 = (ct0 + nt) * 32 + 16 * h;
+      bool narrow = FAST;
+      if (FAST) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        T[(8 * (i >> 2) + 4 * (lane >> 5) + (i & 3)) * 36 + (lane & 31)] = acc[mt][nt][i];
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const int row = m0 + mt * 32 + er;
-      if (nvalid[nt] && row < M) {
-#pragma unroll 1
-        for (int grp = 0; grp < 4; ++grp) {
-          const int cl = ec0 + 4 * grp;
-          const int col = (ntile0 + nt) * 32 + cl;
-          if (col >= g.n) break;
-          const v4i a4 = *reinterpret_cast<const v4i *>(&T[er * 36 + cl]);
-          const bool full = col + 3 < g.n;
-          int bias[4] = {0, 0, 0, 0};
-          if (g.bias) {
-            if (full && (g.n & 3) == 0) {
-              const v4i b4 = *reinterpret_cast<const v4i *>(g.bias + col);
-              bias[0] = b4[0]; bias[1] = b4[1]; bias[2] = b4[2]; bias[3] = b4[3];
-            } else {
+        for (int j = 0; j < 16; ++j) {
+          const int b = bias4[nt][j >> 2][j & 3];
+          narrow = narrow && b <= g.acc_lim && b >= -g.acc_lim;
+        }
+      }
+      // Uniform per wavefront: the int32 form only when every lane qualifies.
+      const bool fast = FAST && __all(narrow);
 #pragma unroll
-              for (int j = 0; j < 4; ++j) bias[j] = col + j < g.n ? g.bias[col + j] : 0;
-            }
-          }
-          int rv[4] = {0, 0, 0, 0};
-          if (EPI == EPI_RES) {
-            const int8_t *rp = g.res + (size_t)row * g.ldr + col;
+      for (int mt = 0; mt < MT; ++mt) {
+        const int row = r0 + mt * 32 + l32;
+        if (row >= M || c0 >= g.n) continue;
+        size_t orow = (size_t)row;
+        if (EPI == EPI_PATCH) {
+          const int b = row / kPatchesPerImage;
+          orow = (size_t)b * kTokens + 1 + (row - b * kPatchesPerImage);
+        }
+        int o[16], mid[16];
+        if (fast) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) rv[j] = col + j < g.n ? rp[j] : 0;
-          }
-          size_t orow = (size_t)row;
-          if (EPI == EPI_PATCH) {
-            const int b = row / kPatchesPerImage, p = row - b * kPatchesPerImage;
-            orow = (size_t)b * kTokens + 1 + p;
-            const int8_t *pp = g.pos + (size_t)(p + 1) * 192 + col;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) rv[j] = pp[j];
-          }
-          int out[4], aux[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const bool n32 = g.narrow_ok && bias[j] <= g.acc_lim && bias[j] >= -g.acc_lim;
-            const int v32 = a4[j] + (n32 ? bias[j] : 0);
-            const i64 v = (i64)a4[j] + bias[j];
-            if (EPI == EPI_I32) {
-              out[j] = (int)requant_shift(v, g.shift_a, 32);
-            } else if (EPI == EPI_I8) {
-              out[j] = n32 ? requant_i32(v32, g.shift_a, -128, 127)
-                           : (int)requant_shift(v, g.shift_a, 8);
+          for (int j = 0; j < 16; ++j) {
+            const int v = acc[mt][nt][j] + bias4[nt][j >> 2][j & 3];
+            if (EPI == EPI_I8) {
+              o[j] = rq(v, rnd_a, g.shift_a, -128, 127);
             } else if (EPI == EPI_GELU) {
-              if (n32) {
-                const int q = requant_i32(v32, g.shift_a, -(1 << 23), (1 << 23) - 1);
-                out[j] = requant_i32(gelu_q16(q), g.shift_b, -128, 127);
-              } else {
-                out[j] = gelu_post(v, g.shift_a, g.shift_b);
-              }
-            } else {  // EPI_RES, EPI_PATCH
-              const int t = n32 ? requant_i32(v32, g.shift_a, -128, 127)
-                                : (int)requant_shift(v, g.shift_a, 8);
-              aux[j] = t;
-              out[j] = EPI == EPI_RES ? align_add_pre(rv[j], t, g.da, g.db, g.os, n32)
-                                      : align_add_pre(t, rv[j], g.da, g.db, g.os, n32);
+              const int q = rq(v, rnd_a, g.shift_a, -(1 << 23), (1 << 23) - 1);
+              o[j] = rq(gelu_q16(q), rnd_b, g.shift_b, -128, 127);
+            } else if (RESLIKE) {
+              const int t8 = rq(v, rnd_a, g.shift_a, -128, 127);
+              const int r8 = (int)(int8_t)(res4[mt][nt][j >> 2] >> (8 * (j & 3)));
+              const int s = EPI == EPI_RES ? r8 * (1 << g.da) + t8 * (1 << g.db)
+                                           : t8 * (1 << g.da) + r8 * (1 << g.db);
+              mid[j] = t8;
+              o[j] = rq(s, rnd_o, g.os, -128, 127);
             }
           }
-          if (EPI == EPI_I32) {
-            int32_t *cp = reinterpret_cast<int32_t *>(g.c) + orow * g.ldc + col;
-            if (full && ((g.ldc & 3) == 0)) {
-              *reinterpret_cast<v4i *>(cp) = v4i{out[0], out[1], out[2], out[3]};
-            } else {
+        } else {
 #pragma unroll
-              for (int j = 0; j < 4; ++j)
-                if (col + j < g.n) cp[j] = out[j];
-            }
+          for (int j = 0; j < 16; ++j) {
+            const int r8 = RESLIKE ? (int)(int8_t)(res4[mt][nt][j >> 2] >> (8 * (j & 3))) : 0;
+            const v2i r = epi_exact(EPI, acc[mt][nt][j], bias4[nt][j >> 2][j & 3], r8, g.shift_a,
+                                    g.shift_b, g.da, g.db, g.os);
+            o[j] = r[0];
+            mid[j] = r[1];
+          }
+        }
+        const bool full = g.vec_out && c0 + 16 <= g.n;
+        if (EPI == EPI_I32) {
+          int32_t *cp = reinterpret_cast<int32_t *>(g.c) + orow * g.ldc + c0;
+          if (full) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              *reinterpret_cast<v4i *>(cp + 4 * q) = v4i{o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
           } else {
-            int8_t *cp = reinterpret_cast<int8_t *>(g.c) + orow * g.ldc + col;
-            const int word = (out[0] & 0xFF) | ((out[1] & 0xFF) << 8) | ((out[2] & 0xFF) << 16) |
-                             ((out[3] & 0xFF) << 24);
-            if (full && ((g.ldc & 3) == 0)) {
-              *reinterpret_cast<int *>(cp) = word;
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+              if (c0 + j < g.n) cp[j] = o[j];
+          }
+        } else {
+          int8_t *cp = reinterpret_cast<int8_t *>(g.c) + orow * g.ldc + c0;
+          if (full) {
+            *reinterpret_cast<v4i *>(cp) = v4i{pack4(o[0], o[1], o[2], o[3]), pack4(o[4], o[5], o[6], o[7]),
+                                               pack4(o[8], o[9], o[10], o[11]),
+                                               pack4(o[12], o[13], o[14], o[15])};
+          } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+              if (c0 + j < g.n) cp[j] = (int8_t)o[j];
+          }
+          if (EPI == EPI_RES && g.aux) {
+            int8_t *xp = g.aux + orow * g.ldc + c0;
+            if (full) {
+              *reinterpret_cast<v4i *>(xp) =
+                  v4i{pack4(mid[0], mid[1], mid[2], mid[3]), pack4(mid[4], mid[5], mid[6], mid[7]),
+                      pack4(mid[8], mid[9], mid[10], mid[11]), pack4(mid[12], mid[13], mid[14], mid[15])};
             } else {
 #pragma unroll
-              for (int j = 0; j < 4; ++j)
-                if (col + j < g.n) cp[j] = (int8_t)out[j];
-            }
-            if (EPI == EPI_RES && g.aux) {
-              int8_t *xp = g.aux + (size_t)row * g.ldc + col;
-              const int aw = (aux[0] & 0xFF) | ((aux[1] & 0xFF) << 8) | ((aux[2] & 0xFF) << 16) |
-                             ((aux[3] & 0xFF) << 24);
-              if (full && ((g.ldc & 3) == 0)) {
-                *reinterpret_cast<int *>(xp) = aw;
-              } else {
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                  if (col + j < g.n) xp[j] = (int8_t)aux[j];
-              }
+              for (int j = 0; j < 16; ++j)
+                if (c0 + j < g.n) xp[j] = (int8_t)mid[j];
             }
           }
         }
       }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   }
-  }  // tile loop
 }
 
-// Shared host-side set-up of the int32 epilogue preconditions.
+// Host-side set-up of the epilogue preconditions.
 void epilogue_limits_pub(GemmArgs &g, int epi) {
   const long long acc_max = (long long)g.k * 128 * 128;  // |A W| bound (int8 x int8)
   const long long lim = (1ll << 30) - 1 - acc_max;
   g.acc_lim = lim > 0 ? (int)lim : -1;
-  g.narrow_ok = 1;
+  g.narrow_ok = g.acc_lim > 0;
+  g.da = g.db = g.os = 0;
   if (epi == EPI_RES || epi == EPI_PATCH) {
     // residual: align_add(res @ res_exp, t @ mid_exp -> out_exp);
     // patch:    align_add(t @ mid_exp, pos @ res_exp -> out_exp)
@@ -261,47 +372,60 @@ void epilogue_limits_pub(GemmArgs &g, int epi) {
     g.da = a_exp - c;
     g.db = b_exp - c;
     g.os = g.out_exp - c;
-    g.narrow_ok = g.da <= 21 && g.db <= 21;
   }
 }
 
-template <int MT, int NT, int EPI, int AMODE, int KTC = 0>
+static bool fast_epilogue(const GemmArgs &g, int epi) {
+  auto in = [](int s) { return s >= 1 && s <= 30; };
+  if (!g.narrow_ok || !in(g.shift_a)) return false;
+  switch (epi) {
+    case EPI_I8: return true;
+    case EPI_GELU: return in(g.shift_b);
+    case EPI_RES:
+    case EPI_PATCH: return g.da <= 21 && g.db <= 21 && in(g.os);
+    default: return false;
+  }
+}
+
+template <int MT, int NT, int WM, int EPI, int AMODE, int KTC>
 static int run(const GemmArgs &g, hipStream_t s) {
-  constexpr int BM = 64 * MT, BN = 64 * NT;
+  constexpr int BM = 32 * MT * WM, BN = 32 * NT * (4 / WM);
   const int n_blocks = (g.n + BN - 1) / BN;
-  const long long m_blocks = (g.m + BM - 1) / BM;
-  long long grid = m_blocks * n_blocks;
-  if (grid <= 0) return HV_OK;
+  const long long tiles = (long long)((g.m + BM - 1) / BM) * n_blocks;
+  if (tiles <= 0) return HV_OK;
+  long long grid = (tiles + 7) / 8 * 8;
   if (grid > kGridCap) grid = kGridCap;
-  hipLaunchKernelGGL((k_gemm<MT, NT, EPI, AMODE, KTC>), dim3((unsigned)grid), dim3(256), 0, s,
-                     g, n_blocks);
+  const bool fast = fast_epilogue(g, EPI);
+  if (fast)
+    hipLaunchKernelGGL((k_gemm<MT, NT, WM, EPI, AMODE, KTC, true>), dim3((unsigned)grid), dim3(256),
+                       0, s, g, n_blocks);
+  else
+    hipLaunchKernelGGL((k_gemm<MT, NT, WM, EPI, AMODE, KTC, false>), dim3((unsigned)grid),
+                       dim3(256), 0, s, g, n_blocks);
   return check_hip(hipGetLastError(), "k_gemm launch");
 }
 
-// Tile choice: N that is a multiple of 192 (QKV 576, FFN1 768, proj/FFN2
-// 192) uses 192-wide column blocks; other N (head 1000, tests) 128-wide.
-// Large-N GEMMs use 128-row tiles, N = 192 GEMMs 64-row tiles so the grid
-// still fills 256 CUs.
-template <int EPI, int AMODE, int KTC>
-static int dispatch_tiles(const GemmArgs &g, hipStream_t s) {
-  // The GELU epilogue needs more registers; 128x128 tiles keep it spill-free.
-  if (EPI == EPI_GELU && g.n > 192) return run<2, 2, EPI, AMODE, KTC>(g, s);
-  if (g.n % 192 == 0) {
-    if (g.n > 192) return run<2, 3, EPI, AMODE, KTC>(g, s);
-    return run<1, 3, EPI, AMODE, KTC>(g, s);
-  }
-  return run<1, 2, EPI, AMODE, KTC>(g, s);
-}
-
-// K = 192 (every GEMM but FFN2) and K = 768 (FFN2) get compile-time trip
-// counts; other K (tests, tails) take the runtime loop.
+// Tile shapes: 128x64 output tiles (two 32-row tiles per wavefront) for the
+// epilogues with few operations per element, 64x64 for GELU, whose
+// epilogue holds more registers.  K = 192 and K = 768 get compile-time K
+// loops; other K (the generic entry point) the runtime loop.
 template <int EPI>
-static int dispatch_k(const GemmArgs &g, int a_mode, hipStream_t s) {
-  if (a_mode == A_GATHER) return dispatch_tiles<EPI, A_GATHER, 0>(g, s);
+static int dispatch(const GemmArgs &g, int a_mode, hipStream_t s) {
+  if (a_mode == A_PATCH) {
+    if (EPI != EPI_PATCH || g.k != 768) return fail(HV_EVALUE, "gemm: bad patch GEMM");
+    return run<2, 1, 2, EPI_PATCH, A_PATCH, 24>(g, s);
+  }
+  if (EPI == EPI_PATCH) return fail(HV_EVALUE, "gemm: patch epilogue needs the patch gather");
+  if (a_mode == A_GATHER) return run<1, 1, 2, EPI, A_GATHER, 0>(g, s);
   if (a_mode != A_ROWS) return fail(HV_EVALUE, "gemm: bad A mode %d", a_mode);
-  if (g.k == 192) return dispatch_tiles<EPI, A_ROWS, 6>(g, s);
-  if (g.k == 768) return dispatch_tiles<EPI, A_ROWS, 24>(g, s);
-  return dispatch_tiles<EPI, A_ROWS, 0>(g, s);
+  if (EPI == EPI_GELU) {
+    if (g.k == 192) return run<1, 1, 2, EPI, A_ROWS, 6>(g, s);
+    if (g.k == 768) return run<1, 1, 2, EPI, A_ROWS, 24>(g, s);
+    return run<1, 1, 2, EPI, A_ROWS, 0>(g, s);
+  }
+  if (g.k == 192) return run<2, 1, 2, EPI, A_ROWS, 6>(g, s);
+  if (g.k == 768) return run<2, 1, 2, EPI, A_ROWS, 24>(g, s);
+  return run<1, 1, 2, EPI, A_ROWS, 0>(g, s);
 }
 
 int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
@@ -312,12 +436,22 @@ int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
   if (g.m < 0) return fail(HV_EVALUE, "gemm: M=%d must be non-negative", g.m);
   if (a_mode != A_PATCH && (g.lda % 16 || ((uintptr_t)g.a & 15)))
     return fail(HV_EVALUE, "gemm: A must be 16-byte aligned with lda %% 16 == 0");
+  if (a_mode == A_PATCH && ((uintptr_t)g.a & 15))
+    return fail(HV_EVALUE, "gemm: images must be 16-byte aligned");
+  if (g.bias && ((uintptr_t)g.bias & 15))
+    return fail(HV_EVALUE, "gemm: bias must be 16-byte aligned");
   if (g.k > 131071) return fail(HV_EOVERFLOW, "gemm: K=%d may overflow int32", g.k);
+  const int esz = epi == EPI_I32 ? 4 : 1;
+  g.vec_out = ((uintptr_t)g.c & 15) == 0 && (g.ldc * esz) % 16 == 0 &&
+              (!g.aux || ((uintptr_t)g.aux & 15) == 0);
+  if (epi == EPI_RES) g.vec_res = ((uintptr_t)g.res & 15) == 0 && g.ldr % 16 == 0;
+  if (epi == EPI_PATCH) g.vec_res = ((uintptr_t)g.pos & 15) == 0;
   switch (epi) {
-    case EPI_I8: return dispatch_k<EPI_I8>(g, a_mode, s);
-    case EPI_I32: return dispatch_k<EPI_I32>(g, a_mode, s);
-    case EPI_GELU: return dispatch_k<EPI_GELU>(g, a_mode, s);
-    case EPI_RES: return dispatch_k<EPI_RES>(g, a_mode, s);
+    case EPI_I8: return dispatch<EPI_I8>(g, a_mode, s);
+    case EPI_I32: return dispatch<EPI_I32>(g, a_mode, s);
+    case EPI_GELU: return dispatch<EPI_GELU>(g, a_mode, s);
+    case EPI_RES: return dispatch<EPI_RES>(g, a_mode, s);
+    case EPI_PATCH: return dispatch<EPI_PATCH>(g, a_mode, s);
     default: return fail(HV_EVALUE, "gemm: bad epilogue %d", epi);
   }
 }
@@ -335,7 +469,6 @@ __global__ void k_cls_rows(const int8_t *cls, const int8_t *pos, int8_t *x, int 
 int launch_patch_embed(const hv_patch_dev &p, const int8_t *images, int batch, int8_t *x,
                        hipStream_t s) {
   if (batch <= 0) return HV_OK;
-  if ((uintptr_t)images & 15) return fail(HV_EVALUE, "patch: images must be 16-byte aligned");
   GemmArgs g{};
   g.a = images;
   g.b = p.weight_p;
@@ -351,7 +484,7 @@ int launch_patch_embed(const hv_patch_dev &p, const int8_t *images, int batch, i
   g.res_exp = p.pos_exp;
   g.out_exp = p.tokens_exp;
   g.lda = 0;
-  int rc = launch_block_gemm(BG_PATCH, g, nullptr, s);
+  int rc = launch_gemm(g, A_PATCH, EPI_PATCH, s);
   if (rc) return rc;
   hipLaunchKernelGGL(k_cls_rows, dim3(batch), dim3(192), 0, s, p.cls, p.pos, x, p.cls_exp,
                      p.pos_exp, p.tokens_exp);

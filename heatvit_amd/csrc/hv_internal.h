@@ -31,25 +31,16 @@ struct GemmArgs {
   int res_exp, mid_exp, out_exp;
   // Filled by launch_gemm: int32 epilogue preconditions.
   int acc_lim;     // a column takes the int32 path when |bias| <= acc_lim
-  int narrow_ok;   // epilogue shifts allow int32 (residual: da, db <= 21)
+  int narrow_ok;   // acc_lim > 0
   int da, db, os;  // residual / patch align-add shifts
+  int vec_out;     // c (and aux) allow 16-byte row stores
+  int vec_res;     // res (or pos) allow 16-byte row loads
 };
 
+// epilogue: HV_EPI_* or 4 (patch: A_PATCH gather, position-row residual).
 int launch_gemm(const GemmArgs &g, int a_mode, int epilogue, hipStream_t s);
 // Fills acc_lim / narrow_ok / da / db / os of the int32 epilogue paths.
 void epilogue_limits_pub(GemmArgs &g, int epilogue);
-
-// LayerNorm parameters for the fused prologue of the persistent GEMM.
-struct LnArgs {
-  const int8_t *gamma, *beta;
-  int8_t *out;  // optional copy of the normalised rows (checkpoints)
-  int x_exp, g_exp, b_exp, out_exp;
-  int gs, bs, os, fast_norm, fast_align;  // derived by the launcher
-};
-
-// Per-token GEMMs of the block on the persistent kernel (hv_gemm_p.hip).
-enum { BG_QKV = 0, BG_PROJ = 1, BG_FFN1 = 2, BG_FFN2 = 3, BG_PATCH = 4 };
-int launch_block_gemm(int which, const GemmArgs &g, const LnArgs *ln, hipStream_t s);
 
 // Patch embedding (transformer.patch_embedding): A rows are gathered
 // patches of NHWC 224x224x3 images, epilogue adds the position rows, and the

@@ -14,10 +14,18 @@ from . import _lib
 from .params import BlockParams, HeatViTParams, PatchParams, SelectorParams, check_scale_exps
 
 
+# Position of output channel c (0..31) of a weight tile among the MFMA
+# operand rows: channel 16*h + 4*a + b sits at row 8*a + 4*h + b, so result
+# lane l of the transposed product holds channels 16*(l//32) .. +15.
+MFMA32_ROW_OF_CHANNEL = np.array([8 * ((c % 16) // 4) + 4 * (c // 16) + c % 4 for c in range(32)])
+MFMA32_CHANNEL_OF_ROW = np.argsort(MFMA32_ROW_OF_CHANNEL)
+
+
 def pack_mfma32(w):
     """Pack an int8 matrix W[K][N] (K % 32 == 0) into the mfma32 layout:
-    [ceil(N/32)][K/32][64 lanes][16 bytes], element (k, n) at lane
-    (n % 32) + 32 * ((k % 32) // 16), byte k % 16, zero-padded columns."""
+    [ceil(N/32)][K/32][64 lanes][16 bytes], element (k, n) at tile
+    (n // 32, k // 32), lane MFMA32_ROW_OF_CHANNEL[n % 32] + 32 * ((k % 32) // 16),
+    byte k % 16, zero-padded columns."""
     w = np.asarray(w, np.int8)
     k, n = w.shape
     if k % 32:
@@ -25,6 +33,7 @@ def pack_mfma32(w):
     n32 = -(-n // 32) * 32
     wp = np.zeros((k, n32), np.int8)
     wp[:, :n] = w
+    wp = wp.reshape(k, n32 // 32, 32)[:, :, MFMA32_CHANNEL_OF_ROW].reshape(k, n32)
     t = wp.reshape(k // 32, 2, 16, n32 // 32, 32).transpose(3, 0, 1, 4, 2)
     return np.ascontiguousarray(t).reshape(-1)
 
@@ -33,7 +42,8 @@ def unpack_mfma32(packed, k, n):
     """Inverse of pack_mfma32 (used by tests)."""
     n32 = -(-n // 32) * 32
     t = np.asarray(packed, np.int8).reshape(n32 // 32, k // 32, 2, 32, 16)
-    return np.ascontiguousarray(t.transpose(1, 2, 4, 0, 3).reshape(k, n32)[:, :n])
+    wp = t.transpose(1, 2, 4, 0, 3).reshape(k, n32 // 32, 32)[:, :, MFMA32_ROW_OF_CHANNEL]
+    return np.ascontiguousarray(wp.reshape(k, n32)[:, :n])
 
 
 class _Holder:

@@ -22,8 +22,10 @@
  * Packed GEMM weight layout ("mfma32"): a logical int8 matrix W[K][N]
  * (row-major, the reference's layout) with K % 32 == 0 is padded to
  * N32 = ceil(N/32)*32 columns and stored as [N32/32][K/32][64][16] bytes:
- * element (k, n) lives at tile (n/32, k/32), lane (n%32) + 32*((k%32)/16),
- * byte k%16.  Each 1 KiB tile is the B operand of one 32x32x32 int8 MFMA.
+ * element (k, n) lives at tile (n/32, k/32), lane r(n%32) + 32*((k%32)/16),
+ * byte k%16, where r(c) = 8*((c%16)/4) + 4*(c/16) + c%4.  Each 1 KiB tile is
+ * the first operand of one 32x32x32 int8 MFMA; the row order r puts output
+ * channels 16*(l/32) .. +15 of a token row in result lane l.
  */
 #ifndef HEATVIT_HIP_H
 #define HEATVIT_HIP_H

@@ -41,11 +41,22 @@ def test_mfma32_packing_roundtrip_and_layout():
         p = pack_mfma32(w)
         assert p.size == -(-n // 32) * 32 * k
         assert np.array_equal(unpack_mfma32(p, k, n), w)
-        # element (k, n) sits at tile (n/32, k/32), lane n%32 + 32*((k%32)/16), byte k%16
-        for kk, nn in ((0, 0), (k - 1, n - 1), (17, min(33, n - 1))):
+        # element (k, n) sits at tile (n/32, k/32), lane r(n%32) + 32*((k%32)/16),
+        # byte k%16, with r(c) = 8*((c%16)/4) + 4*(c/16) + c%4 (include/heatvit_hip.h)
+        for kk, nn in ((0, 0), (k - 1, n - 1), (17, min(33, n - 1)), (40 % k, min(21, n - 1))):
+            c = nn % 32
             tile = (nn // 32) * (k // 32) + kk // 32
-            lane = nn % 32 + 32 * ((kk % 32) // 16)
+            lane = 8 * ((c % 16) // 4) + 4 * (c // 16) + c % 4 + 32 * ((kk % 32) // 16)
             assert p[tile * 1024 + lane * 16 + kk % 16] == w[kk, nn]
+    # MFMA 32x32 result layout: lane l, element i is operand row
+    # 8*(i//4) + 4*(l//32) + i%4; with this packing that row carries output
+    # channel 16*(l//32) + i, so each lane ends with 16 contiguous channels.
+    w = np.arange(32, dtype=np.int8)[None, :].repeat(32, 0)  # W[k][n] = n
+    tile = pack_mfma32(w).reshape(64, 16)
+    for lane in range(64):
+        for i in range(16):
+            row = 8 * (i // 4) + 4 * (lane // 32) + i % 4
+            assert tile[row, 0] == 16 * (lane // 32) + i
     with pytest.raises(ValueError):
         pack_mfma32(np.zeros((17, 4), np.int8))
 
