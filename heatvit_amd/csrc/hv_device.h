@@ -75,7 +75,7 @@ __device__ __forceinline__ i64 requant128(i128 v, int shift, int bits) {
 }
 
 // round_div (fixed.py:57-70) for den > 0: nearest, ties away from zero.
-__device__ __forceinline__ i64 round_div_pos(i64 num, i64 den) {
+__host__ __device__ __forceinline__ i64 round_div_pos(i64 num, i64 den) {
   u64 mag = num < 0 ? (u64)(-num) : (u64)num;
   u64 q = mag / (u64)den, r = mag - q * (u64)den;
   if (2 * r >= (u64)den) q += 1;
@@ -143,23 +143,21 @@ __device__ __forceinline__ int gelu_q16(int x) {
   const int ip = x + (x >> 1) + (x >> 3) + (x >> 4);
   const int ip2 = ip + (ip >> 1) - (ip >> 4);
   const unsigned a = (unsigned)(ip2 < 0 ? -ip2 : ip2);
-  const unsigned q = a >> 16, r = a & 0xFFFFu;
-  const unsigned frac = (__umul24(r, 11u) + 15u) >> 4;
-  unsigned e;
-  if (ip2 < 0) {
-    e = (65536u - frac) >> (q < 31u ? q : 31u);
-  } else {
-    const unsigned sh = (65536u + frac) << (q < 8u ? q : 8u);
-    e = sh < (1u << 23) - 1 ? sh : (1u << 23) - 1;
-  }
+  const unsigned q = a >> 16;
+  const unsigned frac = (__umul24(a & 0xFFFFu, 11u) + 15u) >> 4;
+  // Both branches of nonlinear.gelu, selected without a divergent branch.
+  const unsigned e_neg = (65536u - frac) >> (q < 31u ? q : 31u);
+  const unsigned e_pos = min((65536u + frac) << (q < 8u ? q : 8u), (1u << 23) - 1);
+  const unsigned e = ip2 < 0 ? e_neg : e_pos;
   const unsigned den = 65536u + e;
   const float est = (float)e * 65536.0f * __builtin_amdgcn_rcpf((float)den) + 0.5f;
-  unsigned sig = (unsigned)est;
-  const int rem = (int)((e << 16) + (den >> 1) - __umul24(sig, den));
-  sig = rem < 0 ? sig - 1 : (rem >= (int)den ? sig + 1 : sig);
+  // sig < 2^17 and den < 2^24: the product below is a 24-bit multiply whose
+  // low 32 bits are all the wrapping remainder needs.
+  unsigned sig = min((unsigned)est, 0x1FFFFu);
+  const int rem = (int)((e << 16) + (den >> 1) - sig * den);
+  sig = sig + (rem >= (int)den ? 1u : 0u) + (unsigned)(rem >> 31);
   const unsigned ax = (unsigned)(x < 0 ? -x : x);
-  const unsigned y = __umul24(ax >> 16, sig) +
-                     ((__umul24(ax & 0xFFFFu, sig) + 32768u) >> 16);
+  const unsigned y = __umul24(ax >> 16, sig) + ((__umul24(ax & 0xFFFFu, sig) + 32768u) >> 16);
   return x < 0 ? -(int)y : (int)y;
 }
 
@@ -183,43 +181,120 @@ __device__ __forceinline__ int plan_sigmoid(int x) {
 }
 
 // _softmax_exp (nonlinear.py:98-106) for x_tilde in [-(2^31 - 1), 0].
-__device__ __forceinline__ unsigned softmax_exp(int xt) {
+// shifted < 2^17, so its square is one 32x32->64 multiply-add; the Q16
+// polynomial term stays below 2^32; e < 2^17 makes e >> min(z, 31) equal
+// to the reference's e >> z for every z.
+__host__ __device__ __forceinline__ unsigned softmax_exp(int xt) {
   const unsigned nx = (unsigned)(-xt);
   const unsigned z = nx / 45426u;
-  const int p = xt + (int)(z * 45426u);
-  const unsigned s = (unsigned)(p + 88670);          // (43244, 88670]
+  const int p = xt + (int)(z * 45426u);              // (-45426, 0]
+  const unsigned s = (unsigned)(p + 88670) & 0x1FFFFu;  // (43244, 88670]
   const unsigned square = (unsigned)(((u64)s * s + 32768u) >> 16);   // <= 119971
-  const unsigned e = (unsigned)(((u64)23495u * square + 32768u) >> 16) + 22544u;
-  return z >= 32 ? 0u : (e >> z);
+  const unsigned e = ((23495u * square + 32768u) >> 16) + 22544u;    // < 2^17
+  return e >> (z < 31u ? z : 31u);
 }
 
-// round_div(2^32, sum) for sum > 0 (nonlinear.py:119).
-__device__ __forceinline__ u64 softmax_recip(u64 sum) {
+// round_div(2^32, sum) for a row sum that includes exp(0) = 65554, so
+// 65554 <= sum < 2^32 and the result is below 2^17 (nonlinear.py:119):
+// float estimate, exact correction on the remainder.
+__host__ __device__ __forceinline__ unsigned softmax_recip(u64 sum) {
   const u64 num = 1ull << 32;
-  u64 q = num / sum, r = num - q * sum;
-  if (2 * r >= sum) q += 1;
-  return q;
+  u64 q = (u64)(4294967296.0f / (float)sum);
+  while (q * sum > num) --q;
+  while ((q + 1) * sum <= num) ++q;
+  const u64 r = num - q * sum;
+  return (unsigned)(2 * r >= sum ? q + 1 : q);
 }
 
 // ratio = rsa(e * recip, 16); with delta2 = 65536 the scaled value equals
-// the ratio (nonlinear.py:120-121).
-__device__ __forceinline__ unsigned softmax_ratio(unsigned e, u64 recip) {
+// the ratio (nonlinear.py:120-121).  e, recip < 2^17.
+__host__ __device__ __forceinline__ unsigned softmax_ratio(unsigned e, unsigned recip) {
   return (unsigned)(((u64)e * recip + 32768u) >> 16);
 }
 
 // softmax_attention narrowing (nonlinear.py:133): min(rsa(scaled, 8), 255).
-__device__ __forceinline__ unsigned prob_u8(unsigned ratio) {
+__host__ __device__ __forceinline__ unsigned prob_u8(unsigned ratio) {
   const unsigned p = (ratio + 128u) >> 8;
   return p > 255u ? 255u : p;
 }
 
 // floor square root over u64 (fixed.isqrt, fixed.py:73-80): double estimate
 // and exact integer correction.
-__device__ __forceinline__ u64 isqrt_u64(u64 x) {
+__host__ __device__ __forceinline__ u64 isqrt_u64(u64 x) {
   u64 r = (u64)__builtin_sqrt((double)x);
   while (r > 0 && r * r > x) --r;
   while ((r + 1) * (r + 1) <= x) ++r;
   return r;
+}
+
+// ---------------------------------------------------------------- layernorm
+// int32 element path of nonlinear.layernorm (nonlinear.py:136-186) for
+// input scales in [-16, -4] (s = x_scale + 32 in [16, 28], the x^2 rounding
+// shift -(2*x_scale + 32) <= 0 so sum_square = (sum x^2) << t exactly).
+//
+// norm = sat24(rsa(V, 48)) with V = (x*2^s - mean) * inv = x*A - B,
+// A = inv*2^s (< 2^71), B = mean*inv.  Since inv > 0, V < 0 exactly when
+// x <= xt = floor((mean - 1) / 2^s), and rsa(V, 48) = floor(W / 2^48) with
+// W = x*A + C - [x <= xt], C = 2^47 - B.  A is split into signed 24-bit
+// limbs (a2, a1, a0) and C into (c2, c1, c0) with c1, c0 in [0, 2^24), so
+// floor(W / 2^48) follows from three 24-bit multiply-adds and two carries,
+// all inside int32 (|x*a0|, |x*a1| <= 2^30, |x*a2| <= 2^29 + 128).  c2 is
+// clamped to [-2^30, 2^30]: beyond that |x*a2 + c2 + carry| > 2^29 - 200
+// saturates to the same 24-bit bound either way.
+struct LnRow {
+  int a0, a1, a2, c0, c1, c2, xt;
+  bool neg_var;
+};
+
+__host__ __device__ __forceinline__ int sext24(long long v) {
+  return (int)((unsigned)((unsigned long long)v << 8)) >> 8;
+}
+
+// round_div(2^48, d) for 1 <= d < 2^32: double estimate, exact correction.
+__host__ __device__ __forceinline__ u64 recip48(u64 d) {
+  const u64 num = 1ull << 48;
+  u64 q = (u64)((double)num / (double)d);
+  while (q * d > num) --q;
+  while ((q + 1) * d <= num) ++q;
+  const u64 r = num - q * d;
+  return 2 * r >= d ? q + 1 : q;
+}
+
+// Per-row constants from the row sums sx = sum x, sxx = sum x^2.
+__host__ __device__ __forceinline__ LnRow ln_row_consts(int sx, int sxx, int s, int t) {
+  LnRow r;
+  const i64 mean = round_div_pos((i64)sx * (1ll << s), 192);
+  const i64 e2 = round_div_pos((i64)sxx * (1ll << t), 192);
+  const u64 m = mean < 0 ? (u64)(-mean) : (u64)mean;  // < 2^37
+  const u64 mh = m >> 16, ml = m & 0xFFFFull;
+  const i64 mean_sq = (i64)(mh * mh + ((((mh * ml) << 17) + ml * ml + (1ull << 31)) >> 32));
+  i64 var = e2 - mean_sq;
+  r.neg_var = var < 0;
+  if (var < 0) var = 0;
+  const u64 sd = isqrt_u64((u64)var + 4295u);
+  const u64 inv = recip48(sd);  // < 2^42
+  const i128 A = (i128)inv << s;
+  r.a0 = sext24((long long)(A & 0xFFFFFF));
+  const i128 A1 = (A - r.a0) >> 24;
+  r.a1 = sext24((long long)(A1 & 0xFFFFFF));
+  r.a2 = sext24((long long)((A1 - r.a1) >> 24));  // < 2^22 + 2 for s <= 28
+  const i128 C = ((i128)1 << 47) - (i128)mean * (i128)inv;
+  r.c0 = (int)(C & 0xFFFFFF);
+  const i128 C1 = C >> 24;
+  r.c1 = (int)(C1 & 0xFFFFFF);
+  const i128 c2 = C1 >> 24;
+  r.c2 = c2 > (1 << 30) ? (1 << 30) : (c2 < -(1 << 30) ? -(1 << 30) : (int)c2);
+  const i64 xt = (mean - 1) >> s;
+  r.xt = xt > 127 ? 127 : (xt < -129 ? -129 : (int)xt);
+  return r;
+}
+
+// norm_q16 of one element (sat24 included).
+__host__ __device__ __forceinline__ int ln_norm(int x, const LnRow &r) {
+  const int u0 = x * r.a0 + r.c0 - (x <= r.xt ? 1 : 0);
+  const int u1 = x * r.a1 + r.c1 + (u0 >> 24);
+  const int v = x * r.a2 + r.c2 + (u1 >> 24);
+  return v < -(1 << 23) ? -(1 << 23) : (v > (1 << 23) - 1 ? (1 << 23) - 1 : v);
 }
 
 __device__ __forceinline__ int sat_q016(i64 v) { return v < 0 ? 0 : (v > 65536 ? 65536 : (int)v); }

@@ -62,7 +62,8 @@ struct AttnArgs {
   int score_shift;    // score_exp - 2*qkv_out_exp (requant to int32)
   int q16_shift;      // -(score_exp + 13)
   int ctx_shift;      // context_out_exp - (prob_exp + qkv_out_exp)
-  int q16_mode, q16_s;  // int32 fast path for the score -> Q8.16 conversion
+  int q16_mode, q16_s, q16_rnd;  // int32 fast path for the score -> Q8.16 conversion
+  int ctx_fast, ctx_rnd;         // int32 context requant (shift in [1, 30])
 };
 int launch_attention(const AttnArgs &a, hipStream_t s);
 

@@ -93,6 +93,65 @@ __global__ __launch_bounds__(256) void k_layernorm(const int8_t *__restrict__ x,
   }  // row loop
 }
 
+// int32 LayerNorm for input scales in [-16, -4] with gamma at the common
+// exponent (g_exp - 16 <= b_exp), beta shift bs <= 22 and output shift os in
+// [1, 29] (LnRow in hv_device.h): eight lanes per row, 24 channels each.
+// Row sums come from packed int8 dot products; each element costs three
+// 24-bit multiply-adds for norm_q16, one for gamma/beta and the requant.
+__global__ __launch_bounds__(256) void k_layernorm32(const int8_t *__restrict__ x,
+                                                     const int8_t *__restrict__ gamma,
+                                                     const int8_t *__restrict__ beta,
+                                                     int8_t *__restrict__ y, int rows,
+                                                     const int32_t *rows_dev, int s, int t,
+                                                     int bs, int os, uint8_t *neg_var) {
+  const int sub = threadIdx.x & 7;
+  const int R = rows_dev ? min(*rows_dev, rows) : rows;
+  const int c0 = sub * 24;
+  int gm[24], bsh[24];
+#pragma unroll
+  for (int j = 0; j < 24; ++j) {
+    gm[j] = gamma[c0 + j];
+    bsh[j] = (int)beta[c0 + j] * (1 << bs);
+  }
+  const int rnd = 1 << (os - 1);
+  for (int row = blockIdx.x * 32 + (threadIdx.x >> 3); row < R; row += gridDim.x * 32) {
+    const int2 *xr = reinterpret_cast<const int2 *>(x + (size_t)row * 192 + c0);
+    int w[6];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const int2 v = xr[q];
+      w[2 * q] = v.x;
+      w[2 * q + 1] = v.y;
+    }
+    int sx = 0, sxx = 0;
+#pragma unroll
+    for (int q = 0; q < 6; ++q) {
+      sx = __builtin_amdgcn_sdot4(w[q], 0x01010101, sx, false);
+      sxx = __builtin_amdgcn_sdot4(w[q], w[q], sxx, false);
+    }
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) {
+      sx += __shfl_xor(sx, off);
+      sxx += __shfl_xor(sxx, off);
+    }
+    const LnRow r = ln_row_consts(sx, sxx, s, t);
+    int out[6] = {0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 24; ++j) {
+      const int xv = (int)(int8_t)(w[j >> 2] >> (8 * (j & 3)));
+      const int norm = ln_norm(xv, r);
+      const int a = norm * gm[j] + bsh[j];
+      int o = (a + rnd + (a >> 31)) >> os;
+      o = min(max(o, -128), 127);
+      out[j >> 2] |= (o & 0xFF) << (8 * (j & 3));
+    }
+    int2 *yr = reinterpret_cast<int2 *>(y + (size_t)row * 192 + c0);
+#pragma unroll
+    for (int q = 0; q < 3; ++q) yr[q] = int2{out[2 * q], out[2 * q + 1]};
+    if (neg_var && sub == 0) neg_var[row] = r.neg_var ? 1 : 0;
+  }
+}
+
 int launch_layernorm(const int8_t *x, const int8_t *g, const int8_t *b, int8_t *y, int rows,
                      const int32_t *rows_dev, int x_exp, int g_exp, int b_exp, int out_exp,
                      uint8_t *neg_var, hipStream_t s) {
@@ -102,6 +161,14 @@ int launch_layernorm(const int8_t *x, const int8_t *g, const int8_t *b, int8_t *
   if (((uintptr_t)x & 3) || ((uintptr_t)y & 3))
     return fail(HV_EVALUE, "layernorm: rows must be 4-byte aligned");
   const int common = (g_exp - 16) < b_exp ? (g_exp - 16) : b_exp;
+  const int gs = g_exp - 16 - common, bs = b_exp - common, os = out_exp - common;
+  if (x_exp >= -16 && x_exp <= -4 && gs == 0 && bs <= 22 && os >= 1 && os <= 29 &&
+      ((uintptr_t)x & 7) == 0 && ((uintptr_t)y & 7) == 0) {
+    const int blocks = (rows + 31) / 32;
+    hipLaunchKernelGGL(k_layernorm32, dim3(blocks < 256 * 8 ? blocks : 256 * 8), dim3(256), 0, s,
+                       x, g, b, y, rows, rows_dev, x_exp + 32, 2 * x_exp + 32, bs, os, neg_var);
+    return check_hip(hipGetLastError(), "k_layernorm32 launch");
+  }
   const bool fast_norm = x_exp <= -1;
   const bool fast_align = (g_exp - 16 - common) <= 30 && (b_exp - common) <= 54;
   const int blocks = (rows + 15) / 16;
@@ -133,10 +200,11 @@ int launch_layernorm(const int8_t *x, const int8_t *g, const int8_t *b, int8_t *
 // reciprocal per lane.  The UQ0.8 probabilities stay in registers: packed
 // four per dword they are exactly the B operand of ctx^T = V^T P^T once V^T
 // is stored in LDS with the matching key order (key 16t + 4g + i of a
-// 64-key chunk at byte 16g + 4t + i).  P is unsigned, so the MFMA sees
-// P - 128 and 128 * colsum(V) is added back; |acc| <= 197*255*128 < 2^23.
-// Lane l then holds four consecutive context channels of query l%16 and
-// stores them as one dword.
+// 64-key chunk at byte 16g + 4t + i).  P is unsigned and the MFMA signed,
+// so P = 2*(P >> 1) + (P & 1) runs as two products with int8 operands;
+// |ctx| <= 197*128*255 < 2^23.  Lane l then holds four consecutive context
+// channels of query l%16 and stores them as one dword.  V^T is built with
+// 4x4 byte transposes in registers (dword LDS stores).
 // ---------------------------------------------------------------------------
 static constexpr int kMaxKeys = 208;   // 13 key tiles of 16
 static constexpr int kKStride = 80;    // LDS row strides: the 16 lanes of a
@@ -148,29 +216,37 @@ __device__ __forceinline__ int vt_pos(int k) {
 
 // q16 = sat24(rsa(requant(acc, 2*qkv, score, 32), -(score+13))).  Modes
 // chosen on the host (|acc| <= 64*128*128 = 2^20): 0 = rsa(acc, s) then
-// sat24, 1 = sat24(acc << s) with s <= 10, 2 = the general two-step form.
-__device__ __forceinline__ int attn_q16(int acc, const AttnArgs &g) {
-  if (g.q16_mode == 0) {
-    const int s = g.q16_s;
-    int r = acc;
-    if (s > 0) {
-      const unsigned mag = (unsigned)(acc < 0 ? -acc : acc);
-      const int m = (int)((mag + (1u << (s - 1))) >> s);
-      r = acc < 0 ? -m : m;
-    }
-    return r > (1 << 23) - 1 ? (1 << 23) - 1 : (r < -(1 << 23) ? -(1 << 23) : r);
-  }
-  if (g.q16_mode == 1) {
-    const int r = acc * (1 << g.q16_s);
-    return r > (1 << 23) - 1 ? (1 << 23) - 1 : (r < -(1 << 23) ? -(1 << 23) : r);
-  }
-  return (int)requant_shift(requant_shift(acc, g.score_shift, 32), g.q16_shift, 24);
+// sat24 (s in [1, 30]), 1 = sat24(acc << s) with s <= 10, 2 = the general
+// two-step form.
+__device__ __noinline__ int attn_q16_general(int acc, int score_shift, int q16_shift) {
+  return (int)requant_shift(requant_shift(acc, score_shift, 32), q16_shift, 24);
 }
 
+template <int MODE>
+__device__ __forceinline__ int attn_q16(int acc, const AttnArgs &g) {
+  int r;
+  if (MODE == 0) {
+    r = (acc + g.q16_rnd + (acc >> 31)) >> g.q16_s;
+  } else if (MODE == 1) {
+    r = acc * (1 << g.q16_s);
+  } else {
+    return attn_q16_general(acc, g.score_shift, g.q16_shift);
+  }
+  return min(max(r, -(1 << 23)), (1 << 23) - 1);
+}
+
+__device__ __noinline__ int attn_score_ckpt(int acc, int score_shift) {
+  return (int)requant_shift(acc, score_shift, 32);
+}
+
+__device__ __noinline__ int attn_ctx_general(int v, int ctx_shift) {
+  return (int)requant_shift(v, ctx_shift, 8);
+}
+
+template <int MODE, bool CKPT>
 __global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
   __shared__ __attribute__((aligned(16))) int8_t Ks[kMaxKeys * kKStride];
   __shared__ __attribute__((aligned(16))) int8_t Vt[64 * kVStride];
-  __shared__ int colsum[64];
 
   const int b = blockIdx.x / 3, h = blockIdx.x - 3 * (blockIdx.x / 3);
   const int row0 = g.offsets[b];
@@ -187,20 +263,26 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
     if (r < N) v = *reinterpret_cast<const v4i *>(qkv + (size_t)r * 576 + 192 + h * 64 + c);
     *reinterpret_cast<v4i *>(&Ks[r * kKStride + c]) = v;
   }
-  for (int i = tid; i < n64 * 64 * 4; i += 256) {
-    const int r = i >> 2, c = (i & 3) * 16;
-    v4i v = v4i{0};
-    if (r < N) v = *reinterpret_cast<const v4i *>(qkv + (size_t)r * 576 + 384 + h * 64 + c);
-    const int8_t *vb = reinterpret_cast<const int8_t *>(&v);
-    const int pos = vt_pos(r);
+  // V^T: item (key quad kq, 16-channel group dg); keys beyond N are zero.
+  for (int i = tid; i < n64 * 64; i += 256) {
+    const int kq = i >> 2, dg = i & 3;
+    v4i rows[4];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) Vt[(c + j) * kVStride + pos] = vb[j];
-  }
-  __syncthreads();
-  if (tid < 64) {
-    int s = 0;
-    for (int r = 0; r < n64 * 64; ++r) s += Vt[tid * kVStride + r];  // padding is zero
-    colsum[tid] = s;
+    for (int j = 0; j < 4; ++j) {
+      const int r = 4 * kq + j;
+      rows[j] = r < N ? *reinterpret_cast<const v4i *>(qkv + (size_t)r * 576 + 384 + h * 64 + dg * 16)
+                      : v4i{0};
+    }
+    const int pos = vt_pos(4 * kq);
+#pragma unroll
+    for (int dq = 0; dq < 4; ++dq)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        unsigned col = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) col |= (((unsigned)rows[j][dq] >> (8 * e)) & 0xFFu) << (8 * j);
+        *reinterpret_cast<unsigned *>(&Vt[(dg * 16 + dq * 4 + e) * kVStride + pos]) = col;
+      }
   }
   __syncthreads();
 
@@ -219,13 +301,12 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int key = kt * 16 + 4 * grp + i;
-          const int v = attn_q16(st[i], g);
+          const int v = attn_q16<MODE>(st[i], g);
           val[kt][i] = v;
           if (key < N) {
             mx = v > mx ? v : mx;
-            if (g.score && q < N)
-              g.score[(((size_t)b * 3 + h) * 197 + q) * 197 + key] =
-                  (int32_t)requant_shift(st[i], g.score_shift, 32);
+            if (CKPT && g.score && q < N)
+              g.score[(((size_t)b * 3 + h) * 197 + q) * 197 + key] = attn_score_ckpt(st[i], g.score_shift);
           }
         }
       }
@@ -247,45 +328,48 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
     }
     sum += __shfl_xor(sum, 16);
     sum += __shfl_xor(sum, 32);
-    const u64 recip = softmax_recip(sum);
-    v4i pk[4];
+    const unsigned recip = softmax_recip(sum);
+    v4i pk_hi[4], pk_lo[4];
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int kt = kc * 4 + t;
-        int word = 0x80808080;  // prob 0 -> P - 128 = -128 (V^T is zero there)
+        unsigned whi = 0, wlo = 0;
         if (kt < 13 && kt < n16) {
-          word = 0;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int key = kt * 16 + 4 * grp + i;
             const unsigned p = key < N ? prob_u8(softmax_ratio((unsigned)val[kt][i], recip)) : 0u;
-            word |= (int)((p - 128u) & 0xFFu) << (8 * i);
-            if (g.prob && q < N && key < N)
+            whi |= (p >> 1) << (8 * i);
+            wlo |= (p & 1u) << (8 * i);
+            if (CKPT && g.prob && q < N && key < N)
               g.prob[(((size_t)b * 3 + h) * 197 + q) * 197 + key] = (uint8_t)p;
           }
         }
-        pk[kc][t] = word;
+        pk_hi[kc][t] = (int)whi;
+        pk_lo[kc][t] = (int)wlo;
       }
     }
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
-      v4i acc = v4i{0};
+      v4i ahi = v4i{0}, alo = v4i{0};
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
         if (kc < n64) {
           const v4i va = *reinterpret_cast<const v4i *>(&Vt[(dt * 16 + ql) * kVStride + kc * 64 + grp * 16]);
-          acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(va, pk[kc], acc, 0, 0, 0);
+          ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(va, pk_hi[kc], ahi, 0, 0, 0);
+          alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(va, pk_lo[kc], alo, 0, 0, 0);
         }
       }
       if (q < N) {
         int word = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int d = dt * 16 + 4 * grp + i;
-          const i64 v = (i64)acc[i] + 128ll * colsum[d];
-          word |= ((int)requant_shift(v, g.ctx_shift, 8) & 0xFF) << (8 * i);
+          const int v = 2 * ahi[i] + alo[i];
+          const int o = g.ctx_fast ? min(max((v + g.ctx_rnd + (v >> 31)) >> g.ctx_shift, -128), 127)
+                                   : attn_ctx_general(v, g.ctx_shift);
+          word |= (o & 0xFF) << (8 * i);
         }
         *reinterpret_cast<int *>(g.ctx + (size_t)(row0 + q) * 192 + h * 64 + dt * 16 + 4 * grp) = word;
       }
@@ -302,16 +386,29 @@ int launch_attention(const AttnArgs &a_in, hipStream_t s) {
   const int s1 = -a.score_shift, s2 = a.q16_shift;
   a.q16_mode = 2;
   a.q16_s = 0;
+  a.q16_rnd = 0;
   if (a.score_shift <= 0 && s1 <= 10) {
     if (s2 >= s1) {
       a.q16_mode = 0;
-      a.q16_s = s2 - s1 > 31 ? 31 : s2 - s1;
+      a.q16_s = s2 - s1 > 30 ? 30 : s2 - s1;
+      if (a.q16_s == 0) a.q16_mode = 1;  // plain saturation
+      a.q16_rnd = a.q16_s > 0 ? 1 << (a.q16_s - 1) : 0;
     } else if (s1 - s2 <= 10) {
       a.q16_mode = 1;
       a.q16_s = s1 - s2;
     }
   }
-  hipLaunchKernelGGL(k_attention, dim3(a.batch * 3), dim3(256), 0, s, a);
+  // |ctx| < 2^23: the int32 requant is exact for shifts in [1, 30].
+  a.ctx_fast = a.ctx_shift >= 1 && a.ctx_shift <= 30;
+  a.ctx_rnd = a.ctx_fast ? 1 << (a.ctx_shift - 1) : 0;
+  const bool ck = a.score || a.prob;
+  const dim3 grid(a.batch * 3), block(256);
+  if (a.q16_mode == 0 && !ck) hipLaunchKernelGGL((k_attention<0, false>), grid, block, 0, s, a);
+  else if (a.q16_mode == 0) hipLaunchKernelGGL((k_attention<0, true>), grid, block, 0, s, a);
+  else if (a.q16_mode == 1 && !ck) hipLaunchKernelGGL((k_attention<1, false>), grid, block, 0, s, a);
+  else if (a.q16_mode == 1) hipLaunchKernelGGL((k_attention<1, true>), grid, block, 0, s, a);
+  else if (!ck) hipLaunchKernelGGL((k_attention<2, false>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((k_attention<2, true>), grid, block, 0, s, a);
   return check_hip(hipGetLastError(), "k_attention launch");
 }
 
@@ -346,7 +443,7 @@ __global__ __launch_bounds__(64) void k_softmax_rows(const int32_t *x, const int
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-  const u64 recip = softmax_recip(sum);
+  const unsigned recip = softmax_recip(sum);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int c = lane + 64 * j;
