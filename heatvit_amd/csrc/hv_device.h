@@ -139,27 +139,42 @@ __device__ __forceinline__ int align_add_pre(int a, int b, int da, int db, int o
 //  * |x| * sig < 2^39: with |x| = ah * 2^16 + al (ah < 2^7) the rounded shift
 //    is ah * sig + ((al * sig + 2^15) >> 16), two 24-bit products, and its
 //    magnitude stays below |x| < 2^23, so the 24-bit saturation never acts.
-__device__ __forceinline__ int gelu_q16(int x) {
+__host__ __device__ __forceinline__ unsigned mul_u24(unsigned a, unsigned b) {
+  return (a & 0xFFFFFFu) * (b & 0xFFFFFFu);
+}
+
+// The single-precision reciprocal the quotient estimate uses; any value
+// within a few ulp of 1/d works (the correction step is exact).
+struct RcpHw {
+  __device__ static float rcp(float d) { return __builtin_amdgcn_rcpf(d); }
+};
+
+template <typename R>
+__host__ __device__ __forceinline__ int gelu_q16_r(int x) {
   const int ip = x + (x >> 1) + (x >> 3) + (x >> 4);
   const int ip2 = ip + (ip >> 1) - (ip >> 4);
   const unsigned a = (unsigned)(ip2 < 0 ? -ip2 : ip2);
   const unsigned q = a >> 16;
-  const unsigned frac = (__umul24(a & 0xFFFFu, 11u) + 15u) >> 4;
+  const unsigned frac = (mul_u24(a & 0xFFFFu, 11u) + 15u) >> 4;
   // Both branches of nonlinear.gelu, selected without a divergent branch.
   const unsigned e_neg = (65536u - frac) >> (q < 31u ? q : 31u);
-  const unsigned e_pos = min((65536u + frac) << (q < 8u ? q : 8u), (1u << 23) - 1);
+  const unsigned sh = (65536u + frac) << (q < 8u ? q : 8u);
+  const unsigned e_pos = sh < (1u << 23) - 1 ? sh : (1u << 23) - 1;
   const unsigned e = ip2 < 0 ? e_neg : e_pos;
   const unsigned den = 65536u + e;
-  const float est = (float)e * 65536.0f * __builtin_amdgcn_rcpf((float)den) + 0.5f;
+  const float est = (float)e * 65536.0f * R::rcp((float)den) + 0.5f;
   // sig < 2^17 and den < 2^24: the product below is a 24-bit multiply whose
   // low 32 bits are all the wrapping remainder needs.
-  unsigned sig = min((unsigned)est, 0x1FFFFu);
-  const int rem = (int)((e << 16) + (den >> 1) - sig * den);
+  unsigned sig = (unsigned)est;
+  sig = sig < 0x1FFFFu ? sig : 0x1FFFFu;
+  const int rem = (int)((e << 16) + (den >> 1) - mul_u24(sig, den));
   sig = sig + (rem >= (int)den ? 1u : 0u) + (unsigned)(rem >> 31);
   const unsigned ax = (unsigned)(x < 0 ? -x : x);
-  const unsigned y = __umul24(ax >> 16, sig) + ((__umul24(ax & 0xFFFFu, sig) + 32768u) >> 16);
+  const unsigned y = mul_u24(ax >> 16, sig) + ((mul_u24(ax & 0xFFFFu, sig) + 32768u) >> 16);
   return x < 0 ? -(int)y : (int)y;
 }
+
+__device__ __forceinline__ int gelu_q16(int x) { return gelu_q16_r<RcpHw>(x); }
 
 // requant(gelu(requant(v, src, -16, 24)), -16, dst, 8): the GEMM+GELU
 // post-op of ffn (transformer.py:349-358) and selector._gemm_gelu

@@ -1,0 +1,118 @@
+// Host build of the device-side integer helpers (heatvit_amd/csrc/hv_device.h)
+// checked against the CPU oracle.  Test infrastructure: compiled and run by
+// tests/test_device_math_cpu.py; the oracle is the checker here.
+//
+//   gelu     exhaustive over the 24-bit domain, with the reciprocal estimate
+//            exact and perturbed by one ulp either way (the hardware rcp is
+//            only ulp-accurate), against hvo_gelu;
+//   softmax  the 32-bit exp / reciprocal / ratio path against
+//            hvo_softmax_attention and hvo_softmax_selector on random rows;
+//   layernorm the int32 limb-split normalisation (ln_row_consts / ln_norm)
+//            against hvo_layernorm on random and degenerate rows over the
+//            exponent range the kernel takes it for.
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <random>
+
+#include "hv_device.h"
+extern "C" {
+#include "hv_oracle.h"
+}
+
+using namespace hv;
+
+struct RcpExact { static float rcp(float d) { return 1.0f / d; } };
+struct RcpLo { static float rcp(float d) { return std::nextafter(1.0f / d, 0.0f); } };
+struct RcpHi { static float rcp(float d) { return std::nextafter(1.0f / d, 1.0f); } };
+
+static long check_gelu() {
+  long bad = 0;
+  for (int x = -(1 << 23); x < (1 << 23); ++x) {
+    const int ref = hvo_gelu(x);
+    if (gelu_q16_r<RcpExact>(x) != ref || gelu_q16_r<RcpLo>(x) != ref || gelu_q16_r<RcpHi>(x) != ref) {
+      if (++bad < 5) std::printf("gelu mismatch at x=%d (ref %d)\n", x, ref);
+    }
+  }
+  return bad;
+}
+
+static long check_softmax(int rows) {
+  std::mt19937_64 rng(3);
+  int32_t x[256], ref_sel[256];
+  uint8_t ref_att[256];
+  long bad = 0;
+  for (int it = 0; it < rows; ++it) {
+    const int n = 1 + (int)(rng() % 197);
+    const int spread = 1 << (rng() % 25);
+    const int base = (int)(rng() % (1 << 24)) - (1 << 23);
+    for (int i = 0; i < n; ++i) {
+      long long v = base + (long long)(rng() % (2ull * spread + 1)) - spread;
+      x[i] = (int32_t)(v < -(1 << 23) ? -(1 << 23) : (v > (1 << 23) - 1 ? (1 << 23) - 1 : v));
+    }
+    if (hvo_softmax_attention(x, n, ref_att) || hvo_softmax_selector(x, n, ref_sel)) return -1;
+    int mx = x[0];
+    for (int i = 1; i < n; ++i) mx = x[i] > mx ? x[i] : mx;
+    unsigned e[256];
+    unsigned long long sum = 0;
+    for (int i = 0; i < n; ++i) sum += (e[i] = softmax_exp(x[i] - mx));
+    const unsigned recip = softmax_recip(sum);
+    for (int i = 0; i < n; ++i) {
+      const unsigned ratio = softmax_ratio(e[i], recip);
+      if (prob_u8(ratio) != ref_att[i] || (int)(ratio > 65536u ? 65536u : ratio) != ref_sel[i])
+        if (++bad < 5) std::printf("softmax mismatch row %d col %d\n", it, i);
+    }
+  }
+  return bad;
+}
+
+static long check_layernorm(int rows) {
+  std::mt19937_64 rng(7);
+  int8_t x[192], g[192], b[192], ref[192];
+  long bad = 0;
+  for (int it = 0; it < rows; ++it) {
+    const int x_exp = -4 - (int)(rng() % 13);  // [-16, -4]
+    const int g_exp = -4 - (int)(rng() % 9);
+    const int b_exp = g_exp - 16 + (int)(rng() % 23);  // beta shift in [0, 22]
+    const int common = g_exp - 16;
+    const int bs = b_exp - common;
+    const int out_exp = common + 1 + (int)(rng() % 29);  // output shift in [1, 29]
+    const int os = out_exp - common;
+    const int kind = it % 8, base = (int)(rng() % 256) - 128, amp = 1 + (int)(rng() % 128);
+    const int outlier = (int)(rng() % 192);
+    for (int c = 0; c < 192; ++c) {
+      int v;
+      if (kind == 0) v = base;                           // constant row
+      else if (kind == 1) v = c == outlier ? 127 : base;  // one outlier
+      else if (kind == 2) v = (rng() & 1) ? 127 : -128;  // extremes
+      else if (kind == 3) v = base + (int)(rng() % 3) - 1;
+      else v = base + (int)(rng() % (2 * amp + 1)) - amp;
+      x[c] = (int8_t)(v < -128 ? -128 : (v > 127 ? 127 : v));
+      g[c] = (int8_t)((int)(rng() % 256) - 128);
+      b[c] = (int8_t)((int)(rng() % 256) - 128);
+    }
+    int nv = 0;
+    if (hvo_layernorm(x, g, b, x_exp, g_exp, b_exp, out_exp, ref, &nv)) return -1;
+    int sx = 0, sxx = 0;
+    for (int c = 0; c < 192; ++c) {
+      sx += x[c];
+      sxx += x[c] * x[c];
+    }
+    const LnRow r = ln_row_consts(sx, sxx, x_exp + 32, 2 * x_exp + 32);
+    if ((int)r.neg_var != nv) ++bad;
+    for (int c = 0; c < 192; ++c) {
+      const int a = ln_norm(x[c], r) * g[c] + b[c] * (1 << bs);
+      int o = (a + (1 << (os - 1)) + (a >> 31)) >> os;
+      o = o < -128 ? -128 : (o > 127 ? 127 : o);
+      if (o != ref[c] && ++bad < 5) std::printf("layernorm mismatch row %d col %d\n", it, c);
+    }
+  }
+  return bad;
+}
+
+int main(int argc, char **argv) {
+  const int rows = argc > 1 ? std::atoi(argv[1]) : 100000;
+  const long g = check_gelu(), s = check_softmax(rows), l = check_layernorm(rows);
+  std::printf("gelu_bad=%ld softmax_bad=%ld layernorm_bad=%ld\n", g, s, l);
+  return (g || s || l) ? 1 : 0;
+}
