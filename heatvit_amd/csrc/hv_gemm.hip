@@ -30,7 +30,7 @@
 //   EPI_PATCH    t = requant(v, img+w, act, 8); out = align_add(t, pos[p+1])
 //                into row b*197 + 1 + p                transformer.py:120-145
 // The int32 form of each epilogue is taken when the launch's shifts lie in
-// [1, 30], the align-add shifts are at most 21, and every bias of the
+// [-30, 30], the align-add shifts are at most 21, and every bias of the
 // wavefront's columns satisfies |bias| <= 2^30 - 1 - K*2^14 (so v, the
 // aligned sums and every rounding addend stay below 2^31); the other cases
 // call the exact 64/128-bit form, kept out of line.
@@ -64,11 +64,29 @@ __device__ __forceinline__ const int8_t *patch_ptr(const int8_t *images, int r, 
   return images + (size_t)b * kImageBytes + ((pr * 16 + in_row) * 224 + pc * 16) * 3 + rem;
 }
 
-// requant for |v| < 2^30 and shift s in [1, 30] with rnd = 2^(s-1):
-// round_shift_away is (v + rnd - (v < 0)) >> s, then saturate.
-__device__ __forceinline__ int rq(int v, int rnd, int s, int lo, int hi) {
-  const int r = (v + rnd + (v >> 31)) >> s;
-  return min(max(r, lo), hi);
+// requant of |v| < 2^30 to [lo, hi] by a launch-uniform shift s in
+// [-30, 30].  s >= 1: round_shift_away is (v + 2^(s-1) - (v < 0)) >> s.
+// s <= 0: the left shift saturates, so v is first clamped to
+// [(lo >> -s) - 1, (hi >> -s) + 1], which keeps v << -s inside int32 and
+// outside [lo, hi] exactly when the unclamped value is.
+struct Rq {
+  int s, rnd, vlo, vhi, lo, hi;
+};
+
+__device__ __forceinline__ Rq rq_setup(int s, int lo, int hi) {
+  Rq r;
+  r.s = s;
+  r.lo = lo;
+  r.hi = hi;
+  r.rnd = s > 0 ? 1 << (s - 1) : 0;
+  r.vlo = s > 0 ? 0 : (lo >> -s) - 1;
+  r.vhi = s > 0 ? 0 : (hi >> -s) + 1;
+  return r;
+}
+
+__device__ __forceinline__ int rq(int v, const Rq &r) {
+  const int t = r.s > 0 ? (v + r.rnd + (v >> 31)) >> r.s : min(max(v, r.vlo), r.vhi) << -r.s;
+  return min(max(t, r.lo), r.hi);
 }
 
 // Exact epilogue of one element (64/128-bit), out of line.  Returns
@@ -106,9 +124,9 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
   const int T8 = (T + 7) >> 3;
   const int KT = KTC ? KTC : (g.k >> 5);
   const int n32t = (g.n + 31) >> 5;
-  const int rnd_a = FAST ? 1 << (g.shift_a - 1) : 0;
-  const int rnd_b = FAST && EPI == EPI_GELU ? 1 << (g.shift_b - 1) : 0;
-  const int rnd_o = FAST && RESLIKE ? 1 << (g.os - 1) : 0;
+  const Rq rq_a = rq_setup(g.shift_a, EPI == EPI_GELU ? -(1 << 23) : -128,
+                           EPI == EPI_GELU ? (1 << 23) - 1 : 127);
+  const Rq rq_b = rq_setup(EPI == EPI_GELU ? g.shift_b : g.os, -128, 127);
 
   // The grid is a multiple of 8, so t & 7 (the XCD) is fixed per workgroup
   // and XCD x works through logical tiles [x*T8, (x+1)*T8).
@@ -292,17 +310,16 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
           for (int j = 0; j < 16; ++j) {
             const int v = acc[mt][nt][j] + bias4[nt][j >> 2][j & 3];
             if (EPI == EPI_I8) {
-              o[j] = rq(v, rnd_a, g.shift_a, -128, 127);
+              o[j] = rq(v, rq_a);
             } else if (EPI == EPI_GELU) {
-              const int q = rq(v, rnd_a, g.shift_a, -(1 << 23), (1 << 23) - 1);
-              o[j] = rq(gelu_q16(q), rnd_b, g.shift_b, -128, 127);
+              o[j] = rq(gelu_q16(rq(v, rq_a)), rq_b);
             } else if (RESLIKE) {
-              const int t8 = rq(v, rnd_a, g.shift_a, -128, 127);
+              const int t8 = rq(v, rq_a);
               const int r8 = (int)(int8_t)(res4[mt][nt][j >> 2] >> (8 * (j & 3)));
               const int s = EPI == EPI_RES ? r8 * (1 << g.da) + t8 * (1 << g.db)
                                            : t8 * (1 << g.da) + r8 * (1 << g.db);
               mid[j] = t8;
-              o[j] = rq(s, rnd_o, g.os, -128, 127);
+              o[j] = rq(s, rq_b);
             }
           }
         } else {
@@ -376,7 +393,7 @@ void epilogue_limits_pub(GemmArgs &g, int epi) {
 }
 
 static bool fast_epilogue(const GemmArgs &g, int epi) {
-  auto in = [](int s) { return s >= 1 && s <= 30; };
+  auto in = [](int s) { return s >= -30 && s <= 30; };
   if (!g.narrow_ok || !in(g.shift_a)) return false;
   switch (epi) {
     case EPI_I8: return true;
