@@ -302,9 +302,23 @@ int hv_block_forward(const hv_block_dev *p, const int8_t *x, const int32_t *offs
   return block_forward(*p, x, offsets, batch, max_rows, z, ck, w, (hipStream_t)stream);
 }
 
+struct SelectorWs {
+  int32_t *hs;
+  int8_t *stats;
+};
+
+static SelectorWs carve_selector(Carve &cv, int batch) {
+  SelectorWs w;
+  w.hs = cv.take<int32_t>((size_t)batch * 3 * 196);
+  w.stats = cv.take<int8_t>((size_t)batch * 196 * 3);
+  return w;
+}
+
 size_t hv_selector_workspace_bytes(int batch) {
-  (void)batch;
-  return 0;
+  if (batch <= 0) return 0;
+  Carve cv{nullptr, 0};
+  carve_selector(cv, batch);
+  return cv.used;
 }
 
 int hv_selector_forward(const hv_selector_dev *p, const int8_t *tokens, const int32_t *offsets,
@@ -313,12 +327,16 @@ int hv_selector_forward(const hv_selector_dev *p, const int8_t *tokens, const in
                         int32_t *kept_index, int32_t *state, const hv_selector_ckpt *ck,
                         void *workspace, size_t workspace_bytes, hv_stream_t stream) {
   g_err[0] = 0;
-  (void)workspace;
-  (void)workspace_bytes;
   if (!p || !tokens || !offsets || !out_tokens || !out_offsets || !pkg_out || !fused ||
       !kept_index || !state)
     return fail(HV_EVALUE, "selector: null argument");
+  if (batch <= 0) return HV_OK;
+  Carve cv{(uint8_t *)workspace, workspace_bytes};
+  const SelectorWs w = carve_selector(cv, batch);
+  if (!cv.ok || !workspace) return fail(HV_EVALUE, "selector: workspace too small");
   SelectorArgs a{};
+  a.hs = w.hs;
+  a.stats = w.stats;
   a.p = p; a.tokens = tokens; a.offsets = offsets; a.pkg_in = pkg_in; a.batch = batch;
   a.out_tokens = out_tokens; a.out_offsets = out_offsets; a.pkg_out = pkg_out; a.fused = fused;
   a.kept_index = kept_index; a.state = state;
@@ -357,6 +375,7 @@ struct ModelWs {
   BlockWs blk;
   int32_t *off_a, *off_b, *fused, *kept, *state;
   uint8_t *pkg_a, *pkg_b;
+  SelectorWs sel;
 };
 
 static ModelWs carve_model(Carve &cv, int batch) {
@@ -372,6 +391,7 @@ static ModelWs carve_model(Carve &cv, int batch) {
   w.state = cv.take<int32_t>((size_t)batch * 3 * 5);
   w.pkg_a = cv.take<uint8_t>(batch);
   w.pkg_b = cv.take<uint8_t>(batch);
+  w.sel = carve_selector(cv, batch);
   return w;
 }
 
@@ -423,6 +443,7 @@ int hv_model_forward(const hv_model_dev *p, const int8_t *images, int batch, int
       a.tokens = w.xa; a.offsets = w.off_a; a.pkg_in = w.pkg_a; a.batch = batch;
       a.out_tokens = w.xb; a.out_offsets = w.off_b; a.pkg_out = w.pkg_b;
       a.fused = w.fused; a.kept_index = w.kept; a.state = st + (size_t)sel * batch * 5;
+      a.hs = w.sel.hs; a.stats = w.sel.stats;
       a.token_counts = token_counts; a.stage = sel + 1;
       {
         ProfScope ps(HV_PROF_SELECTOR, s);

@@ -176,6 +176,31 @@ __host__ __device__ __forceinline__ int gelu_q16_r(int x) {
 
 __device__ __forceinline__ int gelu_q16(int x) { return gelu_q16_r<RcpHw>(x); }
 
+// requant of |v| < 2^30 to [lo, hi] by a launch-uniform shift s in
+// [-30, 30].  s >= 1: round_shift_away is (v + 2^(s-1) - (v < 0)) >> s.
+// s <= 0: the left shift saturates, so v is first clamped to
+// [(lo >> -s) - 1, (hi >> -s) + 1], which keeps v << -s inside int32 and
+// outside [lo, hi] exactly when the unclamped value is.
+struct Rq {
+  int s, rnd, vlo, vhi, lo, hi;
+};
+
+__device__ __forceinline__ Rq rq_setup(int s, int lo, int hi) {
+  Rq r;
+  r.s = s;
+  r.lo = lo;
+  r.hi = hi;
+  r.rnd = s > 0 ? 1 << (s - 1) : 0;
+  r.vlo = s > 0 ? 0 : (lo >> -s) - 1;
+  r.vhi = s > 0 ? 0 : (hi >> -s) + 1;
+  return r;
+}
+
+__device__ __forceinline__ int rq(int v, const Rq &r) {
+  const int t = r.s > 0 ? (v + r.rnd + (v >> 31)) >> r.s : min(max(v, r.vlo), r.vhi) << -r.s;
+  return min(max(t, r.lo), r.hi);
+}
+
 // requant(gelu(requant(v, src, -16, 24)), -16, dst, 8): the GEMM+GELU
 // post-op of ffn (transformer.py:349-358) and selector._gemm_gelu
 // (selector.py:89-99).  shift_in = -16 - src_exp, shift_out = dst_exp + 16.

@@ -64,31 +64,6 @@ __device__ __forceinline__ const int8_t *patch_ptr(const int8_t *images, int r, 
   return images + (size_t)b * kImageBytes + ((pr * 16 + in_row) * 224 + pc * 16) * 3 + rem;
 }
 
-// requant of |v| < 2^30 to [lo, hi] by a launch-uniform shift s in
-// [-30, 30].  s >= 1: round_shift_away is (v + 2^(s-1) - (v < 0)) >> s.
-// s <= 0: the left shift saturates, so v is first clamped to
-// [(lo >> -s) - 1, (hi >> -s) + 1], which keeps v << -s inside int32 and
-// outside [lo, hi] exactly when the unclamped value is.
-struct Rq {
-  int s, rnd, vlo, vhi, lo, hi;
-};
-
-__device__ __forceinline__ Rq rq_setup(int s, int lo, int hi) {
-  Rq r;
-  r.s = s;
-  r.lo = lo;
-  r.hi = hi;
-  r.rnd = s > 0 ? 1 << (s - 1) : 0;
-  r.vlo = s > 0 ? 0 : (lo >> -s) - 1;
-  r.vhi = s > 0 ? 0 : (hi >> -s) + 1;
-  return r;
-}
-
-__device__ __forceinline__ int rq(int v, const Rq &r) {
-  const int t = r.s > 0 ? (v + r.rnd + (v >> 31)) >> r.s : min(max(v, r.vlo), r.vhi) << -r.s;
-  return min(max(t, r.lo), r.hi);
-}
-
 // Exact epilogue of one element (64/128-bit), out of line.  Returns
 // {output, requantised product (residual forms)}.
 typedef int v2i __attribute__((ext_vector_type(2)));

@@ -1,19 +1,25 @@
 // hv_selector.hip -- token selector (selector.token_selector,
-// selector.py:503-563) over a ragged batch, one workgroup per image.
+// selector.py:503-563) over a ragged batch.
 //
-// k_selector_score: local MLP + head statistics (:253, :358), candidate mean
-//   (:273), concat + 64->32->16->2 score MLP + 2-way selector softmax (:292,
-//   :307, :338), head-weight MLP with PLAN (:370), head fuse (:392), then the
-//   stable keep list (fused >= 32768) and the per-image state.  The tiny
-//   per-candidate GEMMs (K = 64/32/16/3) run on v_dot4_i32_i8 from LDS-held,
-//   output-major weights; one thread owns one (candidate, head) chain.
-// k_selector_keep: the stable keep list and per-image state of
-//   finalize_tokens (:456-500) from the fused scores.
+// k_selector_head, one workgroup per (image, head): local MLP + head
+//   statistic (:253, :358), candidate mean (:273), concat + 64->32->16->2
+//   score MLP + 2-way selector softmax (:292, :307, :338).  One thread owns
+//   one candidate chain; the tiny GEMMs (K = 64/32/16) run on v_dot4_i32_i8
+//   from LDS-held, output-major weights.  Head scores and statistics go to
+//   a workspace.
+// k_selector_keep, one wavefront per image: head-weight MLP with PLAN
+//   (:370) and the head fuse (:392) per candidate (skipped when the fused
+//   scores are given), then the stable keep list (fused >= 32768) and the
+//   per-image state of finalize_tokens (:456-500).
 // k_selector_compact: finalize_tokens (:421-500) as stream compaction:
 //   each image's output offset is the prefix sum of the counts of earlier
 //   images; CLS, the kept rows in input order and the package row
 //   (score-weighted mean of pruned normals plus the incoming package, or
 //   their plain mean when the scores sum to zero) are written there.
+//
+// GELU layers use the int32 requant/GELU path when the host finds every
+// shift in [-30, 30] and each layer's biases satisfy |b| <= 2^30 - 1 -
+// K*2^14 (checked per workgroup, uniform); otherwise the exact 64-bit form.
 #include "hv_device.h"
 #include "hv_internal.h"
 
@@ -25,53 +31,67 @@ __device__ __forceinline__ int dot4(int a, int b, int c) {
   return __builtin_amdgcn_sdot4(a, b, c, false);
 }
 
-__global__ __launch_bounds__(256) void k_selector_score(hv_selector_dev p, const int8_t *tokens,
-                                                        const int32_t *offsets,
-                                                        const uint8_t *pkg_in, int32_t *fused_out,
-                                                        int32_t *kept_index, int32_t *state,
-                                                        hv_selector_ckpt ck) {
-  __shared__ int wl[3 * 32 * 16];   // local_wt [3][32][64] as int words
-  __shared__ int w1[3 * 32 * 16];   // w1t [3][32][64]
-  __shared__ int w2[3 * 16 * 8];    // w2t [3][16][32]
-  __shared__ int w3[3 * 2 * 4];     // w3t [3][2][16]
-  __shared__ int local_s[3 * kMaxCand * 8];  // [3][C][32] int8 as words
-  __shared__ int glob[3 * 8];                 // [3][32] int8 as words
-  __shared__ int8_t stats[kMaxCand * 3];
-  __shared__ int hs[3 * kMaxCand];
-  __shared__ int fused_s[kMaxCand];
-  __shared__ int warn_head;
+__device__ __noinline__ int gelu_exact(int acc, int bias, int sh_in, int sh_out) {
+  return gelu_post((i64)acc + bias, sh_in, sh_out);
+}
 
-  const int b = blockIdx.x, tid = threadIdx.x;
+// requant(gelu(requant(acc + bias, src, -16, 24)), -16, dst, 8).
+__device__ __forceinline__ int sel_gelu(int acc, int bias, bool fast, const Rq &ra, const Rq &rb,
+                                        int sh_in, int sh_out) {
+  if (fast) return rq(gelu_q16(rq(acc + bias, ra)), rb);
+  return gelu_exact(acc, bias, sh_in, sh_out);
+}
+
+__global__ __launch_bounds__(256) void k_selector_head(hv_selector_dev p, const int8_t *tokens,
+                                                       const int32_t *offsets,
+                                                       const uint8_t *pkg_in, int32_t *hs_out,
+                                                       int8_t *stats_out, int fast_shifts,
+                                                       hv_selector_ckpt ck) {
+  __shared__ int wl[32 * 16];   // local_wt[h] [32][64] as int words
+  __shared__ int w1[32 * 16];   // w1t[h] [32][64]
+  __shared__ int w2[16 * 8];    // w2t[h] [16][32]
+  __shared__ int w3[2 * 4];     // w3t[h] [2][16]
+  __shared__ int bl[32], bb1[32], bb2[16];
+  __shared__ int local_s[kMaxCand * 8];  // [C][32] int8 as words
+  __shared__ int glob[8];                 // [32] int8 as words
+  __shared__ int hbuf[12 * 256];          // per thread: h1 (8 words), h2 (4 words)
+
+  const int b = blockIdx.x / 3, h = blockIdx.x - 3 * (blockIdx.x / 3), tid = threadIdx.x;
   const int row0 = offsets[b], N = offsets[b + 1] - row0, C = N - 1;
-  int32_t *st = state + (size_t)b * 5;
   const int pkg = pkg_in ? (pkg_in[b] ? 1 : 0) : 0;
-  if (C < 1 || C > kMaxCand || C - pkg < 1) {
-    // token_selector needs CLS plus one candidate (selector.py:513-514) and
-    // an incoming package needs a normal candidate beside it (:448-449);
-    // the state's token count -1 reports the ValueError.
-    if (tid == 0) { st[0] = -1; st[1] = 0; st[2] = 0; st[3] = 0; st[4] = 0; }
-    return;
-  }
+  if (C < 1 || C > kMaxCand || C - pkg < 1) return;  // reported by k_selector_keep
 
   {
-    const int *src = reinterpret_cast<const int *>(p.local_wt);
-    for (int i = tid; i < 3 * 32 * 16; i += 256) wl[i] = src[i];
-    src = reinterpret_cast<const int *>(p.w1t);
-    for (int i = tid; i < 3 * 32 * 16; i += 256) w1[i] = src[i];
-    src = reinterpret_cast<const int *>(p.w2t);
-    for (int i = tid; i < 3 * 16 * 8; i += 256) w2[i] = src[i];
-    src = reinterpret_cast<const int *>(p.w3t);
-    if (tid < 24) w3[tid] = src[tid];
-    if (tid == 0) warn_head = 0;
+    const int *src = reinterpret_cast<const int *>(p.local_wt) + h * 512;
+    for (int i = tid; i < 512; i += 256) wl[i] = src[i];
+    src = reinterpret_cast<const int *>(p.w1t) + h * 512;
+    for (int i = tid; i < 512; i += 256) w1[i] = src[i];
+    src = reinterpret_cast<const int *>(p.w2t) + h * 128;
+    if (tid < 128) w2[tid] = src[tid];
+    src = reinterpret_cast<const int *>(p.w3t) + h * 8;
+    if (tid < 8) w3[tid] = src[tid];
+    if (tid < 32) bl[tid] = p.local_b[h * 32 + tid];
+    if (tid < 32) bb1[tid] = p.b1[h * 32 + tid];
+    if (tid < 16) bb2[tid] = p.b2[h * 16 + tid];
   }
   __syncthreads();
+  // int32 GELU preconditions: |acc| <= K*2^14 with K = 64 (32 for layer 2).
+  bool fast = fast_shifts != 0;
+  {
+    const int lim64 = (1 << 30) - 1 - 64 * 16384, lim32 = (1 << 30) - 1 - 32 * 16384;
+#pragma unroll 4
+    for (int j = 0; j < 32; ++j)
+      fast = fast && bl[j] <= lim64 && bl[j] >= -lim64 && bb1[j] <= lim64 && bb1[j] >= -lim64;
+#pragma unroll 4
+    for (int j = 0; j < 16; ++j) fast = fast && bb2[j] <= lim32 && bb2[j] >= -lim32;
+  }
 
   const int8_t *cand = tokens + (size_t)(row0 + 1) * 192;
-  // Stage 1: per (head, candidate): local MLP with GELU, and the head lane mean.
+  // Stage 1: local MLP with GELU and the head lane mean.
   {
     const int sh_in = -16 - (p.in_exp + p.local_w_exp), sh_out = p.local_out_exp + 16;
-    for (int q = tid; q < 3 * C; q += 256) {
-      const int h = q / C, c = q - h * C;
+    const Rq ra = rq_setup(sh_in, -(1 << 23), (1 << 23) - 1), rb = rq_setup(sh_out, -128, 127);
+    for (int c = tid; c < C; c += 256) {
       int x[16];
       const v4i *src = reinterpret_cast<const v4i *>(cand + (size_t)c * 192 + h * 64);
 #pragma unroll
@@ -82,38 +102,37 @@ __global__ __launch_bounds__(256) void k_selector_score(hv_selector_dev p, const
       int lane_sum = 0;
 #pragma unroll
       for (int k = 0; k < 16; ++k) lane_sum = dot4(x[k], 0x01010101, lane_sum);
-      stats[c * 3 + h] = (int8_t)sat_bits(round_div_pos(lane_sum, 64), 8);
-      if (ck.head_stats) ck.head_stats[((size_t)b * kMaxCand + c) * 3 + h] = stats[c * 3 + h];
-      int packed[8];
+      const int8_t stat = (int8_t)sat_bits(round_div_pos(lane_sum, 64), 8);
+      stats_out[((size_t)b * kMaxCand + c) * 3 + h] = stat;
+      if (ck.head_stats) ck.head_stats[((size_t)b * kMaxCand + c) * 3 + h] = stat;
+#pragma unroll 1
+      for (int jg = 0; jg < 8; ++jg) {
+        int word = 0;
 #pragma unroll
-      for (int j = 0; j < 32; ++j) {
-        int acc = 0;
-        const int *w = &wl[(h * 32 + j) * 16];
+        for (int jj = 0; jj < 4; ++jj) {
+          const int j = jg * 4 + jj;
+          int acc = 0;
+          const int *w = &wl[j * 16];
 #pragma unroll
-        for (int k = 0; k < 16; ++k) acc = dot4(x[k], w[k], acc);
-        const int v = gelu_post((i64)acc + p.local_b[h * 32 + j], sh_in, sh_out);
-        if ((j & 3) == 0) packed[j >> 2] = 0;
-        packed[j >> 2] |= (v & 0xFF) << (8 * (j & 3));
-      }
-#pragma unroll
-      for (int k = 0; k < 8; ++k) local_s[(h * C + c) * 8 + k] = packed[k];
-      if (ck.local) {
-        int *dst = reinterpret_cast<int *>(ck.local + (((size_t)b * 3 + h) * kMaxCand + c) * 32);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) dst[k] = packed[k];
+          for (int k = 0; k < 16; ++k) acc = dot4(x[k], w[k], acc);
+          const int v = sel_gelu(acc, bl[j], fast, ra, rb, sh_in, sh_out);
+          word |= (v & 0xFF) << (8 * jj);
+        }
+        local_s[c * 8 + jg] = word;
+        if (ck.local)
+          reinterpret_cast<int *>(ck.local + (((size_t)b * 3 + h) * kMaxCand + c) * 32)[jg] = word;
       }
     }
   }
   __syncthreads();
   // Stage 2: global feature = sat8(round_div(sum_c local, C)).
-  if (tid < 96) {
-    const int h = tid >> 5, j = tid & 31;
+  if (tid < 32) {
     const int8_t *l8 = reinterpret_cast<const int8_t *>(local_s);
     int s = 0;
-    for (int c = 0; c < C; ++c) s += l8[(h * C + c) * 32 + j];
+    for (int c = 0; c < C; ++c) s += l8[c * 32 + tid];
     const int8_t gv = (int8_t)sat_bits(round_div_pos(s, C), 8);
-    reinterpret_cast<int8_t *>(glob)[h * 32 + j] = gv;
-    if (ck.global) ck.global[((size_t)b * 3 + h) * 32 + j] = gv;
+    reinterpret_cast<int8_t *>(glob)[tid] = gv;
+    if (ck.global) ck.global[((size_t)b * 3 + h) * 32 + tid] = gv;
   }
   __syncthreads();
   // Stage 3: score MLP on [local | global] and the 2-way selector softmax.
@@ -122,40 +141,56 @@ __global__ __launch_bounds__(256) void k_selector_score(hv_selector_dev p, const
     const int s2_in = -16 - (p.h1_out_exp + p.score_w2_exp), s2_out = p.h2_out_exp + 16;
     const int s3 = p.logits_out_exp - (p.h2_out_exp + p.score_w3_exp);
     const int sq = -16 - p.logits_out_exp;
-    for (int q = tid; q < 3 * C; q += 256) {
-      const int h = q / C, c = q - h * C;
+    const Rq r1a = rq_setup(s1_in, -(1 << 23), (1 << 23) - 1), r1b = rq_setup(s1_out, -128, 127);
+    const Rq r2a = rq_setup(s2_in, -(1 << 23), (1 << 23) - 1), r2b = rq_setup(s2_out, -128, 127);
+    for (int c = tid; c < C; c += 256) {
       int lg[16];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) lg[k] = local_s[(h * C + c) * 8 + k];
+      for (int k = 0; k < 8; ++k) lg[k] = local_s[c * 8 + k];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) lg[8 + k] = glob[h * 8 + k];
+      for (int k = 0; k < 8; ++k) lg[8 + k] = glob[k];
+      int *hb = &hbuf[tid];  // word i of this thread at hb[256 * i]
+#pragma unroll 1
+      for (int jg = 0; jg < 8; ++jg) {
+        int word = 0;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int j = jg * 4 + jj;
+          int acc = 0;
+          const int *w = &w1[j * 16];
+#pragma unroll
+          for (int k = 0; k < 16; ++k) acc = dot4(lg[k], w[k], acc);
+          const int v = sel_gelu(acc, bb1[j], fast, r1a, r1b, s1_in, s1_out);
+          word |= (v & 0xFF) << (8 * jj);
+        }
+        hb[256 * jg] = word;
+      }
       int h1[8];
 #pragma unroll
-      for (int j = 0; j < 32; ++j) {
-        int acc = 0;
-        const int *w = &w1[(h * 32 + j) * 16];
+      for (int k = 0; k < 8; ++k) h1[k] = hb[256 * k];
+#pragma unroll 1
+      for (int jg = 0; jg < 4; ++jg) {
+        int word = 0;
 #pragma unroll
-        for (int k = 0; k < 16; ++k) acc = dot4(lg[k], w[k], acc);
-        const int v = gelu_post((i64)acc + p.b1[h * 32 + j], s1_in, s1_out);
-        if ((j & 3) == 0) h1[j >> 2] = 0;
-        h1[j >> 2] |= (v & 0xFF) << (8 * (j & 3));
+        for (int jj = 0; jj < 4; ++jj) {
+          const int j = jg * 4 + jj;
+          int acc = 0;
+          const int *w = &w2[j * 8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) acc = dot4(h1[k], w[k], acc);
+          const int v = sel_gelu(acc, bb2[j], fast, r2a, r2b, s2_in, s2_out);
+          word |= (v & 0xFF) << (8 * jj);
+        }
+        hb[256 * (8 + jg)] = word;
       }
       int h2[4];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        int acc = 0;
-        const int *w = &w2[(h * 16 + j) * 8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) acc = dot4(h1[k], w[k], acc);
-        const int v = gelu_post((i64)acc + p.b2[h * 16 + j], s2_in, s2_out);
-        if ((j & 3) == 0) h2[j >> 2] = 0;
-        h2[j >> 2] |= (v & 0xFF) << (8 * (j & 3));
-      }
+      for (int k = 0; k < 4; ++k) h2[k] = hb[256 * (8 + k)];
       int qv[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         int acc = 0;
-        const int *w = &w3[(h * 2 + j) * 4];
+        const int *w = &w3[j * 4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) acc = dot4(h2[k], w[k], acc);
         const int logit = (int)requant_shift((i64)acc + p.b3[h * 2 + j], s3, 8);
@@ -164,74 +199,89 @@ __global__ __launch_bounds__(256) void k_selector_score(hv_selector_dev p, const
       const int mx = qv[0] > qv[1] ? qv[0] : qv[1];
       const unsigned e0 = softmax_exp(qv[0] - mx), e1 = softmax_exp(qv[1] - mx);
       const unsigned ratio = softmax_ratio(e1, softmax_recip((u64)e0 + e1));
-      hs[h * C + c] = (int)(ratio > 65536u ? 65536u : ratio);
-      if (ck.head_scores) ck.head_scores[((size_t)b * 3 + h) * kMaxCand + c] = hs[h * C + c];
+      const int hsv = (int)(ratio > 65536u ? 65536u : ratio);
+      hs_out[((size_t)b * 3 + h) * kMaxCand + c] = hsv;
+      if (ck.head_scores) ck.head_scores[((size_t)b * 3 + h) * kMaxCand + c] = hsv;
     }
   }
-  __syncthreads();
-  // Stage 4: head-weight MLP (3->3 GELU, 3->3 PLAN) and the weighted fuse.
-  {
-    const int a_in = -16 - (p.stats_out_exp + p.hw_w1_exp), a_out = p.hw_hidden_out_exp + 16;
-    const int b_sh = -16 - (p.hw_hidden_out_exp + p.hw_w2_exp);
-    for (int c = tid; c < C; c += 256) {
-      int hid[3];
-#pragma unroll
-      for (int j = 0; j < 3; ++j) {
-        int acc = p.hw_b1[j];
-#pragma unroll
-        for (int k = 0; k < 3; ++k) acc += (int)stats[c * 3 + k] * (int)p.hw_w1t[j * 3 + k];
-        hid[j] = gelu_post(acc, a_in, a_out);
-      }
-      i64 num = 0, den = 0;
-      int w[3];
-#pragma unroll
-      for (int j = 0; j < 3; ++j) {
-        i64 acc = p.hw_b2[j];
-#pragma unroll
-        for (int k = 0; k < 3; ++k) acc += (i64)hid[k] * p.hw_w2t[j * 3 + k];
-        w[j] = sat_q016(plan_sigmoid((int)requant_shift(acc, b_sh, 24)));
-        if (ck.head_weights) ck.head_weights[((size_t)b * kMaxCand + c) * 3 + j] = w[j];
-        num += (i64)hs[j * C + c] * w[j];
-        den += w[j];
-      }
-      if (den == 0) {
-        num = (i64)hs[c] + hs[C + c] + hs[2 * C + c];
-        den = 3;
-        atomicOr(&warn_head, 1);
-      }
-      const int f = sat_q016(round_div_pos(num, den));
-      fused_s[c] = f;
-      fused_out[(size_t)b * kMaxCand + c] = f;
-    }
-  }
-  __syncthreads();
-  // The head-fuse warning travels to k_selector_keep in the state word.
-  if (tid == 0) st[4] = warn_head;
 }
 
-// Stable keep list of the normal candidates (fused >= 32768, input order)
-// and the per-image state {token_count, package_present, kept, pruned,
-// warnings} (selector.py:456-500).  One wavefront per image.
+// Head fuse of one candidate (selector.py:370-418): head-weight MLP (3->3
+// GELU, 3->3 PLAN) on the head statistics and the weighted mean of the head
+// scores; *warn is set when the weights sum to zero (plain mean then).
+__device__ int fuse_candidate(const hv_selector_dev &p, const int8_t *stats, const int32_t *hs,
+                              int C, int c, int32_t *weights_out, bool *warn) {
+  const int a_in = -16 - (p.stats_out_exp + p.hw_w1_exp), a_out = p.hw_hidden_out_exp + 16;
+  const int b_sh = -16 - (p.hw_hidden_out_exp + p.hw_w2_exp);
+  int hid[3];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    int acc = p.hw_b1[j];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) acc += (int)stats[k] * (int)p.hw_w1t[j * 3 + k];
+    hid[j] = gelu_post(acc, a_in, a_out);
+  }
+  i64 num = 0, den = 0;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    i64 acc = p.hw_b2[j];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) acc += (i64)hid[k] * p.hw_w2t[j * 3 + k];
+    const int w = sat_q016(plan_sigmoid((int)requant_shift(acc, b_sh, 24)));
+    if (weights_out) weights_out[j] = w;
+    num += (i64)hs[j * kMaxCand] * w;
+    den += w;
+  }
+  *warn = den == 0;
+  if (den == 0) {
+    num = (i64)hs[0] + hs[kMaxCand] + hs[2 * kMaxCand];
+    den = 3;
+  }
+  return sat_q016(round_div_pos(num, den));
+}
+
+// Optional head fuse, then the stable keep list of the normal candidates
+// (fused >= 32768, input order) and the per-image state {token_count,
+// package_present, kept, pruned, warnings} (selector.py:456-500).  One
+// wavefront per image.
 __global__ __launch_bounds__(64) void k_selector_keep(const int32_t *offsets,
-                                                      const uint8_t *pkg_in,
-                                                      const int32_t *fused, int32_t *kept_index,
-                                                      int32_t *state, int head_warn_in_state) {
+                                                      const uint8_t *pkg_in, int32_t *fused,
+                                                      int32_t *kept_index, int32_t *state,
+                                                      hv_selector_dev p, const int32_t *hs,
+                                                      const int8_t *stats, int32_t *weights_ck) {
   const int b = blockIdx.x, lane = threadIdx.x;
   const int C = offsets[b + 1] - offsets[b] - 1;
   const int pkg = pkg_in ? (pkg_in[b] ? 1 : 0) : 0;
   int32_t *st = state + (size_t)b * 5;
   if (C < 1 || C > kMaxCand || C - pkg < 1) {
+    // token_selector needs CLS plus one candidate (selector.py:513-514) and
+    // an incoming package needs a normal candidate beside it (:448-449);
+    // the state's token count -1 reports the ValueError.
     if (lane == 0) { st[0] = -1; st[1] = 0; st[2] = 0; st[3] = 0; st[4] = 0; }
     return;
   }
-  const int32_t *f = fused + (size_t)b * kMaxCand;
+  int32_t *f = fused + (size_t)b * kMaxCand;
   const int n_norm = C - pkg;
   int kept = 0;
   i64 den = 0;
+  bool warn_any = false;
   for (int base = 0; base < C; base += 64) {
     const int c = base + lane;
     const bool in = c < C;
-    const int fc = in ? f[c] : 0;
+    int fc = 0;
+    if (hs) {
+      if (in) {
+        bool warn = false;
+        fc = fuse_candidate(p, stats + ((size_t)b * kMaxCand + c) * 3,
+                            hs + (size_t)b * 3 * kMaxCand + c, C, c,
+                            weights_ck ? weights_ck + ((size_t)b * kMaxCand + c) * 3 : nullptr,
+                            &warn);
+        warn_any = warn_any || warn;
+        f[c] = fc;
+      }
+    } else {
+      fc = in ? f[c] : 0;
+    }
     const bool is_norm = c < n_norm;
     const bool keep = is_norm && fc >= 32768;
     const bool part = (is_norm && !keep) || (pkg && c == C - 1);
@@ -245,15 +295,15 @@ __global__ __launch_bounds__(64) void k_selector_keep(const int32_t *offsets,
     den += d;
   }
   for (int i = kept + lane; i < kMaxCand; i += 64) kept_index[(size_t)b * kMaxCand + i] = -1;
+  const bool warn_head = __ballot(warn_any) != 0;
   if (lane == 0) {
-    const int warn_head = head_warn_in_state ? (st[4] & 1) : 0;
     const int n_part = C - kept;  // pruned normals + the incoming package
     const int exists = n_part > 0;
     st[0] = 1 + kept + exists;
     st[1] = exists;
     st[2] = kept;
     st[3] = n_part - pkg;
-    st[4] = warn_head | ((exists && den == 0) ? 2 : 0);
+    st[4] = (warn_head ? 1 : 0) | ((exists && den == 0) ? 2 : 0);
   }
 }
 
@@ -322,13 +372,21 @@ __global__ __launch_bounds__(256) void k_selector_compact(
 int launch_selector(const SelectorArgs &a, hipStream_t s) {
   if (a.batch <= 0) return HV_OK;
   int rc = HV_OK;
+  hv_selector_dev p{};
   if (a.p) {
-    hipLaunchKernelGGL(k_selector_score, dim3(a.batch), dim3(256), 0, s, *a.p, a.tokens,
-                       a.offsets, a.pkg_in, a.fused, a.kept_index, a.state, a.ck);
-    if ((rc = check_hip(hipGetLastError(), "k_selector_score launch"))) return rc;
+    if (!a.hs || !a.stats) return fail(HV_EVALUE, "selector: missing workspace");
+    p = *a.p;
+    auto in = [](int v) { return v >= -30 && v <= 30; };
+    const int fast = in(-16 - (p.in_exp + p.local_w_exp)) && in(p.local_out_exp + 16) &&
+                     in(-16 - (p.concat_out_exp + p.score_w1_exp)) && in(p.h1_out_exp + 16) &&
+                     in(-16 - (p.h1_out_exp + p.score_w2_exp)) && in(p.h2_out_exp + 16);
+    hipLaunchKernelGGL(k_selector_head, dim3(a.batch * 3), dim3(256), 0, s, p, a.tokens,
+                       a.offsets, a.pkg_in, a.hs, a.stats, fast, a.ck);
+    if ((rc = check_hip(hipGetLastError(), "k_selector_head launch"))) return rc;
   }
   hipLaunchKernelGGL(k_selector_keep, dim3(a.batch), dim3(64), 0, s, a.offsets, a.pkg_in,
-                     a.fused, a.kept_index, a.state, a.p ? 1 : 0);
+                     a.fused, a.kept_index, a.state, p, a.p ? a.hs : nullptr,
+                     a.p ? a.stats : nullptr, a.p ? a.ck.head_weights : nullptr);
   if ((rc = check_hip(hipGetLastError(), "k_selector_keep launch"))) return rc;
   hipLaunchKernelGGL(k_selector_compact, dim3(a.batch), dim3(256), 0, s, a.tokens, a.offsets,
                      a.pkg_in, a.batch, a.fused, a.kept_index, a.state, a.out_tokens,

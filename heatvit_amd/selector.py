@@ -93,10 +93,11 @@ def token_selector_batch(token_sets, package_flags, params):
     ck = _lib.SelectorCkpt(*[ck_bufs[k].data_ptr() for k in (
         "local", "global_", "head_scores", "head_stats", "head_weights")])
     L = _lib.lib()
+    ws = torch.empty(max(1, L.hv_selector_workspace_bytes(b)), dtype=torch.uint8, device="cuda")
     _lib.check(L.hv_selector_forward(dev.struct, dev_in.data_ptr(), off.data_ptr(),
                                      pkg_in.data_ptr(), b, out.data_ptr(), out_off.data_ptr(),
                                      pkg_out.data_ptr(), fused.data_ptr(), kept.data_ptr(),
-                                     state.data_ptr(), ck, None, 0, _stream()),
+                                     state.data_ptr(), ck, ws.data_ptr(), ws.numel(), _stream()),
                "token_selector")
     out, out_off = out.cpu().numpy(), out_off.cpu().numpy()
     fused, kept, state = fused.cpu().numpy(), kept.cpu().numpy(), state.cpu().numpy()
