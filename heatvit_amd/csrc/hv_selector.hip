@@ -125,11 +125,20 @@ __global__ __launch_bounds__(256) void k_selector_head(hv_selector_dev p, const 
     }
   }
   __syncthreads();
-  // Stage 2: global feature = sat8(round_div(sum_c local, C)).
-  if (tid < 32) {
+  // Stage 2: global feature = sat8(round_div(sum_c local, C)); eight
+  // partial sums per channel, then one thread per channel.
+  {
     const int8_t *l8 = reinterpret_cast<const int8_t *>(local_s);
+    const int ch = tid & 31, part = tid >> 5;
     int s = 0;
-    for (int c = 0; c < C; ++c) s += l8[c * 32 + tid];
+    for (int c = part; c < C; c += 8) s += l8[c * 32 + ch];
+    hbuf[tid] = s;
+  }
+  __syncthreads();
+  if (tid < 32) {
+    int s = 0;
+#pragma unroll
+    for (int part = 0; part < 8; ++part) s += hbuf[part * 32 + tid];
     const int8_t gv = (int8_t)sat_bits(round_div_pos(s, C), 8);
     reinterpret_cast<int8_t *>(glob)[tid] = gv;
     if (ck.global) ck.global[((size_t)b * 3 + h) * 32 + tid] = gv;
@@ -343,8 +352,14 @@ __global__ __launch_bounds__(256) void k_selector_compact(
         reinterpret_cast<const v4i *>(tokens + (size_t)src * 192)[chunk];
   }
   if (!exists) return;
+  // Package row: num[ch] = sum over partitioned candidates of w_c * x_c[ch]
+  // with w_c = fused score (or 1 when the scores sum to zero).  |num| <=
+  // 196 * 65536 * 128 < 2^31.  Thread (channel group of 16, candidate
+  // group g) accumulates candidates g, g + 21, ...; LDS sums the groups.
   const int32_t *f = fused + (size_t)b * kMaxCand;
   const int n_norm = C - pkg;
+  __shared__ int wgt[kMaxCand];
+  __shared__ int part_sum[21 * 192];
   if (tid < 64) {
     long long d = 0;
     for (int c = tid; c < C; c += 64) {
@@ -356,14 +371,33 @@ __global__ __launch_bounds__(256) void k_selector_compact(
   }
   __syncthreads();
   const long long den = den_s;
+  for (int c = tid; c < C; c += 256) {
+    const bool part = (c < n_norm && f[c] < 32768) || (pkg && c == C - 1);
+    wgt[c] = part ? (den == 0 ? 1 : f[c]) : 0;
+  }
+  __syncthreads();
+  if (tid < 12 * 21) {
+    const int cg = tid / 12, chg = tid - cg * 12;
+    int acc[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = 0;
+    const int8_t *cand = tokens + (size_t)(row0 + 1) * 192 + chg * 16;
+    for (int c = cg; c < C; c += 21) {
+      const int w = wgt[c];
+      if (w == 0) continue;
+      const v4i v = *reinterpret_cast<const v4i *>(cand + (size_t)c * 192);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[j] += w * (int)(int8_t)(v[j >> 2] >> (8 * (j & 3)));
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) part_sum[cg * 192 + chg * 16 + j] = acc[j];
+  }
+  __syncthreads();
   const int n_part = C - kept;
   if (tid < 192) {
-    long long num = 0;
-    const int8_t *cand = tokens + (size_t)(row0 + 1) * 192 + tid;
-    for (int c = 0; c < C; ++c) {
-      const bool part = (c < n_norm && f[c] < 32768) || (pkg && c == C - 1);
-      if (part) num += (den == 0 ? 1ll : (long long)f[c]) * cand[(size_t)c * 192];
-    }
+    int num = 0;
+#pragma unroll
+    for (int g = 0; g < 21; ++g) num += part_sum[g * 192 + tid];
     out[(size_t)(out0 + 1 + kept) * 192 + tid] =
         (int8_t)sat_bits(round_div_pos(num, den == 0 ? n_part : den), 8);
   }
