@@ -45,7 +45,8 @@ enum { EPI_I8 = HV_EPI_I8, EPI_I32 = HV_EPI_I32, EPI_GELU = HV_EPI_GELU,
 static constexpr int kPatchesPerImage = 196;
 static constexpr int kTokens = 197;
 static constexpr int kImageBytes = 224 * 224 * 3;
-static constexpr int kGridCap = 256 * 8;  // workgroups: 256 CUs x 8 resident
+static constexpr int kGridCap = 256 * 8;     // workgroups: 256 CUs x 8 resident
+static constexpr int kLdsGridCap = 256 * 2;  // LDS-staged kernel: 2 per CU
 
 template <int AMODE>
 __device__ __forceinline__ const int8_t *a_row(const GemmArgs &g, int r) {
@@ -82,6 +83,148 @@ __device__ __noinline__ v2i epi_exact(int epi, int acc, int bias, int res, int s
 __device__ __forceinline__ int pack4(int a, int b, int c, int d) {
   return (int)((unsigned)(a & 0xFF) | ((unsigned)(b & 0xFF) << 8) | ((unsigned)(c & 0xFF) << 16) |
                ((unsigned)d << 24));
+}
+
+
+// Epilogue operands that do not depend on the product: the 16 biases of
+// each column tile this lane finishes and, for the residual forms, the 16
+// residual (or position) bytes of each of its rows.
+template <int MT, int NT, int EPI>
+__device__ __forceinline__ void epi_operands(const GemmArgs &g, const int (&arow)[MT], int ct0,
+                                             int h, v4i (&bias4)[NT][4], v4i (&res4)[MT][NT]) {
+  constexpr bool RESLIKE = EPI == EPI_RES || EPI == EPI_PATCH;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int c0 = (ct0 + nt) * 32 + 16 * h;
+    if (g.bias && c0 + 16 <= g.n) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) bias4[nt][q] = *reinterpret_cast<const v4i *>(g.bias + c0 + 4 * q);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        bias4[nt][j >> 2][j & 3] = g.bias && c0 + j < g.n ? g.bias[c0 + j] : 0;
+    }
+  }
+  if constexpr (RESLIKE) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int c0 = (ct0 + nt) * 32 + 16 * h;
+        const int8_t *rp;
+        if (EPI == EPI_RES) {
+          rp = g.res + (size_t)arow[mt] * g.ldr + c0;
+        } else {
+          const int p = arow[mt] % kPatchesPerImage;
+          rp = g.pos + (size_t)(p + 1) * 192 + c0;
+        }
+        if (g.vec_res && c0 + 16 <= g.n) {
+          res4[mt][nt] = *reinterpret_cast<const v4i *>(rp);
+        } else {
+          int w[4] = {0, 0, 0, 0};
+          for (int j = 0; j < 16 && c0 + j < g.n; ++j) w[j >> 2] |= ((int)rp[j] & 0xFF) << (8 * (j & 3));
+          res4[mt][nt] = v4i{w[0], w[1], w[2], w[3]};
+        }
+      }
+  }
+}
+
+// Epilogue of one wavefront tile: lane l finishes row r0 + 32*mt + l%32,
+// channels c0 .. c0+15 of each column tile.
+template <int MT, int NT, int EPI, bool FAST>
+__device__ __forceinline__ void epi_tile(const GemmArgs &g, const v16i (&acc)[MT][NT],
+                                         const v4i (&bias4)[NT][4], const v4i (&res4)[MT][NT],
+                                         int r0, int ct0, int M, int h, int l32, const Rq &rq_a,
+                                         const Rq &rq_b) {
+  constexpr bool RESLIKE = EPI == EPI_RES || EPI == EPI_PATCH;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int c0 = (ct0 + nt) * 32 + 16 * h;
+    bool narrow = FAST;
+    if (FAST) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int b = bias4[nt][j >> 2][j & 3];
+        narrow = narrow && b <= g.acc_lim && b >= -g.acc_lim;
+      }
+    }
+    // Uniform per wavefront: the int32 form only when every lane qualifies.
+    const bool fast = FAST && __all(narrow);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int row = r0 + mt * 32 + l32;
+      if (row >= M || c0 >= g.n) continue;
+      size_t orow = (size_t)row;
+      if (EPI == EPI_PATCH) {
+        const int b = row / kPatchesPerImage;
+        orow = (size_t)b * kTokens + 1 + (row - b * kPatchesPerImage);
+      }
+      int o[16], mid[16];
+      if (fast) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int v = acc[mt][nt][j] + bias4[nt][j >> 2][j & 3];
+          if (EPI == EPI_I8) {
+            o[j] = rq(v, rq_a);
+          } else if (EPI == EPI_GELU) {
+            o[j] = rq(gelu_q16(rq(v, rq_a)), rq_b);
+          } else if (RESLIKE) {
+            const int t8 = rq(v, rq_a);
+            const int r8 = (int)(int8_t)(res4[mt][nt][j >> 2] >> (8 * (j & 3)));
+            const int s = EPI == EPI_RES ? r8 * (1 << g.da) + t8 * (1 << g.db)
+                                         : t8 * (1 << g.da) + r8 * (1 << g.db);
+            mid[j] = t8;
+            o[j] = rq(s, rq_b);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int r8 = RESLIKE ? (int)(int8_t)(res4[mt][nt][j >> 2] >> (8 * (j & 3))) : 0;
+          const v2i r = epi_exact(EPI, acc[mt][nt][j], bias4[nt][j >> 2][j & 3], r8, g.shift_a,
+                                  g.shift_b, g.da, g.db, g.os);
+          o[j] = r[0];
+          mid[j] = r[1];
+        }
+      }
+      const bool full = g.vec_out && c0 + 16 <= g.n;
+      if (EPI == EPI_I32) {
+        int32_t *cp = reinterpret_cast<int32_t *>(g.c) + orow * g.ldc + c0;
+        if (full) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<v4i *>(cp + 4 * q) = v4i{o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
+        } else {
+#pragma unroll
+          for (int j = 0; j < 16; ++j)
+            if (c0 + j < g.n) cp[j] = o[j];
+        }
+      } else {
+        int8_t *cp = reinterpret_cast<int8_t *>(g.c) + orow * g.ldc + c0;
+        if (full) {
+          *reinterpret_cast<v4i *>(cp) = v4i{pack4(o[0], o[1], o[2], o[3]), pack4(o[4], o[5], o[6], o[7]),
+                                             pack4(o[8], o[9], o[10], o[11]),
+                                             pack4(o[12], o[13], o[14], o[15])};
+        } else {
+#pragma unroll
+          for (int j = 0; j < 16; ++j)
+            if (c0 + j < g.n) cp[j] = (int8_t)o[j];
+        }
+        if (EPI == EPI_RES && g.aux) {
+          int8_t *xp = g.aux + orow * g.ldc + c0;
+          if (full) {
+            *reinterpret_cast<v4i *>(xp) =
+                v4i{pack4(mid[0], mid[1], mid[2], mid[3]), pack4(mid[4], mid[5], mid[6], mid[7]),
+                    pack4(mid[8], mid[9], mid[10], mid[11]), pack4(mid[12], mid[13], mid[14], mid[15])};
+          } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+              if (c0 + j < g.n) xp[j] = (int8_t)mid[j];
+          }
+        }
+      }
+    }
+  }
 }
 
 template <int MT, int NT, int WM, int EPI, int AMODE, int KTC, bool FAST>
@@ -134,43 +277,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
       return *reinterpret_cast<const v4i *>(bp[nt] + kt * 1024);
     };
 
-    // Epilogue operands that do not depend on the product.
-    v4i bias4[NT][4];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int c0 = (ct0 + nt) * 32 + 16 * h;
-      if (g.bias && c0 + 16 <= g.n) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) bias4[nt][q] = *reinterpret_cast<const v4i *>(g.bias + c0 + 4 * q);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-          bias4[nt][j >> 2][j & 3] = g.bias && c0 + j < g.n ? g.bias[c0 + j] : 0;
-      }
-    }
-    v4i res4[MT][NT];
-    if constexpr (RESLIKE) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          const int c0 = (ct0 + nt) * 32 + 16 * h;
-          const int8_t *rp;
-          if (EPI == EPI_RES) {
-            rp = g.res + (size_t)arow[mt] * g.ldr + c0;
-          } else {
-            const int p = arow[mt] % kPatchesPerImage;
-            rp = g.pos + (size_t)(p + 1) * 192 + c0;
-          }
-          if (g.vec_res && c0 + 16 <= g.n) {
-            res4[mt][nt] = *reinterpret_cast<const v4i *>(rp);
-          } else {
-            int w[4] = {0, 0, 0, 0};
-            for (int j = 0; j < 16 && c0 + j < g.n; ++j) w[j >> 2] |= ((int)rp[j] & 0xFF) << (8 * (j & 3));
-            res4[mt][nt] = v4i{w[0], w[1], w[2], w[3]};
-          }
-        }
-    }
+    v4i bias4[NT][4], res4[MT][NT];
+    epi_operands<MT, NT, EPI>(g, arow, ct0, h, bias4, res4);
 
     v16i acc[MT][NT];
 #pragma unroll
@@ -256,95 +364,126 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
       }
     }
 
-    // Epilogue: lane l finishes row r0 + 32*mt + l%32, channels c0 .. c0+15.
+    epi_tile<MT, NT, EPI, FAST>(g, acc, bias4, res4, r0, ct0, M, h, l32, rq_a, rq_b);
+  }
+}
+
+// A staged through LDS: for K = 192*NCH the A tile is brought in by K-chunks
+// of 192 bytes (6 MFMA K-steps) with fully coalesced 16-byte loads (12
+// threads per row), double-buffered in LDS at a 208-byte row stride
+// (conflict-free fragment reads).  The next chunk -- or the next tile's
+// first chunk -- and its weight fragments are loaded while the current
+// chunk's MFMAs run; one barrier per chunk.
+template <int MT, int NT, int WM, int EPI, int AMODE, int KTC, bool FAST>
+__global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g, int n_blocks) {
+  constexpr int WN = 4 / WM, BM = 32 * MT * WM, BT = NT * WN;
+  constexpr int KC = 6, NCH = KTC / KC, ROW = 208;
+  constexpr int PIECES = BM * 12, PPT = PIECES / 256;
+  static_assert(KTC % KC == 0 && PIECES % 256 == 0, "tile / K shape");
+  __shared__ __attribute__((aligned(16))) int8_t As[2][BM * ROW];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave - wm * WN;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int M = g.m_dev ? min(*g.m_dev, g.m) : g.m;
+  if (M <= 0) return;
+  const int T = ((M + BM - 1) / BM) * n_blocks;
+  const int T8 = (T + 7) >> 3;
+  const int n32t = (g.n + 31) >> 5;
+  const Rq rq_a = rq_setup(g.shift_a, EPI == EPI_GELU ? -(1 << 23) : -128,
+                           EPI == EPI_GELU ? (1 << 23) - 1 : 127);
+  const Rq rq_b = rq_setup(EPI == EPI_GELU ? g.shift_b : g.os, -128, 127);
+  // The grid is a multiple of 8, so t & 7 (the XCD) is fixed per workgroup;
+  // XCD x works through logical tiles [x*T8, (x+1)*T8) in order, so the
+  // first out-of-range tile ends the sequence.
+  auto logical = [&](int t) { return t < 8 * T8 ? (t & 7) * T8 + (t >> 3) : T; };
+
+  int t = blockIdx.x;
+  int L = logical(t);
+  if (L >= T) return;
+
+  v4i apre[PPT];
+  v4i bcur[NT][KC], bnext[NT][KC];
+  auto load_step = [&](int Ls, int c) {
+    const int mb = Ls / n_blocks, nb = Ls - mb * n_blocks;
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int i = tid + j * 256, pr = i / 12, pc = i - pr * 12;
+      const int r = min(mb * BM + pr, M - 1);
+      const int8_t *src = AMODE == A_PATCH ? patch_ptr(g.a, r, c * 192 + pc * 16)
+                                           : g.a + (size_t)r * g.lda + c * 192 + pc * 16;
+      apre[j] = *reinterpret_cast<const v4i *>(src);
+    }
+    const int ct0 = nb * BT + wn * NT;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const int c0 = (ct0 + nt) * 32 + 16 * h;
-      bool narrow = FAST;
-      if (FAST) {
+      const int8_t *bp = g.b + ((size_t)min(ct0 + nt, n32t - 1) * KTC + c * KC) * 1024 + lane * 16;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int b = bias4[nt][j >> 2][j & 3];
-          narrow = narrow && b <= g.acc_lim && b >= -g.acc_lim;
-        }
-      }
-      // Uniform per wavefront: the int32 form only when every lane qualifies.
-      const bool fast = FAST && __all(narrow);
+      for (int kt = 0; kt < KC; ++kt) bnext[nt][kt] = *reinterpret_cast<const v4i *>(bp + kt * 1024);
+    }
+  };
+  auto tile_rows = [&](int Ls, int (&arow)[MT], int &r0, int &ct0) {
+    const int mb = Ls / n_blocks, nb = Ls - mb * n_blocks;
+    r0 = mb * BM + wm * 32 * MT;
+    ct0 = nb * BT + wn * NT;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) arow[mt] = min(r0 + mt * 32 + l32, M - 1);
+  };
+
+  int arow[MT], r0, ct0;
+  tile_rows(L, arow, r0, ct0);
+  v4i bias4[NT][4], res4[MT][NT];
+  epi_operands<MT, NT, EPI>(g, arow, ct0, h, bias4, res4);
+  load_step(L, 0);
+  v16i acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v16i{0};
+
+  int c = 0, buf = 0;
+  while (true) {
+    int8_t *Ab = As[buf];
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int i = tid + j * 256, pr = i / 12, pc = i - pr * 12;
+      *reinterpret_cast<v4i *>(Ab + pr * ROW + pc * 16) = apre[j];
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int kt = 0; kt < KC; ++kt) bcur[nt][kt] = bnext[nt][kt];
+    __syncthreads();
+    // Next step: the following chunk of this tile or the next tile's first.
+    const bool last_chunk = c == NCH - 1;
+    const int Ln = last_chunk ? logical(t + (int)gridDim.x) : L;
+    const int cn = last_chunk ? 0 : c + 1;
+    const bool more = Ln < T;
+    if (more) load_step(Ln, cn);
+#pragma unroll
+    for (int kt = 0; kt < KC; ++kt)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const int row = r0 + mt * 32 + l32;
-        if (row >= M || c0 >= g.n) continue;
-        size_t orow = (size_t)row;
-        if (EPI == EPI_PATCH) {
-          const int b = row / kPatchesPerImage;
-          orow = (size_t)b * kTokens + 1 + (row - b * kPatchesPerImage);
-        }
-        int o[16], mid[16];
-        if (fast) {
+        const v4i af = *reinterpret_cast<const v4i *>(Ab + (wm * 32 * MT + mt * 32 + l32) * ROW +
+                                                      kt * 32 + 16 * h);
 #pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int v = acc[mt][nt][j] + bias4[nt][j >> 2][j & 3];
-            if (EPI == EPI_I8) {
-              o[j] = rq(v, rq_a);
-            } else if (EPI == EPI_GELU) {
-              o[j] = rq(gelu_q16(rq(v, rq_a)), rq_b);
-            } else if (RESLIKE) {
-              const int t8 = rq(v, rq_a);
-              const int r8 = (int)(int8_t)(res4[mt][nt][j >> 2] >> (8 * (j & 3)));
-              const int s = EPI == EPI_RES ? r8 * (1 << g.da) + t8 * (1 << g.db)
-                                           : t8 * (1 << g.da) + r8 * (1 << g.db);
-              mid[j] = t8;
-              o[j] = rq(s, rq_b);
-            }
-          }
-        } else {
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int r8 = RESLIKE ? (int)(int8_t)(res4[mt][nt][j >> 2] >> (8 * (j & 3))) : 0;
-            const v2i r = epi_exact(EPI, acc[mt][nt][j], bias4[nt][j >> 2][j & 3], r8, g.shift_a,
-                                    g.shift_b, g.da, g.db, g.os);
-            o[j] = r[0];
-            mid[j] = r[1];
-          }
-        }
-        const bool full = g.vec_out && c0 + 16 <= g.n;
-        if (EPI == EPI_I32) {
-          int32_t *cp = reinterpret_cast<int32_t *>(g.c) + orow * g.ldc + c0;
-          if (full) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-              *reinterpret_cast<v4i *>(cp + 4 * q) = v4i{o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
-          } else {
-#pragma unroll
-            for (int j = 0; j < 16; ++j)
-              if (c0 + j < g.n) cp[j] = o[j];
-          }
-        } else {
-          int8_t *cp = reinterpret_cast<int8_t *>(g.c) + orow * g.ldc + c0;
-          if (full) {
-            *reinterpret_cast<v4i *>(cp) = v4i{pack4(o[0], o[1], o[2], o[3]), pack4(o[4], o[5], o[6], o[7]),
-                                               pack4(o[8], o[9], o[10], o[11]),
-                                               pack4(o[12], o[13], o[14], o[15])};
-          } else {
-#pragma unroll
-            for (int j = 0; j < 16; ++j)
-              if (c0 + j < g.n) cp[j] = (int8_t)o[j];
-          }
-          if (EPI == EPI_RES && g.aux) {
-            int8_t *xp = g.aux + orow * g.ldc + c0;
-            if (full) {
-              *reinterpret_cast<v4i *>(xp) =
-                  v4i{pack4(mid[0], mid[1], mid[2], mid[3]), pack4(mid[4], mid[5], mid[6], mid[7]),
-                      pack4(mid[8], mid[9], mid[10], mid[11]), pack4(mid[12], mid[13], mid[14], mid[15])};
-            } else {
-#pragma unroll
-              for (int j = 0; j < 16; ++j)
-                if (c0 + j < g.n) xp[j] = (int8_t)mid[j];
-            }
-          }
-        }
+        for (int nt = 0; nt < NT; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bcur[nt][kt], af, acc[mt][nt], 0, 0, 0);
       }
+    if (last_chunk) {
+      epi_tile<MT, NT, EPI, FAST>(g, acc, bias4, res4, r0, ct0, M, h, l32, rq_a, rq_b);
+      if (!more) break;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v16i{0};
+      t += gridDim.x;
+      tile_rows(Ln, arow, r0, ct0);
+      epi_operands<MT, NT, EPI>(g, arow, ct0, h, bias4, res4);
     }
+    L = Ln;
+    c = cn;
+    buf ^= 1;
   }
 }
 
@@ -397,27 +536,44 @@ static int run(const GemmArgs &g, hipStream_t s) {
   return check_hip(hipGetLastError(), "k_gemm launch");
 }
 
-// Tile shapes: 128x64 output tiles (two 32-row tiles per wavefront) for the
-// epilogues with few operations per element, 64x64 for GELU, whose
-// epilogue holds more registers.  K = 192 and K = 768 get compile-time K
-// loops; other K (the generic entry point) the runtime loop.
+template <int MT, int NT, int WM, int EPI, int AMODE, int KTC>
+static int run_lds(const GemmArgs &g, hipStream_t s) {
+  constexpr int BM = 32 * MT * WM, BN = 32 * NT * (4 / WM);
+  const int n_blocks = (g.n + BN - 1) / BN;
+  const long long tiles = (long long)((g.m + BM - 1) / BM) * n_blocks;
+  if (tiles <= 0) return HV_OK;
+  long long grid = (tiles + 7) / 8 * 8;
+  if (grid > kLdsGridCap) grid = kLdsGridCap;
+  if (fast_epilogue(g, EPI))
+    hipLaunchKernelGGL((k_gemm_lds<MT, NT, WM, EPI, AMODE, KTC, true>), dim3((unsigned)grid),
+                       dim3(256), 0, s, g, n_blocks);
+  else
+    hipLaunchKernelGGL((k_gemm_lds<MT, NT, WM, EPI, AMODE, KTC, false>), dim3((unsigned)grid),
+                       dim3(256), 0, s, g, n_blocks);
+  return check_hip(hipGetLastError(), "k_gemm_lds launch");
+}
+
+// Shapes (measured at 50432 rows): K = 192 GEMMs use the direct kernel with
+// 128x64 tiles (64x64 for GELU, whose epilogue holds more registers); K =
+// 768 (FFN2, patch embedding) the LDS-staged kernel with 128x64 tiles and
+// two workgroups per CU; other K and the gathered head rows the runtime-K
+// direct kernel.
 template <int EPI>
 static int dispatch(const GemmArgs &g, int a_mode, hipStream_t s) {
-  if (a_mode == A_PATCH) {
-    if (EPI != EPI_PATCH || g.k != 768) return fail(HV_EVALUE, "gemm: bad patch GEMM");
-    return run<2, 1, 2, EPI_PATCH, A_PATCH, 24>(g, s);
-  }
-  if (EPI == EPI_PATCH) return fail(HV_EVALUE, "gemm: patch epilogue needs the patch gather");
-  if (a_mode == A_GATHER) return run<1, 1, 2, EPI, A_GATHER, 0>(g, s);
-  if (a_mode != A_ROWS) return fail(HV_EVALUE, "gemm: bad A mode %d", a_mode);
-  if (EPI == EPI_GELU) {
-    if (g.k == 192) return run<1, 1, 2, EPI, A_ROWS, 6>(g, s);
-    if (g.k == 768) return run<1, 1, 2, EPI, A_ROWS, 24>(g, s);
+  if constexpr (EPI == EPI_PATCH) {
+    if (a_mode != A_PATCH || g.k != 768) return fail(HV_EVALUE, "gemm: bad patch GEMM");
+    return run_lds<2, 1, 2, EPI_PATCH, A_PATCH, 24>(g, s);
+  } else {
+    if (a_mode == A_GATHER) return run<1, 1, 2, EPI, A_GATHER, 0>(g, s);
+    if (a_mode != A_ROWS) return fail(HV_EVALUE, "gemm: bad A mode %d", a_mode);
+    if constexpr (EPI == EPI_GELU) {
+      if (g.k == 192) return run<1, 1, 2, EPI, A_ROWS, 6>(g, s);
+    } else if constexpr (EPI != EPI_I32) {
+      if (g.k == 192) return run<2, 1, 2, EPI, A_ROWS, 6>(g, s);
+      if (g.k == 768) return run_lds<2, 1, 2, EPI, A_ROWS, 24>(g, s);
+    }
     return run<1, 1, 2, EPI, A_ROWS, 0>(g, s);
   }
-  if (g.k == 192) return run<2, 1, 2, EPI, A_ROWS, 6>(g, s);
-  if (g.k == 768) return run<2, 1, 2, EPI, A_ROWS, 24>(g, s);
-  return run<1, 1, 2, EPI, A_ROWS, 0>(g, s);
 }
 
 int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
