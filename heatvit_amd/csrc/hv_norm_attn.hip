@@ -287,7 +287,10 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
   __syncthreads();
 
   const int ql = lane & 15, grp = lane >> 4;
-  for (int qt = wave; qt < n16; qt += 4) {
+  // Query tiles round-robin over the wavefronts, rotated by workgroup so
+  // the wavefront that gets the extra tile sits on a different SIMD in
+  // neighbouring workgroups.
+  for (int qt = (wave + blockIdx.x) & 3; qt < n16; qt += 4) {
     const int q = qt * 16 + ql;  // this lane's query
     v4i qb = v4i{0};
     if (q < N) qb = *reinterpret_cast<const v4i *>(qkv + (size_t)q * 576 + h * 64 + grp * 16);
@@ -301,13 +304,13 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int key = kt * 16 + 4 * grp + i;
-          const int v = attn_q16<MODE>(st[i], g);
+          // Padded keys get -2^30: below every q16 value, and their
+          // exponential is exactly zero (z > 31), so the later passes need no mask.
+          const int v = key < N ? attn_q16<MODE>(st[i], g) : -(1 << 30);
           val[kt][i] = v;
-          if (key < N) {
-            mx = v > mx ? v : mx;
-            if (CKPT && g.score && q < N)
-              g.score[(((size_t)b * 3 + h) * 197 + q) * 197 + key] = attn_score_ckpt(st[i], g.score_shift);
-          }
+          mx = v > mx ? v : mx;
+          if (CKPT && g.score && q < N && key < N)
+            g.score[(((size_t)b * 3 + h) * 197 + q) * 197 + key] = attn_score_ckpt(st[i], g.score_shift);
         }
       }
     }
@@ -319,8 +322,7 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
       if (kt < n16) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int key = kt * 16 + 4 * grp + i;
-          const unsigned e = key < N ? softmax_exp(val[kt][i] - mx) : 0u;
+          const unsigned e = softmax_exp(val[kt][i] - mx);
           val[kt][i] = (int)e;
           sum += e;
         }
@@ -335,20 +337,22 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int kt = kc * 4 + t;
-        unsigned whi = 0, wlo = 0;
+        unsigned w = 0;
         if (kt < 13 && kt < n16) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int key = kt * 16 + 4 * grp + i;
-            const unsigned p = key < N ? prob_u8(softmax_ratio((unsigned)val[kt][i], recip)) : 0u;
-            whi |= (p >> 1) << (8 * i);
-            wlo |= (p & 1u) << (8 * i);
-            if (CKPT && g.prob && q < N && key < N)
-              g.prob[(((size_t)b * 3 + h) * 197 + q) * 197 + key] = (uint8_t)p;
+            // min(rsa(rsa(e * recip, 16), 8), 255) with one rounding: the
+            // first rounding's discarded bits cannot carry past a multiple
+            // of 2^8, so it equals (e * recip + 2^15 + 2^23) >> 24.
+            const u64 pr = (u64)(unsigned)val[kt][i] * recip + (32768u + (1u << 23));
+            const unsigned p = min((unsigned)(pr >> 24), 255u);
+            w |= p << (8 * i);
+            if (CKPT && g.prob && q < N && kt * 16 + 4 * grp + i < N)
+              g.prob[(((size_t)b * 3 + h) * 197 + q) * 197 + kt * 16 + 4 * grp + i] = (uint8_t)p;
           }
         }
-        pk_hi[kc][t] = (int)whi;
-        pk_lo[kc][t] = (int)wlo;
+        pk_hi[kc][t] = (int)((w >> 1) & 0x7F7F7F7Fu);
+        pk_lo[kc][t] = (int)(w & 0x01010101u);
       }
     }
 #pragma unroll
