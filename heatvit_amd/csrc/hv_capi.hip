@@ -27,9 +27,10 @@ int check_hip(hipError_t e, const char *what) {
 }
 
 // ---------------------------------------------------------------- profiling
-// With profiling on, every launch of the forwards is bracketed by two HIP
-// events recorded on the launch stream; hv_profile_read() sums the elapsed
-// time per kernel class.  Host-side state: one profiling client at a time.
+// With profiling on, every kernel launched inside a class scope carries a
+// start/stop event pair that its dispatch records (hipExtLaunchKernelGGL),
+// so each interval is the kernel's own execution; hv_profile_read() sums
+// them per kernel class.  Host-side state: one profiling client at a time.
 
 struct ProfEvent {
   int cls;
@@ -38,24 +39,28 @@ struct ProfEvent {
 static bool g_prof_on = false;
 static std::vector<ProfEvent> g_prof;
 
+// Active kernel class of the calling thread (-1: none).
+static thread_local int g_prof_cls = -1;
+
 struct ProfScope {
-  int cls;
-  hipStream_t s;
-  hipEvent_t a = nullptr;
-  ProfScope(int c, hipStream_t st) : cls(c), s(st) {
-    if (g_prof_on && hipEventCreate(&a) == hipSuccess) (void)hipEventRecord(a, s);
-  }
-  ~ProfScope() {
-    if (!a) return;
-    hipEvent_t b;
-    if (hipEventCreate(&b) == hipSuccess) {
-      (void)hipEventRecord(b, s);
-      g_prof.push_back({cls, a, b});
-    } else {
-      (void)hipEventDestroy(a);
-    }
-  }
+  int prev;
+  ProfScope(int c, hipStream_t) : prev(g_prof_cls) { g_prof_cls = c; }
+  ~ProfScope() { g_prof_cls = prev; }
 };
+
+void prof_events(hipEvent_t *start, hipEvent_t *stop) {
+  *start = *stop = nullptr;
+  if (!g_prof_on || g_prof_cls < 0) return;
+  hipEvent_t a, b;
+  if (hipEventCreate(&a) != hipSuccess) return;
+  if (hipEventCreate(&b) != hipSuccess) {
+    (void)hipEventDestroy(a);
+    return;
+  }
+  g_prof.push_back({g_prof_cls, a, b});
+  *start = a;
+  *stop = b;
+}
 
 static void prof_clear() {
   for (auto &e : g_prof) {
@@ -80,7 +85,7 @@ __global__ void k_init_offsets(int32_t *offsets, uint8_t *pkg, int32_t *token_co
 
 int launch_init_offsets(int32_t *offsets, uint8_t *pkg, int32_t *token_counts, int batch,
                         int rows, hipStream_t s) {
-  hipLaunchKernelGGL(k_init_offsets, dim3((batch + 256) / 256), dim3(256), 0, s, offsets, pkg,
+  hv_launch(k_init_offsets, dim3((batch + 256) / 256), dim3(256), 0, s, offsets, pkg,
                      token_counts, batch, rows);
   return check_hip(hipGetLastError(), "k_init_offsets launch");
 }
@@ -97,7 +102,7 @@ __global__ void k_copy_ckpt(const int8_t *x, const int32_t *offsets, int8_t *ckp
 
 int launch_copy_ckpt(const int8_t *x, const int32_t *offsets, int batch, int8_t *ckpt,
                      int32_t *ckpt_rows, int slot, hipStream_t s) {
-  hipLaunchKernelGGL(k_copy_ckpt, dim3(batch), dim3(256), 0, s, x, offsets, ckpt, ckpt_rows,
+  hv_launch(k_copy_ckpt, dim3(batch), dim3(256), 0, s, x, offsets, ckpt, ckpt_rows,
                      slot);
   return check_hip(hipGetLastError(), "k_copy_ckpt launch");
 }

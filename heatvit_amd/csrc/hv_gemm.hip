@@ -528,10 +528,10 @@ static int run(const GemmArgs &g, hipStream_t s) {
   if (grid > kGridCap) grid = kGridCap;
   const bool fast = fast_epilogue(g, EPI);
   if (fast)
-    hipLaunchKernelGGL((k_gemm<MT, NT, WM, EPI, AMODE, KTC, true>), dim3((unsigned)grid), dim3(256),
+    hv_launch((k_gemm<MT, NT, WM, EPI, AMODE, KTC, true>), dim3((unsigned)grid), dim3(256),
                        0, s, g, n_blocks);
   else
-    hipLaunchKernelGGL((k_gemm<MT, NT, WM, EPI, AMODE, KTC, false>), dim3((unsigned)grid),
+    hv_launch((k_gemm<MT, NT, WM, EPI, AMODE, KTC, false>), dim3((unsigned)grid),
                        dim3(256), 0, s, g, n_blocks);
   return check_hip(hipGetLastError(), "k_gemm launch");
 }
@@ -545,10 +545,10 @@ static int run_lds(const GemmArgs &g, hipStream_t s) {
   long long grid = (tiles + 7) / 8 * 8;
   if (grid > kLdsGridCap) grid = kLdsGridCap;
   if (fast_epilogue(g, EPI))
-    hipLaunchKernelGGL((k_gemm_lds<MT, NT, WM, EPI, AMODE, KTC, true>), dim3((unsigned)grid),
+    hv_launch((k_gemm_lds<MT, NT, WM, EPI, AMODE, KTC, true>), dim3((unsigned)grid),
                        dim3(256), 0, s, g, n_blocks);
   else
-    hipLaunchKernelGGL((k_gemm_lds<MT, NT, WM, EPI, AMODE, KTC, false>), dim3((unsigned)grid),
+    hv_launch((k_gemm_lds<MT, NT, WM, EPI, AMODE, KTC, false>), dim3((unsigned)grid),
                        dim3(256), 0, s, g, n_blocks);
   return check_hip(hipGetLastError(), "k_gemm_lds launch");
 }
@@ -634,7 +634,7 @@ int launch_patch_embed(const hv_patch_dev &p, const int8_t *images, int batch, i
   g.lda = 0;
   int rc = launch_gemm(g, A_PATCH, EPI_PATCH, s);
   if (rc) return rc;
-  hipLaunchKernelGGL(k_cls_rows, dim3(batch), dim3(192), 0, s, p.cls, p.pos, x, p.cls_exp,
+  hv_launch(k_cls_rows, dim3(batch), dim3(192), 0, s, p.cls, p.pos, x, p.cls_exp,
                      p.pos_exp, p.tokens_exp);
   return check_hip(hipGetLastError(), "k_cls_rows launch");
 }

@@ -1,6 +1,7 @@
 // hv_internal.h -- launchers shared between the kernel files and the C ABI.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -11,6 +12,17 @@ namespace hv {
 // Error reporting (thread-local message, see hv_capi.hip).
 int fail(int status, const char *fmt, ...);
 int check_hip(hipError_t e, const char *what);
+
+// Kernel launch.  While kernel-class profiling is on and a class is active
+// (hv_capi.hip), prof_events hands out a start/stop event pair that the
+// dispatch itself records, so the measured time is the kernel's own.
+void prof_events(hipEvent_t *start, hipEvent_t *stop);
+template <typename F, typename... Args>
+inline void hv_launch(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t s, Args... args) {
+  hipEvent_t a = nullptr, b = nullptr;
+  prof_events(&a, &b);
+  hipExtLaunchKernelGGL(kernel, grid, block, shm, s, a, b, 0, args...);
+}
 
 // A-operand sources of the GEMM.
 enum { A_ROWS = HV_A_ROWS, A_GATHER = HV_A_GATHER, A_PATCH = 2 };

@@ -165,7 +165,7 @@ int launch_layernorm(const int8_t *x, const int8_t *g, const int8_t *b, int8_t *
   if (x_exp >= -16 && x_exp <= -4 && gs == 0 && bs <= 22 && os >= 1 && os <= 29 &&
       ((uintptr_t)x & 7) == 0 && ((uintptr_t)y & 7) == 0) {
     const int blocks = (rows + 31) / 32;
-    hipLaunchKernelGGL(k_layernorm32, dim3(blocks < 256 * 8 ? blocks : 256 * 8), dim3(256), 0, s,
+    hv_launch(k_layernorm32, dim3(blocks < 256 * 8 ? blocks : 256 * 8), dim3(256), 0, s,
                        x, g, b, y, rows, rows_dev, x_exp + 32, 2 * x_exp + 32, bs, os, neg_var);
     return check_hip(hipGetLastError(), "k_layernorm32 launch");
   }
@@ -174,16 +174,16 @@ int launch_layernorm(const int8_t *x, const int8_t *g, const int8_t *b, int8_t *
   const int blocks = (rows + 15) / 16;
   const dim3 grid(blocks < 256 * 8 ? blocks : 256 * 8), block(256);
   if (fast_norm && fast_align)
-    hipLaunchKernelGGL((k_layernorm<true, true>), grid, block, 0, s, x, g, b, y, rows, rows_dev,
+    hv_launch((k_layernorm<true, true>), grid, block, 0, s, x, g, b, y, rows, rows_dev,
                        x_exp, g_exp, b_exp, out_exp, neg_var);
   else if (fast_norm)
-    hipLaunchKernelGGL((k_layernorm<true, false>), grid, block, 0, s, x, g, b, y, rows,
+    hv_launch((k_layernorm<true, false>), grid, block, 0, s, x, g, b, y, rows,
                        rows_dev, x_exp, g_exp, b_exp, out_exp, neg_var);
   else if (fast_align)
-    hipLaunchKernelGGL((k_layernorm<false, true>), grid, block, 0, s, x, g, b, y, rows,
+    hv_launch((k_layernorm<false, true>), grid, block, 0, s, x, g, b, y, rows,
                        rows_dev, x_exp, g_exp, b_exp, out_exp, neg_var);
   else
-    hipLaunchKernelGGL((k_layernorm<false, false>), grid, block, 0, s, x, g, b, y, rows,
+    hv_launch((k_layernorm<false, false>), grid, block, 0, s, x, g, b, y, rows,
                        rows_dev, x_exp, g_exp, b_exp, out_exp, neg_var);
   return check_hip(hipGetLastError(), "k_layernorm launch");
 }
@@ -407,12 +407,12 @@ int launch_attention(const AttnArgs &a_in, hipStream_t s) {
   a.ctx_rnd = a.ctx_fast ? 1 << (a.ctx_shift - 1) : 0;
   const bool ck = a.score || a.prob;
   const dim3 grid(a.batch * 3), block(256);
-  if (a.q16_mode == 0 && !ck) hipLaunchKernelGGL((k_attention<0, false>), grid, block, 0, s, a);
-  else if (a.q16_mode == 0) hipLaunchKernelGGL((k_attention<0, true>), grid, block, 0, s, a);
-  else if (a.q16_mode == 1 && !ck) hipLaunchKernelGGL((k_attention<1, false>), grid, block, 0, s, a);
-  else if (a.q16_mode == 1) hipLaunchKernelGGL((k_attention<1, true>), grid, block, 0, s, a);
-  else if (!ck) hipLaunchKernelGGL((k_attention<2, false>), grid, block, 0, s, a);
-  else hipLaunchKernelGGL((k_attention<2, true>), grid, block, 0, s, a);
+  if (a.q16_mode == 0 && !ck) hv_launch((k_attention<0, false>), grid, block, 0, s, a);
+  else if (a.q16_mode == 0) hv_launch((k_attention<0, true>), grid, block, 0, s, a);
+  else if (a.q16_mode == 1 && !ck) hv_launch((k_attention<1, false>), grid, block, 0, s, a);
+  else if (a.q16_mode == 1) hv_launch((k_attention<1, true>), grid, block, 0, s, a);
+  else if (!ck) hv_launch((k_attention<2, false>), grid, block, 0, s, a);
+  else hv_launch((k_attention<2, true>), grid, block, 0, s, a);
   return check_hip(hipGetLastError(), "k_attention launch");
 }
 
@@ -462,7 +462,7 @@ __global__ __launch_bounds__(64) void k_softmax_rows(const int32_t *x, const int
 int launch_softmax_rows(const int32_t *x, const int32_t *offsets, int rows, uint8_t *att,
                         int32_t *sel, hipStream_t s) {
   if (rows <= 0) return HV_OK;
-  hipLaunchKernelGGL(k_softmax_rows, dim3(rows), dim3(64), 0, s, x, offsets, att, sel);
+  hv_launch(k_softmax_rows, dim3(rows), dim3(64), 0, s, x, offsets, att, sel);
   return check_hip(hipGetLastError(), "k_softmax_rows launch");
 }
 
@@ -492,7 +492,7 @@ int launch_primitive(int op, const int64_t *in, int64_t *out, int64_t n, int a, 
   if (n <= 0) return HV_OK;
   const int64_t blocks = (n + 255) / 256;
   if (blocks > 0x7fffffff) return fail(HV_EVALUE, "too many elements");
-  hipLaunchKernelGGL(k_primitive, dim3((unsigned)blocks), dim3(256), 0, s, op, in, out, n, a, b,
+  hv_launch(k_primitive, dim3((unsigned)blocks), dim3(256), 0, s, op, in, out, n, a, b,
                      c);
   return check_hip(hipGetLastError(), "k_primitive launch");
 }

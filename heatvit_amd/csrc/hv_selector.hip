@@ -414,15 +414,15 @@ int launch_selector(const SelectorArgs &a, hipStream_t s) {
     const int fast = in(-16 - (p.in_exp + p.local_w_exp)) && in(p.local_out_exp + 16) &&
                      in(-16 - (p.concat_out_exp + p.score_w1_exp)) && in(p.h1_out_exp + 16) &&
                      in(-16 - (p.h1_out_exp + p.score_w2_exp)) && in(p.h2_out_exp + 16);
-    hipLaunchKernelGGL(k_selector_head, dim3(a.batch * 3), dim3(256), 0, s, p, a.tokens,
+    hv_launch(k_selector_head, dim3(a.batch * 3), dim3(256), 0, s, p, a.tokens,
                        a.offsets, a.pkg_in, a.hs, a.stats, fast, a.ck);
     if ((rc = check_hip(hipGetLastError(), "k_selector_head launch"))) return rc;
   }
-  hipLaunchKernelGGL(k_selector_keep, dim3(a.batch), dim3(64), 0, s, a.offsets, a.pkg_in,
+  hv_launch(k_selector_keep, dim3(a.batch), dim3(64), 0, s, a.offsets, a.pkg_in,
                      a.fused, a.kept_index, a.state, p, a.p ? a.hs : nullptr,
                      a.p ? a.stats : nullptr, a.p ? a.ck.head_weights : nullptr);
   if ((rc = check_hip(hipGetLastError(), "k_selector_keep launch"))) return rc;
-  hipLaunchKernelGGL(k_selector_compact, dim3(a.batch), dim3(256), 0, s, a.tokens, a.offsets,
+  hv_launch(k_selector_compact, dim3(a.batch), dim3(256), 0, s, a.tokens, a.offsets,
                      a.pkg_in, a.batch, a.fused, a.kept_index, a.state, a.out_tokens,
                      a.out_offsets, a.pkg_out, a.token_counts, a.stage);
   return check_hip(hipGetLastError(), "k_selector_compact launch");

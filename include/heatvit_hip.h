@@ -237,10 +237,11 @@ int hv_model_forward(const hv_model_dev *p, const int8_t *images, int batch, int
 
 /* ------------------------------------------------------------------ */
 /* Kernel-class timing with HIP events (for benchmarks).  While enabled, */
-/* the forwards bracket every launch with two events on the launch       */
-/* stream; hv_profile_read() waits for them and returns the summed       */
-/* milliseconds and launch counts per class (arrays of n entries), then  */
-/* clears the record.  Not thread-safe: one profiling client at a time.  */
+/* every kernel the forwards launch carries a start/stop event pair      */
+/* recorded by its own dispatch; hv_profile_read() waits for them and    */
+/* returns the summed milliseconds and launch counts per class (arrays   */
+/* of n entries), then clears the record.  Not thread-safe: one          */
+/* profiling client at a time.                                           */
 /* ------------------------------------------------------------------ */
 
 #define HV_PROF_PATCH 0
