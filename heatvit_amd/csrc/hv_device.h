@@ -143,16 +143,19 @@ __host__ __device__ __forceinline__ unsigned mul_u24(unsigned a, unsigned b) {
   return (a & 0xFFFFFFu) * (b & 0xFFFFFFu);
 }
 
-// The single-precision reciprocal the quotient estimate uses; any value
-// within a few ulp of 1/d works (the correction step is exact).
+// Device operations behind gelu_q16_r: the single-precision reciprocal the
+// quotient estimate uses (any value within a few ulp of 1/d works, the
+// correction step is exact), and v >> 1 as a bit-field extract, which keeps
+// the compiler from rewriting ip + (ip >> 1) into a 64-bit average.
 struct RcpHw {
   __device__ static float rcp(float d) { return __builtin_amdgcn_rcpf(d); }
+  __device__ static int sar1(int v) { return __builtin_amdgcn_sbfe(v, 1, 31); }
 };
 
 template <typename R>
 __host__ __device__ __forceinline__ int gelu_q16_r(int x) {
   const int ip = x + (x >> 1) + (x >> 3) + (x >> 4);
-  const int ip2 = ip + (ip >> 1) - (ip >> 4);
+  const int ip2 = ip + R::sar1(ip) - (ip >> 4);
   const unsigned a = (unsigned)(ip2 < 0 ? -ip2 : ip2);
   const unsigned q = a >> 16;
   const unsigned frac = (mul_u24(a & 0xFFFFu, 11u) + 15u) >> 4;
@@ -198,6 +201,13 @@ __device__ __forceinline__ Rq rq_setup(int s, int lo, int hi) {
 
 __device__ __forceinline__ int rq(int v, const Rq &r) {
   const int t = r.s > 0 ? (v + r.rnd + (v >> 31)) >> r.s : min(max(v, r.vlo), r.vhi) << -r.s;
+  return min(max(t, r.lo), r.hi);
+}
+
+// The same with the direction fixed at compile time (LEFT: s <= 0).
+template <bool LEFT>
+__device__ __forceinline__ int rq_dir(int v, const Rq &r) {
+  const int t = LEFT ? min(max(v, r.vlo), r.vhi) << -r.s : (v + r.rnd + (v >> 31)) >> r.s;
   return min(max(t, r.lo), r.hi);
 }
 

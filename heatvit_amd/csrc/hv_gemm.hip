@@ -131,7 +131,7 @@ __device__ __forceinline__ void epi_operands(const GemmArgs &g, const int (&arow
 
 // Epilogue of one wavefront tile: lane l finishes row r0 + 32*mt + l%32,
 // channels c0 .. c0+15 of each column tile.
-template <int MT, int NT, int EPI, bool FAST>
+template <int MT, int NT, int EPI, bool FAST, int DIRS>
 __device__ __forceinline__ void epi_tile(const GemmArgs &g, const v16i (&acc)[MT][NT],
                                          const v4i (&bias4)[NT][4], const v4i (&res4)[MT][NT],
                                          int r0, int ct0, int M, int h, int l32, const Rq &rq_a,
@@ -164,17 +164,18 @@ __device__ __forceinline__ void epi_tile(const GemmArgs &g, const v16i (&acc)[MT
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
           const int v = acc[mt][nt][j] + bias4[nt][j >> 2][j & 3];
+          constexpr bool LA = DIRS & 1, LB = (DIRS >> 1) & 1;
           if (EPI == EPI_I8) {
-            o[j] = rq(v, rq_a);
+            o[j] = rq_dir<LA>(v, rq_a);
           } else if (EPI == EPI_GELU) {
-            o[j] = rq(gelu_q16(rq(v, rq_a)), rq_b);
+            o[j] = rq_dir<LB>(gelu_q16(rq_dir<LA>(v, rq_a)), rq_b);
           } else if (RESLIKE) {
-            const int t8 = rq(v, rq_a);
+            const int t8 = rq_dir<LA>(v, rq_a);
             const int r8 = (int)(int8_t)(res4[mt][nt][j >> 2] >> (8 * (j & 3)));
             const int s = EPI == EPI_RES ? r8 * (1 << g.da) + t8 * (1 << g.db)
                                          : t8 * (1 << g.da) + r8 * (1 << g.db);
             mid[j] = t8;
-            o[j] = rq(s, rq_b);
+            o[j] = rq_dir<LB>(s, rq_b);
           }
         }
       } else {
@@ -227,7 +228,7 @@ __device__ __forceinline__ void epi_tile(const GemmArgs &g, const v16i (&acc)[MT
   }
 }
 
-template <int MT, int NT, int WM, int EPI, int AMODE, int KTC, bool FAST>
+template <int MT, int NT, int WM, int EPI, int AMODE, int KTC, bool FAST, int DIRS>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
   constexpr int WN = 4 / WM;
   constexpr int BM = 32 * MT * WM;  // rows per tile
@@ -364,7 +365,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
       }
     }
 
-    epi_tile<MT, NT, EPI, FAST>(g, acc, bias4, res4, r0, ct0, M, h, l32, rq_a, rq_b);
+    epi_tile<MT, NT, EPI, FAST, DIRS>(g, acc, bias4, res4, r0, ct0, M, h, l32, rq_a, rq_b);
   }
 }
 
@@ -374,7 +375,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
 // (conflict-free fragment reads).  The next chunk -- or the next tile's
 // first chunk -- and its weight fragments are loaded while the current
 // chunk's MFMAs run; one barrier per chunk.
-template <int MT, int NT, int WM, int EPI, int AMODE, int KTC, bool FAST>
+template <int MT, int NT, int WM, int EPI, int AMODE, int KTC, bool FAST, int DIRS>
 __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g, int n_blocks) {
   constexpr int WN = 4 / WM, BM = 32 * MT * WM, BT = NT * WN;
   constexpr int KC = 6, NCH = KTC / KC, ROW = 208;
@@ -471,7 +472,7 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g, int n_blocks) {
           acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bcur[nt][kt], af, acc[mt][nt], 0, 0, 0);
       }
     if (last_chunk) {
-      epi_tile<MT, NT, EPI, FAST>(g, acc, bias4, res4, r0, ct0, M, h, l32, rq_a, rq_b);
+      epi_tile<MT, NT, EPI, FAST, DIRS>(g, acc, bias4, res4, r0, ct0, M, h, l32, rq_a, rq_b);
       if (!more) break;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
@@ -518,6 +519,50 @@ static bool fast_epilogue(const GemmArgs &g, int epi) {
   }
 }
 
+// Requant directions of a launch for the int32 epilogue (bit 0: the
+// product requant shifts left, bit 1: the second requant -- GELU output or
+// align-add -- shifts left).
+static int epilogue_dirs(const GemmArgs &g, int epi) {
+  int d = g.shift_a <= 0 ? 1 : 0;
+  if (epi == EPI_GELU && g.shift_b <= 0) d |= 2;
+  if ((epi == EPI_RES || epi == EPI_PATCH) && g.os <= 0) d |= 2;
+  return d;
+}
+
+// Launches kernel template K with FAST = false, or FAST = true and the
+// launch's requant directions.
+template <template <bool, int> class K>
+static int launch_epi(const GemmArgs &g, int epi, long long grid, int n_blocks, hipStream_t s) {
+  const dim3 gd((unsigned)grid), bd(256);
+  if (!fast_epilogue(g, epi)) {
+    hv_launch(K<false, 0>::fn(), gd, bd, 0, s, g, n_blocks);
+  } else {
+    switch (epilogue_dirs(g, epi)) {
+      case 0: hv_launch(K<true, 0>::fn(), gd, bd, 0, s, g, n_blocks); break;
+      case 1: hv_launch(K<true, 1>::fn(), gd, bd, 0, s, g, n_blocks); break;
+      case 2: hv_launch(K<true, 2>::fn(), gd, bd, 0, s, g, n_blocks); break;
+      default: hv_launch(K<true, 3>::fn(), gd, bd, 0, s, g, n_blocks); break;
+    }
+  }
+  return check_hip(hipGetLastError(), "k_gemm launch");
+}
+
+template <int MT, int NT, int WM, int EPI, int AMODE, int KTC>
+struct DirectK {
+  template <bool FAST, int DIRS>
+  struct K {
+    static auto fn() { return &k_gemm<MT, NT, WM, EPI, AMODE, KTC, FAST, FAST ? DIRS : 0>; }
+  };
+};
+
+template <int MT, int NT, int WM, int EPI, int AMODE, int KTC>
+struct LdsK {
+  template <bool FAST, int DIRS>
+  struct K {
+    static auto fn() { return &k_gemm_lds<MT, NT, WM, EPI, AMODE, KTC, FAST, FAST ? DIRS : 0>; }
+  };
+};
+
 template <int MT, int NT, int WM, int EPI, int AMODE, int KTC>
 static int run(const GemmArgs &g, hipStream_t s) {
   constexpr int BM = 32 * MT * WM, BN = 32 * NT * (4 / WM);
@@ -526,14 +571,7 @@ static int run(const GemmArgs &g, hipStream_t s) {
   if (tiles <= 0) return HV_OK;
   long long grid = (tiles + 7) / 8 * 8;
   if (grid > kGridCap) grid = kGridCap;
-  const bool fast = fast_epilogue(g, EPI);
-  if (fast)
-    hv_launch((k_gemm<MT, NT, WM, EPI, AMODE, KTC, true>), dim3((unsigned)grid), dim3(256),
-                       0, s, g, n_blocks);
-  else
-    hv_launch((k_gemm<MT, NT, WM, EPI, AMODE, KTC, false>), dim3((unsigned)grid),
-                       dim3(256), 0, s, g, n_blocks);
-  return check_hip(hipGetLastError(), "k_gemm launch");
+  return launch_epi<DirectK<MT, NT, WM, EPI, AMODE, KTC>::template K>(g, EPI, grid, n_blocks, s);
 }
 
 template <int MT, int NT, int WM, int EPI, int AMODE, int KTC>
@@ -544,13 +582,7 @@ static int run_lds(const GemmArgs &g, hipStream_t s) {
   if (tiles <= 0) return HV_OK;
   long long grid = (tiles + 7) / 8 * 8;
   if (grid > kLdsGridCap) grid = kLdsGridCap;
-  if (fast_epilogue(g, EPI))
-    hv_launch((k_gemm_lds<MT, NT, WM, EPI, AMODE, KTC, true>), dim3((unsigned)grid),
-                       dim3(256), 0, s, g, n_blocks);
-  else
-    hv_launch((k_gemm_lds<MT, NT, WM, EPI, AMODE, KTC, false>), dim3((unsigned)grid),
-                       dim3(256), 0, s, g, n_blocks);
-  return check_hip(hipGetLastError(), "k_gemm_lds launch");
+  return launch_epi<LdsK<MT, NT, WM, EPI, AMODE, KTC>::template K>(g, EPI, grid, n_blocks, s);
 }
 
 // Shapes (measured at 50432 rows): K = 192 GEMMs use the direct kernel with

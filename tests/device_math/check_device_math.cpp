@@ -22,9 +22,12 @@ extern "C" {
 
 using namespace hv;
 
-struct RcpExact { static float rcp(float d) { return 1.0f / d; } };
-struct RcpLo { static float rcp(float d) { return std::nextafter(1.0f / d, 0.0f); } };
-struct RcpHi { static float rcp(float d) { return std::nextafter(1.0f / d, 1.0f); } };
+struct RcpExact {
+  static float rcp(float d) { return 1.0f / d; }
+  static int sar1(int v) { return v >> 1; }
+};
+struct RcpLo : RcpExact { static float rcp(float d) { return std::nextafter(1.0f / d, 0.0f); } };
+struct RcpHi : RcpExact { static float rcp(float d) { return std::nextafter(1.0f / d, 1.0f); } };
 
 static long check_gelu() {
   long bad = 0;
