@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include "../../include/heatvit_hip.h"
+#include "hv_device.h"
 
 namespace hv {
 
@@ -59,6 +60,11 @@ void epilogue_limits_pub(GemmArgs &g, int epilogue);
 // CLS rows are written by a second small kernel.
 int launch_patch_embed(const hv_patch_dev &p, const int8_t *images, int batch, int8_t *x,
                        hipStream_t s);
+
+// Fills *ln for the int32 LayerNorm path (hv_device.h) when the exponents
+// and pointer alignment allow it.
+bool ln32_setup(const int8_t *g, const int8_t *b, int8_t *y, int x_exp, int g_exp, int b_exp,
+                int out_exp, Ln32 *ln);
 
 int launch_layernorm(const int8_t *x, const int8_t *g, const int8_t *b, int8_t *y, int rows,
                      const int32_t *rows_dev, int x_exp, int g_exp, int b_exp, int out_exp,

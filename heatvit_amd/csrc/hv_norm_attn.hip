@@ -98,58 +98,41 @@ __global__ __launch_bounds__(256) void k_layernorm(const int8_t *__restrict__ x,
 // [1, 29] (LnRow in hv_device.h): eight lanes per row, 24 channels each.
 // Row sums come from packed int8 dot products; each element costs three
 // 24-bit multiply-adds for norm_q16, one for gamma/beta and the requant.
-__global__ __launch_bounds__(256) void k_layernorm32(const int8_t *__restrict__ x,
-                                                     const int8_t *__restrict__ gamma,
-                                                     const int8_t *__restrict__ beta,
-                                                     int8_t *__restrict__ y, int rows,
-                                                     const int32_t *rows_dev, int s, int t,
-                                                     int bs, int os, uint8_t *neg_var) {
+__global__ __launch_bounds__(256) void k_layernorm32(const int8_t *__restrict__ x, Ln32 ln,
+                                                     int rows, const int32_t *rows_dev,
+                                                     uint8_t *neg_var) {
   const int sub = threadIdx.x & 7;
   const int R = rows_dev ? min(*rows_dev, rows) : rows;
-  const int c0 = sub * 24;
-  int gm[24], bsh[24];
-#pragma unroll
-  for (int j = 0; j < 24; ++j) {
-    gm[j] = gamma[c0 + j];
-    bsh[j] = (int)beta[c0 + j] * (1 << bs);
-  }
-  const int rnd = 1 << (os - 1);
+  int gm[6], bt[6];
+  ln32_params(ln, sub, gm, bt);
   for (int row = blockIdx.x * 32 + (threadIdx.x >> 3); row < R; row += gridDim.x * 32) {
-    const int2 *xr = reinterpret_cast<const int2 *>(x + (size_t)row * 192 + c0);
-    int w[6];
+    const int2 *xr = reinterpret_cast<const int2 *>(x + (size_t)row * 192 + sub * 24);
+    int w[6], out[6];
 #pragma unroll
     for (int q = 0; q < 3; ++q) {
       const int2 v = xr[q];
       w[2 * q] = v.x;
       w[2 * q + 1] = v.y;
     }
-    int sx = 0, sxx = 0;
-#pragma unroll
-    for (int q = 0; q < 6; ++q) {
-      sx = __builtin_amdgcn_sdot4(w[q], 0x01010101, sx, false);
-      sxx = __builtin_amdgcn_sdot4(w[q], w[q], sxx, false);
-    }
-#pragma unroll
-    for (int off = 1; off < 8; off <<= 1) {
-      sx += __shfl_xor(sx, off);
-      sxx += __shfl_xor(sxx, off);
-    }
-    const LnRow r = ln_row_consts(sx, sxx, s, t);
-    int out[6] = {0, 0, 0, 0, 0, 0};
-#pragma unroll
-    for (int j = 0; j < 24; ++j) {
-      const int xv = (int)(int8_t)(w[j >> 2] >> (8 * (j & 3)));
-      const int norm = ln_norm(xv, r);
-      const int a = norm * gm[j] + bsh[j];
-      int o = (a + rnd + (a >> 31)) >> os;
-      o = min(max(o, -128), 127);
-      out[j >> 2] |= (o & 0xFF) << (8 * (j & 3));
-    }
-    int2 *yr = reinterpret_cast<int2 *>(y + (size_t)row * 192 + c0);
+    const bool neg = ln32_row(w, gm, bt, ln, out);
+    int2 *yr = reinterpret_cast<int2 *>(ln.out + (size_t)row * 192 + sub * 24);
 #pragma unroll
     for (int q = 0; q < 3; ++q) yr[q] = int2{out[2 * q], out[2 * q + 1]};
-    if (neg_var && sub == 0) neg_var[row] = r.neg_var ? 1 : 0;
+    if (neg_var && sub == 0) neg_var[row] = neg ? 1 : 0;
   }
+}
+
+// The int32 LayerNorm applies (and *ln is filled) when the input scale is in
+// [-16, -4], gamma sits at the common exponent, beta's shift is at most 22
+// and the output shift in [1, 29]; pointers must be 8-byte aligned.
+bool ln32_setup(const int8_t *g, const int8_t *b, int8_t *y, int x_exp, int g_exp, int b_exp,
+                int out_exp, Ln32 *ln) {
+  const int common = (g_exp - 16) < b_exp ? (g_exp - 16) : b_exp;
+  const int gs = g_exp - 16 - common, bs = b_exp - common, os = out_exp - common;
+  if (!(x_exp >= -16 && x_exp <= -4 && gs == 0 && bs <= 22 && os >= 1 && os <= 29)) return false;
+  if (((uintptr_t)g & 7) || ((uintptr_t)b & 7) || ((uintptr_t)y & 7)) return false;
+  *ln = Ln32{g, b, y, x_exp + 32, 2 * x_exp + 32, bs, os};
+  return true;
 }
 
 int launch_layernorm(const int8_t *x, const int8_t *g, const int8_t *b, int8_t *y, int rows,
@@ -161,12 +144,11 @@ int launch_layernorm(const int8_t *x, const int8_t *g, const int8_t *b, int8_t *
   if (((uintptr_t)x & 3) || ((uintptr_t)y & 3))
     return fail(HV_EVALUE, "layernorm: rows must be 4-byte aligned");
   const int common = (g_exp - 16) < b_exp ? (g_exp - 16) : b_exp;
-  const int gs = g_exp - 16 - common, bs = b_exp - common, os = out_exp - common;
-  if (x_exp >= -16 && x_exp <= -4 && gs == 0 && bs <= 22 && os >= 1 && os <= 29 &&
-      ((uintptr_t)x & 7) == 0 && ((uintptr_t)y & 7) == 0) {
+  Ln32 ln;
+  if (((uintptr_t)x & 7) == 0 && ln32_setup(g, b, y, x_exp, g_exp, b_exp, out_exp, &ln)) {
     const int blocks = (rows + 31) / 32;
-    hv_launch(k_layernorm32, dim3(blocks < 256 * 8 ? blocks : 256 * 8), dim3(256), 0, s,
-                       x, g, b, y, rows, rows_dev, x_exp + 32, 2 * x_exp + 32, bs, os, neg_var);
+    hv_launch(k_layernorm32, dim3(blocks < 256 * 8 ? blocks : 256 * 8), dim3(256), 0, s, x, ln,
+              rows, rows_dev, neg_var);
     return check_hip(hipGetLastError(), "k_layernorm32 launch");
   }
   const bool fast_norm = x_exp <= -1;
