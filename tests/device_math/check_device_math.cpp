@@ -62,7 +62,11 @@ static long check_softmax(int rows) {
     const unsigned recip = softmax_recip(sum);
     for (int i = 0; i < n; ++i) {
       const unsigned ratio = softmax_ratio(e[i], recip);
-      if (prob_u8(ratio) != ref_att[i] || (int)(ratio > 65536u ? 65536u : ratio) != ref_sel[i])
+      // attention narrowing in one rounding, as the attention kernel does it
+      const unsigned long long pr = (unsigned long long)e[i] * recip + 32768u + (1u << 23);
+      const unsigned p1 = (unsigned)(pr >> 24) > 255u ? 255u : (unsigned)(pr >> 24);
+      if (prob_u8(ratio) != ref_att[i] || p1 != ref_att[i] ||
+          (int)(ratio > 65536u ? 65536u : ratio) != ref_sel[i])
         if (++bad < 5) std::printf("softmax mismatch row %d col %d\n", it, i);
     }
   }
