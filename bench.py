@@ -80,7 +80,7 @@ def class_work(counts, params, batch):
 def cpu_baseline(images, params, threads):
     from oracle import oracle
     t0 = time.perf_counter()
-    _, _, status = oracle.model_infer_batch(images, params, threads=threads)
+    _, _, status, _ = oracle.model_infer_batch(images, params, threads=threads)
     dt = time.perf_counter() - t0
     assert not status.any()
     return len(images) / dt, dt

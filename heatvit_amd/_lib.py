@@ -2,7 +2,9 @@
 
 Loading fails loudly: there is no CPU fallback anywhere in heatvit_amd.
 Status codes map onto the golden model's exception types (HV_EVALUE ->
-ValueError, HV_EOVERFLOW -> OverflowError, HIP errors -> RuntimeError).
+ValueError, HV_EOVERFLOW -> OverflowError, HIP errors -> RuntimeError);
+each raised exception carries `error_class`, the reference engine's error
+code of the failure (HV_ERR_*, heatvit_pkg.sv:109-118).
 """
 
 import ctypes as C
@@ -11,10 +13,13 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libheatvit_hip.so"
 
 HV_OK, HV_EVALUE, HV_EOVERFLOW, HV_EHIP = 0, -2, -3, -4
+(HV_ERR_NONE, HV_ERR_OPCODE, HV_ERR_DIMENSION, HV_ERR_ADDRESS, HV_ERR_TOKEN_COUNT,
+ HV_ERR_MEMORY_PROTOCOL, HV_ERR_SOFTMAX_ZERO_SUM, HV_ERR_BUSY_START) = range(8)
+HV_WARN_HEAD_DEN_ZERO, HV_WARN_PACKAGE_DEN_ZERO, HV_WARN_LN_NEGATIVE_VARIANCE = 1, 2, 4
 HV_PRIM_REQUANT, HV_PRIM_GELU, HV_PRIM_PLAN, HV_PRIM_RSA = 0, 1, 2, 3
 HV_EPI_I8, HV_EPI_I32, HV_EPI_GELU, HV_EPI_RESIDUAL = 0, 1, 2, 3
 HV_A_ROWS, HV_A_GATHER = 0, 1
-ABI_VERSION = 2
+ABI_VERSION = 3
 PROF_CLASSES = ("patch", "layernorm", "gemm_qkv", "attention", "gemm_proj", "gemm_ffn1",
                 "gemm_ffn2", "selector", "head", "other")
 
@@ -89,7 +94,17 @@ def lib():
     if not torch.cuda.is_available():
         raise RuntimeError("heatvit_amd needs a ROCm GPU (gfx950); none is visible")
     L = C.CDLL(str(LIB_PATH))
+    _declare(L)
+    if L.hv_abi_version() != ABI_VERSION:
+        raise RuntimeError("libheatvit_hip.so ABI version mismatch; rebuild it")
+    _LIB = L
+    return L
+
+
+def _declare(L):
+    """ctypes signatures of every entry point of include/heatvit_hip.h."""
     L.hv_last_error.restype = C.c_char_p
+    L.hv_last_error_class.restype = C.c_int
     L.hv_abi_version.restype = C.c_int
     L.hv_eval_primitive.argtypes = [C.c_int, _vp, _vp, C.c_int64, C.c_int, C.c_int, C.c_int, _vp]
     L.hv_softmax_rows.argtypes = [_vp, _vp, C.c_int, _vp, _vp, _vp]
@@ -99,7 +114,7 @@ def lib():
     L.hv_block_workspace_bytes.restype = C.c_size_t
     L.hv_block_workspace_bytes.argtypes = [C.c_int, C.c_int]
     L.hv_block_forward.argtypes = [C.POINTER(BlockDev), _vp, _vp, C.c_int, C.c_int, _vp,
-                                   C.POINTER(BlockCkpt), _vp, C.c_size_t, _vp]
+                                   C.POINTER(BlockCkpt), _vp, _vp, _vp, C.c_size_t, _vp]
     L.hv_selector_workspace_bytes.restype = C.c_size_t
     L.hv_selector_workspace_bytes.argtypes = [C.c_int]
     L.hv_selector_forward.argtypes = [C.POINTER(SelectorDev), _vp, _vp, _vp, C.c_int, _vp, _vp,
@@ -110,29 +125,29 @@ def lib():
     L.hv_model_workspace_bytes.restype = C.c_size_t
     L.hv_model_workspace_bytes.argtypes = [C.c_int]
     L.hv_model_forward.argtypes = [C.POINTER(ModelDev), _vp, C.c_int, _vp, _vp, _vp, _vp, _vp,
-                                   _vp, C.c_size_t, _vp]
+                                   _vp, _vp, C.c_size_t, _vp]
     L.hv_profile_enable.argtypes = [C.c_int]
     L.hv_profile_read.argtypes = [_vp, _vp, C.c_int]
-    if L.hv_abi_version() != ABI_VERSION:
-        raise RuntimeError("libheatvit_hip.so ABI version mismatch; rebuild it")
-    _LIB = L
-    return L
+
+
+def error(rc, what, L=None):
+    """The exception for status rc of the last call on this thread."""
+    L = L or lib()
+    exc = {HV_EVALUE: ValueError, HV_EOVERFLOW: OverflowError}.get(rc, RuntimeError)
+    e = exc(f"{what}: {L.hv_last_error().decode(errors='replace')}")
+    e.error_class = L.hv_last_error_class()
+    return e
 
 
 def check(rc, what):
-    if rc == HV_OK:
-        return
-    msg = f"{what}: {lib().hv_last_error().decode(errors='replace')}"
-    if rc == HV_EVALUE:
-        raise ValueError(msg)
-    if rc == HV_EOVERFLOW:
-        raise OverflowError(msg)
-    raise RuntimeError(msg)
+    if rc != HV_OK:
+        raise error(rc, what)
 
 
 def exported_symbols():
     """Names declared in include/heatvit_hip.h (checked by the CPU tests)."""
-    return ("hv_last_error", "hv_abi_version", "hv_eval_primitive", "hv_softmax_rows",
+    return ("hv_last_error", "hv_last_error_class", "hv_abi_version", "hv_eval_primitive",
+            "hv_softmax_rows",
             "hv_layernorm_i8", "hv_gemm_i8", "hv_block_workspace_bytes", "hv_block_forward",
             "hv_selector_workspace_bytes", "hv_selector_forward", "hv_selector_finalize",
             "hv_patch_embedding", "hv_profile_enable", "hv_profile_read",

@@ -12,18 +12,25 @@
 namespace hv {
 
 static thread_local char g_err[512];
+static thread_local int g_err_class = HV_ERR_NONE;
 
-int fail(int status, const char *fmt, ...) {
+int fail(int status, int cls, const char *fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
   vsnprintf(g_err, sizeof g_err, fmt, ap);
   va_end(ap);
+  g_err_class = cls;
   return status;
 }
 
 int check_hip(hipError_t e, const char *what) {
   if (e == hipSuccess) return HV_OK;
-  return fail(HV_EHIP, "%s: %s", what, hipGetErrorString(e));
+  return fail(HV_EHIP, HV_ERR_MEMORY_PROTOCOL, "%s: %s", what, hipGetErrorString(e));
+}
+
+static void clear_error() {
+  g_err[0] = 0;
+  g_err_class = HV_ERR_NONE;
 }
 
 // ---------------------------------------------------------------- profiling
@@ -72,22 +79,42 @@ static void prof_clear() {
 
 // ---------------------------------------------------------------- utilities
 
-__global__ void k_init_offsets(int32_t *offsets, uint8_t *pkg, int32_t *token_counts, int batch,
-                               int rows) {
+__global__ void k_init_offsets(int32_t *offsets, uint8_t *pkg, int32_t *token_counts,
+                               int32_t *warnings, int batch, int rows) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i <= batch) offsets[i] = i * rows;
   if (i < batch) {
     pkg[i] = 0;
     if (token_counts)
       for (int s = 0; s < 4; ++s) token_counts[(size_t)i * 4 + s] = rows;
+    if (warnings) warnings[i] = 0;
   }
 }
 
-int launch_init_offsets(int32_t *offsets, uint8_t *pkg, int32_t *token_counts, int batch,
-                        int rows, hipStream_t s) {
+int launch_init_offsets(int32_t *offsets, uint8_t *pkg, int32_t *token_counts,
+                        int32_t *warnings, int batch, int rows, hipStream_t s) {
   hv_launch(k_init_offsets, dim3((batch + 256) / 256), dim3(256), 0, s, offsets, pkg,
-                     token_counts, batch, rows);
+                     token_counts, warnings, batch, rows);
   return check_hip(hipGetLastError(), "k_init_offsets launch");
+}
+
+// The attention's skip condition (k_attention), reported per image.
+__global__ void k_image_check(const int32_t *offsets, int batch, int capacity, int32_t *status,
+                              int32_t *warnings) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  const int row0 = offsets[b], n = offsets[b + 1] - row0;
+  const bool ok = n >= 1 && n <= HV_MAX_TOKENS && row0 >= 0 && row0 <= capacity - n;
+  if (status) status[b] = ok ? HV_ERR_NONE : HV_ERR_TOKEN_COUNT;
+  if (warnings) warnings[b] = 0;
+}
+
+int launch_image_check(const int32_t *offsets, int batch, int capacity, int32_t *status,
+                       int32_t *warnings, hipStream_t s) {
+  if (!status && !warnings) return HV_OK;
+  hv_launch(k_image_check, dim3((batch + 255) / 256), dim3(256), 0, s, offsets, batch, capacity,
+            status, warnings);
+  return check_hip(hipGetLastError(), "k_image_check launch");
 }
 
 __global__ void k_copy_ckpt(const int8_t *x, const int32_t *offsets, int8_t *ckpt,
@@ -138,10 +165,12 @@ static BlockWs carve_block(Carve &cv, size_t rows) {
 
 // transformer_block (transformer.py:401-431) on rows [0, offsets[batch]):
 // LN1, QKV, attention, proj + residual, LN2, FFN1 + GELU, FFN2 + residual.
+// warnings (optional, [B]) receive the LayerNorms' negative-variance bit.
 static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *offsets,
                          int batch, int max_rows, int8_t *z, const hv_block_ckpt *ck,
-                         const BlockWs &w, hipStream_t s) {
+                         int32_t *warnings, const BlockWs &w, hipStream_t s) {
   const int32_t *rows_dev = offsets + batch;
+  const LnWarn lw{offsets, batch, warnings};
   int8_t *qkv = ck && ck->fused_qkv ? ck->fused_qkv : w.qkv;
   int8_t *ctx = ck && ck->concat ? ck->concat : w.ctx;
   int8_t *y = ck && ck->y ? ck->y : w.y;
@@ -153,7 +182,7 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   {
     ProfScope ps(HV_PROF_LAYERNORM, s);
     rc = launch_layernorm(x, p.ln1_gamma, p.ln1_beta, ln1, max_rows, rows_dev, p.x_exp,
-                          p.gamma1_exp, p.beta1_exp, p.ln1_out_exp, nullptr, s);
+                          p.gamma1_exp, p.beta1_exp, p.ln1_out_exp, nullptr, lw, s);
   }
   if (rc) return rc;
   GemmArgs g{};
@@ -167,7 +196,7 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   if (rc) return rc;
 
   AttnArgs a{};
-  a.qkv = qkv; a.offsets = offsets; a.ctx = ctx; a.batch = batch;
+  a.qkv = qkv; a.offsets = offsets; a.ctx = ctx; a.batch = batch; a.rows_cap = max_rows;
   a.score = ck ? ck->score : nullptr;
   a.prob = ck ? ck->prob : nullptr;
   a.score_shift = p.score_exp - 2 * p.qkv_out_exp;
@@ -193,7 +222,7 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   {
     ProfScope ps(HV_PROF_LAYERNORM, s);
     rc = launch_layernorm(y, p.ln2_gamma, p.ln2_beta, ln2, max_rows, rows_dev, p.ffn_x_exp,
-                          p.gamma2_exp, p.beta2_exp, p.ln2_out_exp, nullptr, s);
+                          p.gamma2_exp, p.beta2_exp, p.ln2_out_exp, nullptr, lw, s);
   }
   if (rc) return rc;
   g = GemmArgs{};
@@ -225,9 +254,10 @@ static int check_block(const hv_block_dev &p) {
                    p.msa_out_exp, p.ffn_x_exp, p.gamma2_exp, p.beta2_exp, p.ln2_out_exp,
                    p.w1_exp, p.hidden_out_exp, p.w2_exp, p.ffn_out_exp, p.out_exp};
   for (int v : e)
-    if (!exp_ok(v)) return fail(HV_EVALUE, "block scale exponent %d outside [-32, 31]", v);
+    if (!exp_ok(v))
+      return fail(HV_EVALUE, HV_ERR_DIMENSION, "block scale exponent %d outside [-32, 31]", v);
   if (p.x_exp > 0 || p.ffn_x_exp > 0)
-    return fail(HV_EVALUE, "layernorm input scale must be in [-32, 0]");
+    return fail(HV_EVALUE, HV_ERR_DIMENSION, "layernorm input scale must be in [-32, 0]");
   return HV_OK;
 }
 
@@ -239,31 +269,33 @@ extern "C" {
 
 const char *hv_last_error(void) { return g_err; }
 
-int hv_abi_version(void) { return 2; }
+int hv_last_error_class(void) { return g_err_class; }
+
+int hv_abi_version(void) { return 3; }
 
 int hv_eval_primitive(int op, const int64_t *in, int64_t *out, int64_t n, int a, int b, int c,
                       hv_stream_t stream) {
-  g_err[0] = 0;
+  clear_error();
   return launch_primitive(op, in, out, n, a, b, c, (hipStream_t)stream);
 }
 
 int hv_softmax_rows(const int32_t *x, const int32_t *offsets, int rows, uint8_t *attention,
                     int32_t *selector, hv_stream_t stream) {
-  g_err[0] = 0;
+  clear_error();
   return launch_softmax_rows(x, offsets, rows, attention, selector, (hipStream_t)stream);
 }
 
 int hv_layernorm_i8(const int8_t *x, const int8_t *gamma, const int8_t *beta, int8_t *y,
                     int rows, const int32_t *rows_dev, int x_exp, int gamma_exp, int beta_exp,
                     int out_exp, uint8_t *neg_var, hv_stream_t stream) {
-  g_err[0] = 0;
+  clear_error();
   return launch_layernorm(x, gamma, beta, y, rows, rows_dev, x_exp, gamma_exp, beta_exp,
-                          out_exp, neg_var, (hipStream_t)stream);
+                          out_exp, neg_var, LnWarn{}, (hipStream_t)stream);
 }
 
 int hv_gemm_i8(const hv_gemm_desc *d, hv_stream_t stream) {
-  g_err[0] = 0;
-  if (!d) return fail(HV_EVALUE, "gemm: null descriptor");
+  clear_error();
+  if (!d) return fail(HV_EVALUE, HV_ERR_ADDRESS, "gemm: null descriptor");
   GemmArgs g{};
   g.a = d->a; g.a_rows = d->a_rows; g.b = d->b_packed; g.bias = d->bias; g.c = d->c;
   g.res = d->residual; g.aux = d->aux; g.m_dev = d->m_dev;
@@ -276,13 +308,15 @@ int hv_gemm_i8(const hv_gemm_desc *d, hv_stream_t stream) {
       g.shift_b = d->dst_exp + 16;
       break;
     case HV_EPI_RESIDUAL:
-      if (!d->residual) return fail(HV_EVALUE, "gemm: residual epilogue needs a residual");
+      if (!d->residual)
+        return fail(HV_EVALUE, HV_ERR_ADDRESS, "gemm: residual epilogue needs a residual");
       g.shift_a = d->mid_exp - d->src_exp;
       g.mid_exp = d->mid_exp; g.res_exp = d->res_exp; g.out_exp = d->dst_exp;
       break;
-    default: return fail(HV_EVALUE, "gemm: bad epilogue %d", d->epilogue);
+    default: return fail(HV_EVALUE, HV_ERR_OPCODE, "gemm: bad epilogue %d", d->epilogue);
   }
-  if (d->a_mode == HV_A_GATHER && !d->a_rows) return fail(HV_EVALUE, "gemm: gather without rows");
+  if (d->a_mode == HV_A_GATHER && !d->a_rows)
+    return fail(HV_EVALUE, HV_ERR_ADDRESS, "gemm: gather without rows");
   return launch_gemm(g, d->a_mode, d->epilogue, (hipStream_t)stream);
 }
 
@@ -294,17 +328,20 @@ size_t hv_block_workspace_bytes(int batch, int max_rows) {
 }
 
 int hv_block_forward(const hv_block_dev *p, const int8_t *x, const int32_t *offsets, int batch,
-                     int max_rows, int8_t *z, const hv_block_ckpt *ck, void *workspace,
-                     size_t workspace_bytes, hv_stream_t stream) {
-  g_err[0] = 0;
-  if (!p || !x || !offsets || !z) return fail(HV_EVALUE, "block: null argument");
-  if (batch <= 0 || max_rows <= 0) return fail(HV_EVALUE, "block: empty batch");
+                     int max_rows, int8_t *z, const hv_block_ckpt *ck, int32_t *status,
+                     int32_t *warnings, void *workspace, size_t workspace_bytes,
+                     hv_stream_t stream) {
+  clear_error();
+  if (!p || !x || !offsets || !z) return fail(HV_EVALUE, HV_ERR_ADDRESS, "block: null argument");
+  if (batch <= 0 || max_rows <= 0) return fail(HV_EVALUE, HV_ERR_DIMENSION, "block: empty batch");
   int rc = check_block(*p);
   if (rc) return rc;
   Carve cv{(uint8_t *)workspace, workspace_bytes};
   BlockWs w = carve_block(cv, (size_t)max_rows);
-  if (!cv.ok || !workspace) return fail(HV_EVALUE, "block: workspace too small");
-  return block_forward(*p, x, offsets, batch, max_rows, z, ck, w, (hipStream_t)stream);
+  if (!cv.ok || !workspace) return fail(HV_EVALUE, HV_ERR_ADDRESS, "block: workspace too small");
+  if ((rc = launch_image_check(offsets, batch, max_rows, status, warnings, (hipStream_t)stream)))
+    return rc;
+  return block_forward(*p, x, offsets, batch, max_rows, z, ck, warnings, w, (hipStream_t)stream);
 }
 
 struct SelectorWs {
@@ -331,14 +368,14 @@ int hv_selector_forward(const hv_selector_dev *p, const int8_t *tokens, const in
                         int32_t *out_offsets, uint8_t *pkg_out, int32_t *fused,
                         int32_t *kept_index, int32_t *state, const hv_selector_ckpt *ck,
                         void *workspace, size_t workspace_bytes, hv_stream_t stream) {
-  g_err[0] = 0;
+  clear_error();
   if (!p || !tokens || !offsets || !out_tokens || !out_offsets || !pkg_out || !fused ||
       !kept_index || !state)
-    return fail(HV_EVALUE, "selector: null argument");
+    return fail(HV_EVALUE, HV_ERR_ADDRESS, "selector: null argument");
   if (batch <= 0) return HV_OK;
   Carve cv{(uint8_t *)workspace, workspace_bytes};
   const SelectorWs w = carve_selector(cv, batch);
-  if (!cv.ok || !workspace) return fail(HV_EVALUE, "selector: workspace too small");
+  if (!cv.ok || !workspace) return fail(HV_EVALUE, HV_ERR_ADDRESS, "selector: workspace too small");
   SelectorArgs a{};
   a.hs = w.hs;
   a.stats = w.stats;
@@ -353,10 +390,10 @@ int hv_selector_finalize(const int8_t *tokens, const int32_t *offsets, const uin
                          const int32_t *fused, int batch, int8_t *out_tokens,
                          int32_t *out_offsets, uint8_t *pkg_out, int32_t *kept_index,
                          int32_t *state, hv_stream_t stream) {
-  g_err[0] = 0;
+  clear_error();
   if (!tokens || !offsets || !fused || !out_tokens || !out_offsets || !pkg_out || !kept_index ||
       !state)
-    return fail(HV_EVALUE, "finalize: null argument");
+    return fail(HV_EVALUE, HV_ERR_ADDRESS, "finalize: null argument");
   SelectorArgs a{};
   a.p = nullptr; a.tokens = tokens; a.offsets = offsets; a.pkg_in = pkg_in; a.batch = batch;
   a.out_tokens = out_tokens; a.out_offsets = out_offsets; a.pkg_out = pkg_out;
@@ -366,12 +403,13 @@ int hv_selector_finalize(const int8_t *tokens, const int32_t *offsets, const uin
 
 int hv_patch_embedding(const hv_patch_dev *p, const int8_t *images, int batch, int8_t *x,
                        hv_stream_t stream) {
-  g_err[0] = 0;
-  if (!p || !images || !x) return fail(HV_EVALUE, "patch: null argument");
+  clear_error();
+  if (!p || !images || !x) return fail(HV_EVALUE, HV_ERR_ADDRESS, "patch: null argument");
   const int e[] = {p->image_exp, p->weight_exp, p->activation_exp, p->tokens_exp, p->cls_exp,
                    p->pos_exp};
   for (int v : e)
-    if (!exp_ok(v)) return fail(HV_EVALUE, "patch scale exponent %d outside [-32, 31]", v);
+    if (!exp_ok(v))
+      return fail(HV_EVALUE, HV_ERR_DIMENSION, "patch scale exponent %d outside [-32, 31]", v);
   return launch_patch_embed(*p, images, batch, x, (hipStream_t)stream);
 }
 
@@ -407,30 +445,34 @@ size_t hv_model_workspace_bytes(int batch) {
 }
 
 int hv_model_forward(const hv_model_dev *p, const int8_t *images, int batch, int32_t *logits,
-                     int32_t *token_counts, int32_t *state, int8_t *ckpt, int32_t *ckpt_rows,
-                     void *workspace, size_t workspace_bytes, hv_stream_t stream) {
-  g_err[0] = 0;
+                     int32_t *token_counts, int32_t *state, int32_t *warnings, int8_t *ckpt,
+                     int32_t *ckpt_rows, void *workspace, size_t workspace_bytes,
+                     hv_stream_t stream) {
+  clear_error();
   hipStream_t s = (hipStream_t)stream;
-  if (!p || !images || !logits) return fail(HV_EVALUE, "model: null argument");
-  if (batch <= 0) return fail(HV_EVALUE, "model: empty batch");
+  if (!p || !images || !logits) return fail(HV_EVALUE, HV_ERR_ADDRESS, "model: null argument");
+  if (batch <= 0) return fail(HV_EVALUE, HV_ERR_DIMENSION, "model: empty batch");
   if ((long long)batch * HV_MAX_TOKENS * 768 > 0x7fffffffLL)
-    return fail(HV_EVALUE, "model: batch %d too large", batch);
-  if (p->n_selectors < 0 || p->n_selectors > 3) return fail(HV_EVALUE, "model: bad selector count");
+    return fail(HV_EVALUE, HV_ERR_DIMENSION, "model: batch %d too large", batch);
+  if (p->n_selectors < 0 || p->n_selectors > 3)
+    return fail(HV_EVALUE, HV_ERR_DIMENSION, "model: bad selector count");
   for (int i = 0; i < 12; ++i) {
     int rc = check_block(p->blocks[i]);
     if (rc) return rc;
   }
-  if (p->blocks[11].out_exp > 0) return fail(HV_EVALUE, "layernorm input scale must be in [-32, 0]");
+  if (p->blocks[11].out_exp > 0)
+    return fail(HV_EVALUE, HV_ERR_DIMENSION, "layernorm input scale must be in [-32, 0]");
   Carve cv{(uint8_t *)workspace, workspace_bytes};
   ModelWs w = carve_model(cv, batch);
-  if (!cv.ok || !workspace) return fail(HV_EVALUE, "model: workspace too small");
+  if (!cv.ok || !workspace) return fail(HV_EVALUE, HV_ERR_ADDRESS, "model: workspace too small");
   const int max_rows = batch * HV_MAX_TOKENS;
   int32_t *st = state ? state : w.state;
   int rc;
 
   {
     ProfScope ps(HV_PROF_OTHER, s);
-    rc = launch_init_offsets(w.off_a, w.pkg_a, token_counts, batch, HV_MAX_TOKENS, s);
+    rc = launch_init_offsets(w.off_a, w.pkg_a, token_counts, warnings, batch, HV_MAX_TOKENS,
+                             s);
   }
   if (rc) return rc;
   {
@@ -449,7 +491,7 @@ int hv_model_forward(const hv_model_dev *p, const int8_t *images, int batch, int
       a.out_tokens = w.xb; a.out_offsets = w.off_b; a.pkg_out = w.pkg_b;
       a.fused = w.fused; a.kept_index = w.kept; a.state = st + (size_t)sel * batch * 5;
       a.hs = w.sel.hs; a.stats = w.sel.stats;
-      a.token_counts = token_counts; a.stage = sel + 1;
+      a.token_counts = token_counts; a.stage = sel + 1; a.img_warn = warnings;
       {
         ProfScope ps(HV_PROF_SELECTOR, s);
         rc = launch_selector(a, s);
@@ -462,7 +504,7 @@ int hv_model_forward(const hv_model_dev *p, const int8_t *images, int batch, int
       if (ckpt && (rc = launch_copy_ckpt(w.xa, w.off_a, batch, ckpt, ckpt_rows, sel, s))) return rc;
     }
     if ((rc = block_forward(p->blocks[blk - 1], w.xa, w.off_a, batch, max_rows, w.xb, nullptr,
-                            w.blk, s)))
+                            warnings, w.blk, s)))
       return rc;
     std::swap(w.xa, w.xb);
     if (ckpt && (rc = launch_copy_ckpt(w.xa, w.off_a, batch, ckpt, ckpt_rows, 3 + blk, s))) return rc;
@@ -472,7 +514,8 @@ int hv_model_forward(const hv_model_dev *p, const int8_t *images, int batch, int
     ProfScope ps(HV_PROF_LAYERNORM, s);
     rc = launch_layernorm(w.xa, p->final_gamma, p->final_beta, w.blk.ln, max_rows,
                           w.off_a + batch, p->blocks[11].out_exp, p->final_gamma_exp,
-                          p->final_beta_exp, p->final_ln_out_exp, nullptr, s);
+                          p->final_beta_exp, p->final_ln_out_exp, nullptr,
+                          LnWarn{w.off_a, batch, warnings}, s);
   }
   if (rc) return rc;
   if (ckpt && (rc = launch_copy_ckpt(w.blk.ln, w.off_a, batch, ckpt, ckpt_rows, 16, s))) return rc;
@@ -491,7 +534,7 @@ int hv_profile_enable(int on) {
 }
 
 int hv_profile_read(float *ms, int32_t *launches, int n) {
-  g_err[0] = 0;
+  clear_error();
   for (int i = 0; i < n; ++i) {
     if (ms) ms[i] = 0.f;
     if (launches) launches[i] = 0;

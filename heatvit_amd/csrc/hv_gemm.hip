@@ -593,11 +593,12 @@ static int run_lds(const GemmArgs &g, hipStream_t s) {
 template <int EPI>
 static int dispatch(const GemmArgs &g, int a_mode, hipStream_t s) {
   if constexpr (EPI == EPI_PATCH) {
-    if (a_mode != A_PATCH || g.k != 768) return fail(HV_EVALUE, "gemm: bad patch GEMM");
+    if (a_mode != A_PATCH || g.k != 768)
+      return fail(HV_EVALUE, HV_ERR_DIMENSION, "gemm: bad patch GEMM");
     return run_lds<2, 1, 2, EPI_PATCH, A_PATCH, 24>(g, s);
   } else {
     if (a_mode == A_GATHER) return run<1, 1, 2, EPI, A_GATHER, 0>(g, s);
-    if (a_mode != A_ROWS) return fail(HV_EVALUE, "gemm: bad A mode %d", a_mode);
+    if (a_mode != A_ROWS) return fail(HV_EVALUE, HV_ERR_OPCODE, "gemm: bad A mode %d", a_mode);
     if constexpr (EPI == EPI_GELU) {
       if (g.k == 192) return run<1, 1, 2, EPI, A_ROWS, 6>(g, s);
     } else if constexpr (EPI != EPI_I32) {
@@ -611,16 +612,18 @@ static int dispatch(const GemmArgs &g, int a_mode, hipStream_t s) {
 int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
   GemmArgs g = g_in;
   epilogue_limits_pub(g, epi);
-  if (g.k <= 0 || g.k % 32) return fail(HV_EVALUE, "gemm: K=%d must be a positive multiple of 32", g.k);
-  if (g.n <= 0) return fail(HV_EVALUE, "gemm: N=%d must be positive", g.n);
-  if (g.m < 0) return fail(HV_EVALUE, "gemm: M=%d must be non-negative", g.m);
+  if (g.k <= 0 || g.k % 32)
+    return fail(HV_EVALUE, HV_ERR_DIMENSION, "gemm: K=%d must be a positive multiple of 32", g.k);
+  if (g.n <= 0) return fail(HV_EVALUE, HV_ERR_DIMENSION, "gemm: N=%d must be positive", g.n);
+  if (g.m < 0) return fail(HV_EVALUE, HV_ERR_DIMENSION, "gemm: M=%d must be non-negative", g.m);
   if (a_mode != A_PATCH && (g.lda % 16 || ((uintptr_t)g.a & 15)))
-    return fail(HV_EVALUE, "gemm: A must be 16-byte aligned with lda %% 16 == 0");
+    return fail(HV_EVALUE, HV_ERR_ADDRESS, "gemm: A must be 16-byte aligned with lda %% 16 == 0");
   if (a_mode == A_PATCH && ((uintptr_t)g.a & 15))
-    return fail(HV_EVALUE, "gemm: images must be 16-byte aligned");
+    return fail(HV_EVALUE, HV_ERR_ADDRESS, "gemm: images must be 16-byte aligned");
   if (g.bias && ((uintptr_t)g.bias & 15))
-    return fail(HV_EVALUE, "gemm: bias must be 16-byte aligned");
-  if (g.k > 131071) return fail(HV_EOVERFLOW, "gemm: K=%d may overflow int32", g.k);
+    return fail(HV_EVALUE, HV_ERR_ADDRESS, "gemm: bias must be 16-byte aligned");
+  if (g.k > 131071)
+    return fail(HV_EOVERFLOW, HV_ERR_DIMENSION, "gemm: K=%d may overflow int32", g.k);
   const int esz = epi == EPI_I32 ? 4 : 1;
   g.vec_out = ((uintptr_t)g.c & 15) == 0 && (g.ldc * esz) % 16 == 0 &&
               (!g.aux || ((uintptr_t)g.aux & 15) == 0);
@@ -632,7 +635,7 @@ int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
     case EPI_GELU: return dispatch<EPI_GELU>(g, a_mode, s);
     case EPI_RES: return dispatch<EPI_RES>(g, a_mode, s);
     case EPI_PATCH: return dispatch<EPI_PATCH>(g, a_mode, s);
-    default: return fail(HV_EVALUE, "gemm: bad epilogue %d", epi);
+    default: return fail(HV_EVALUE, HV_ERR_OPCODE, "gemm: bad epilogue %d", epi);
   }
 }
 

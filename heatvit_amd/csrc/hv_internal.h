@@ -10,8 +10,8 @@
 
 namespace hv {
 
-// Error reporting (thread-local message, see hv_capi.hip).
-int fail(int status, const char *fmt, ...);
+// Error reporting: a thread-local message and HV_ERR_* class (hv_capi.hip).
+int fail(int status, int cls, const char *fmt, ...);
 int check_hip(hipError_t e, const char *what);
 
 // Kernel launch.  While kernel-class profiling is on and a class is active
@@ -66,9 +66,18 @@ int launch_patch_embed(const hv_patch_dev &p, const int8_t *images, int batch, i
 bool ln32_setup(const int8_t *g, const int8_t *b, int8_t *y, int x_exp, int g_exp, int b_exp,
                 int out_exp, Ln32 *ln);
 
+// Per-image warning sink of the LayerNorm kernels: a row with a negative
+// variance ORs HV_WARN_LN_NEGATIVE_VARIANCE into img_warn[b] of the image b
+// whose rows offsets[b] .. offsets[b+1] hold it.  img_warn NULL: off.
+struct LnWarn {
+  const int32_t *offsets;
+  int batch;
+  int32_t *img_warn;
+};
+
 int launch_layernorm(const int8_t *x, const int8_t *g, const int8_t *b, int8_t *y, int rows,
                      const int32_t *rows_dev, int x_exp, int g_exp, int b_exp, int out_exp,
-                     uint8_t *neg_var, hipStream_t s);
+                     uint8_t *neg_var, const LnWarn &lw, hipStream_t s);
 
 struct AttnArgs {
   const int8_t *qkv;  // [T][576]
@@ -82,6 +91,7 @@ struct AttnArgs {
   int ctx_shift;      // context_out_exp - (prob_exp + qkv_out_exp)
   int q16_mode, q16_s, q16_rnd;  // int32 fast path for the score -> Q8.16 conversion
   int ctx_fast, ctx_rnd;         // int32 context requant (shift in [1, 30])
+  int rows_cap;                  // rows of qkv / ctx; images outside are skipped
 };
 int launch_attention(const AttnArgs &a, hipStream_t s);
 
@@ -106,13 +116,19 @@ struct SelectorArgs {
   int8_t *stats;        // workspace [B][196][3] head statistics
   int32_t *token_counts;  // optional [B][4] column `stage`
   int stage;
+  int32_t *img_warn;      // optional [B]: the state's warning bits are ORed in
   hv_selector_ckpt ck;    // optional intermediate outputs (null pointers skip)
 };
 int launch_selector(const SelectorArgs &a, hipStream_t s);
 
 // Small utility kernels.
-int launch_init_offsets(int32_t *offsets, uint8_t *pkg, int32_t *token_counts, int batch,
-                        int rows_per_image, hipStream_t s);
+int launch_init_offsets(int32_t *offsets, uint8_t *pkg, int32_t *token_counts,
+                        int32_t *warnings, int batch, int rows_per_image, hipStream_t s);
+// Per-image token-count check of a caller's offsets: status[b] =
+// HV_ERR_TOKEN_COUNT unless 1 <= count <= 197 and the rows lie in
+// [0, capacity), else 0; warnings[b] = 0.  Either pointer may be NULL.
+int launch_image_check(const int32_t *offsets, int batch, int capacity, int32_t *status,
+                       int32_t *warnings, hipStream_t s);
 int launch_copy_ckpt(const int8_t *x, const int32_t *offsets, int batch, int8_t *ckpt,
                      int32_t *ckpt_rows, int slot, hipStream_t s);
 int launch_cls_rows(const int32_t *offsets, int batch, int32_t *rows_out, hipStream_t s);

@@ -16,6 +16,19 @@ namespace hv {
 //  * gamma/beta alignment (shifts gs <= 30, bs <= 54): |aligned| < 2^62.
 // Other exponents take the 128-bit route (mean^2 < 2^78 always does).
 // ---------------------------------------------------------------------------
+// Image of `row` (the last b with offsets[b] <= row, in [0, batch)) gets
+// the negative-variance warning bit.  Rare: only rows that clamp reach it.
+__device__ __noinline__ void ln_warn_row(const int32_t *offsets, int batch, int32_t *img_warn,
+                                         int row) {
+  int lo = 0, hi = batch - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (offsets[mid] <= row) lo = mid;
+    else hi = mid - 1;
+  }
+  atomicOr(img_warn + lo, HV_WARN_LN_NEGATIVE_VARIANCE);
+}
+
 template <bool FAST_NORM, bool FAST_ALIGN>
 __global__ __launch_bounds__(256) void k_layernorm(const int8_t *__restrict__ x,
                                                    const int8_t *__restrict__ gamma,
@@ -23,7 +36,7 @@ __global__ __launch_bounds__(256) void k_layernorm(const int8_t *__restrict__ x,
                                                    int8_t *__restrict__ y, int rows,
                                                    const int32_t *rows_dev, int x_exp,
                                                    int g_exp, int b_exp, int out_exp,
-                                                   uint8_t *neg_var) {
+                                                   uint8_t *neg_var, LnWarn lw) {
   const int sub = threadIdx.x & 15;  // lane within the row group
   const int R = rows_dev ? min(*rows_dev, rows) : rows;
   // Grid-stride over rows: the grid is sized for the chip, not for the
@@ -90,6 +103,7 @@ __global__ __launch_bounds__(256) void k_layernorm(const int8_t *__restrict__ x,
   yr[1] = out[1];
   yr[2] = out[2];
   if (neg_var && sub == 0) neg_var[row] = neg ? 1 : 0;
+  if (neg && lw.img_warn && sub == 0) ln_warn_row(lw.offsets, lw.batch, lw.img_warn, row);
   }  // row loop
 }
 
@@ -100,7 +114,7 @@ __global__ __launch_bounds__(256) void k_layernorm(const int8_t *__restrict__ x,
 // 24-bit multiply-adds for norm_q16, one for gamma/beta and the requant.
 __global__ __launch_bounds__(256) void k_layernorm32(const int8_t *__restrict__ x, Ln32 ln,
                                                      int rows, const int32_t *rows_dev,
-                                                     uint8_t *neg_var) {
+                                                     uint8_t *neg_var, LnWarn lw) {
   const int sub = threadIdx.x & 7;
   const int R = rows_dev ? min(*rows_dev, rows) : rows;
   int gm[6], bt[6];
@@ -119,6 +133,7 @@ __global__ __launch_bounds__(256) void k_layernorm32(const int8_t *__restrict__ 
 #pragma unroll
     for (int q = 0; q < 3; ++q) yr[q] = int2{out[2 * q], out[2 * q + 1]};
     if (neg_var && sub == 0) neg_var[row] = neg ? 1 : 0;
+    if (neg && lw.img_warn && sub == 0) ln_warn_row(lw.offsets, lw.batch, lw.img_warn, row);
   }
 }
 
@@ -137,18 +152,19 @@ bool ln32_setup(const int8_t *g, const int8_t *b, int8_t *y, int x_exp, int g_ex
 
 int launch_layernorm(const int8_t *x, const int8_t *g, const int8_t *b, int8_t *y, int rows,
                      const int32_t *rows_dev, int x_exp, int g_exp, int b_exp, int out_exp,
-                     uint8_t *neg_var, hipStream_t s) {
+                     uint8_t *neg_var, const LnWarn &lw, hipStream_t s) {
   if (x_exp < -32 || x_exp > 0)
-    return fail(HV_EVALUE, "layernorm input scale must be in [-32, 0] (got %d)", x_exp);
+    return fail(HV_EVALUE, HV_ERR_DIMENSION,
+                "layernorm input scale must be in [-32, 0] (got %d)", x_exp);
   if (rows <= 0) return HV_OK;
   if (((uintptr_t)x & 3) || ((uintptr_t)y & 3))
-    return fail(HV_EVALUE, "layernorm: rows must be 4-byte aligned");
+    return fail(HV_EVALUE, HV_ERR_ADDRESS, "layernorm: rows must be 4-byte aligned");
   const int common = (g_exp - 16) < b_exp ? (g_exp - 16) : b_exp;
   Ln32 ln;
   if (((uintptr_t)x & 7) == 0 && ln32_setup(g, b, y, x_exp, g_exp, b_exp, out_exp, &ln)) {
     const int blocks = (rows + 31) / 32;
     hv_launch(k_layernorm32, dim3(blocks < 256 * 8 ? blocks : 256 * 8), dim3(256), 0, s, x, ln,
-              rows, rows_dev, neg_var);
+              rows, rows_dev, neg_var, lw);
     return check_hip(hipGetLastError(), "k_layernorm32 launch");
   }
   const bool fast_norm = x_exp <= -1;
@@ -157,16 +173,16 @@ int launch_layernorm(const int8_t *x, const int8_t *g, const int8_t *b, int8_t *
   const dim3 grid(blocks < 256 * 8 ? blocks : 256 * 8), block(256);
   if (fast_norm && fast_align)
     hv_launch((k_layernorm<true, true>), grid, block, 0, s, x, g, b, y, rows, rows_dev,
-                       x_exp, g_exp, b_exp, out_exp, neg_var);
+                       x_exp, g_exp, b_exp, out_exp, neg_var, lw);
   else if (fast_norm)
     hv_launch((k_layernorm<true, false>), grid, block, 0, s, x, g, b, y, rows,
-                       rows_dev, x_exp, g_exp, b_exp, out_exp, neg_var);
+                       rows_dev, x_exp, g_exp, b_exp, out_exp, neg_var, lw);
   else if (fast_align)
     hv_launch((k_layernorm<false, true>), grid, block, 0, s, x, g, b, y, rows,
-                       rows_dev, x_exp, g_exp, b_exp, out_exp, neg_var);
+                       rows_dev, x_exp, g_exp, b_exp, out_exp, neg_var, lw);
   else
     hv_launch((k_layernorm<false, false>), grid, block, 0, s, x, g, b, y, rows,
-                       rows_dev, x_exp, g_exp, b_exp, out_exp, neg_var);
+                       rows_dev, x_exp, g_exp, b_exp, out_exp, neg_var, lw);
   return check_hip(hipGetLastError(), "k_layernorm launch");
 }
 
@@ -233,7 +249,9 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
   const int b = blockIdx.x / 3, h = blockIdx.x - 3 * (blockIdx.x / 3);
   const int row0 = g.offsets[b];
   const int N = g.offsets[b + 1] - row0;
-  if (N <= 0 || N > HV_MAX_TOKENS) return;  // host validates N <= 197
+  // Images with a token count outside [1, 197] or rows outside the
+  // buffers are skipped (reported by the block's image check).
+  if (N <= 0 || N > HV_MAX_TOKENS || row0 < 0 || row0 > g.rows_cap - N) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n16 = (N + 15) >> 4;  // key / query tiles
   const int n64 = (N + 63) >> 6;  // PV chunks of 64 keys
@@ -468,12 +486,12 @@ __global__ void k_primitive(int op, const int64_t *in, int64_t *out, int64_t n, 
 
 int launch_primitive(int op, const int64_t *in, int64_t *out, int64_t n, int a, int b, int c,
                      hipStream_t s) {
-  if (op < 0 || op > HV_PRIM_RSA) return fail(HV_EVALUE, "unknown primitive %d", op);
+  if (op < 0 || op > HV_PRIM_RSA) return fail(HV_EVALUE, HV_ERR_OPCODE, "unknown primitive %d", op);
   if (op == HV_PRIM_REQUANT && (c < 2 || c > 63))
-    return fail(HV_EVALUE, "requant bits must be in [2, 63]");
+    return fail(HV_EVALUE, HV_ERR_DIMENSION, "requant bits must be in [2, 63]");
   if (n <= 0) return HV_OK;
   const int64_t blocks = (n + 255) / 256;
-  if (blocks > 0x7fffffff) return fail(HV_EVALUE, "too many elements");
+  if (blocks > 0x7fffffff) return fail(HV_EVALUE, HV_ERR_DIMENSION, "too many elements");
   hv_launch(k_primitive, dim3((unsigned)blocks), dim3(256), 0, s, op, in, out, n, a, b,
                      c);
   return check_hip(hipGetLastError(), "k_primitive launch");

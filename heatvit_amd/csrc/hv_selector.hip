@@ -59,7 +59,7 @@ __global__ __launch_bounds__(256) void k_selector_head(hv_selector_dev p, const 
   const int b = blockIdx.x / 3, h = blockIdx.x - 3 * (blockIdx.x / 3), tid = threadIdx.x;
   const int row0 = offsets[b], N = offsets[b + 1] - row0, C = N - 1;
   const int pkg = pkg_in ? (pkg_in[b] ? 1 : 0) : 0;
-  if (C < 1 || C > kMaxCand || C - pkg < 1) return;  // reported by k_selector_keep
+  if (C < 1 || C > kMaxCand || C - pkg < 1 || row0 < 0) return;  // k_selector_keep reports
 
   {
     const int *src = reinterpret_cast<const int *>(p.local_wt) + h * 512;
@@ -257,12 +257,13 @@ __global__ __launch_bounds__(64) void k_selector_keep(const int32_t *offsets,
                                                       const uint8_t *pkg_in, int32_t *fused,
                                                       int32_t *kept_index, int32_t *state,
                                                       hv_selector_dev p, const int32_t *hs,
-                                                      const int8_t *stats, int32_t *weights_ck) {
+                                                      const int8_t *stats, int32_t *weights_ck,
+                                                      int32_t *img_warn) {
   const int b = blockIdx.x, lane = threadIdx.x;
   const int C = offsets[b + 1] - offsets[b] - 1;
   const int pkg = pkg_in ? (pkg_in[b] ? 1 : 0) : 0;
   int32_t *st = state + (size_t)b * 5;
-  if (C < 1 || C > kMaxCand || C - pkg < 1) {
+  if (C < 1 || C > kMaxCand || C - pkg < 1 || offsets[b] < 0) {
     // token_selector needs CLS plus one candidate (selector.py:513-514) and
     // an incoming package needs a normal candidate beside it (:448-449);
     // the state's token count -1 reports the ValueError.
@@ -312,7 +313,10 @@ __global__ __launch_bounds__(64) void k_selector_keep(const int32_t *offsets,
     st[1] = exists;
     st[2] = kept;
     st[3] = n_part - pkg;
-    st[4] = (warn_head ? 1 : 0) | ((exists && den == 0) ? 2 : 0);
+    const int warn = (warn_head ? HV_WARN_HEAD_DEN_ZERO : 0) |
+                     ((exists && den == 0) ? HV_WARN_PACKAGE_DEN_ZERO : 0);
+    st[4] = warn;
+    if (img_warn) img_warn[b] |= warn;
   }
 }
 
@@ -408,7 +412,7 @@ int launch_selector(const SelectorArgs &a, hipStream_t s) {
   int rc = HV_OK;
   hv_selector_dev p{};
   if (a.p) {
-    if (!a.hs || !a.stats) return fail(HV_EVALUE, "selector: missing workspace");
+    if (!a.hs || !a.stats) return fail(HV_EVALUE, HV_ERR_ADDRESS, "selector: missing workspace");
     p = *a.p;
     auto in = [](int v) { return v >= -30 && v <= 30; };
     const int fast = in(-16 - (p.in_exp + p.local_w_exp)) && in(p.local_out_exp + 16) &&
@@ -420,7 +424,7 @@ int launch_selector(const SelectorArgs &a, hipStream_t s) {
   }
   hv_launch(k_selector_keep, dim3(a.batch), dim3(64), 0, s, a.offsets, a.pkg_in,
                      a.fused, a.kept_index, a.state, p, a.p ? a.hs : nullptr,
-                     a.p ? a.stats : nullptr, a.p ? a.ck.head_weights : nullptr);
+                     a.p ? a.stats : nullptr, a.p ? a.ck.head_weights : nullptr, a.img_warn);
   if ((rc = check_hip(hipGetLastError(), "k_selector_keep launch"))) return rc;
   hv_launch(k_selector_compact, dim3(a.batch), dim3(256), 0, s, a.tokens, a.offsets,
                      a.pkg_in, a.batch, a.fused, a.kept_index, a.state, a.out_tokens,

@@ -3,8 +3,11 @@
 HeatViTModel.infer keeps the golden model's signature and result
 (model.py:49-123): logits (1000 int32 at LOGIT_SCALE_EXP = -14), the
 18 checkpoints (patch, selector_NN, block_NN, final_ln, logits) and the
-selector summary.  HeatViTModel.infer_batch and Engine run many images per
-launch sequence; pruned images keep ragged token counts on the device.
+selector summary, plus the engine's warning bits of the forward
+(WARN_HEAD_DEN_ZERO | WARN_PACKAGE_DEN_ZERO | WARN_LN_NEGATIVE_VARIANCE,
+heatvit_pkg.sv:120-122), which the golden model computes and drops.
+HeatViTModel.infer_batch and Engine run many images per launch sequence;
+pruned images keep ragged token counts on the device.
 """
 
 from dataclasses import dataclass
@@ -17,6 +20,7 @@ from .device import DeviceModel
 from .params import HeatViTParams
 
 LOGIT_SCALE_EXP = -14
+WARN_HEAD_DEN_ZERO, WARN_PACKAGE_DEN_ZERO, WARN_LN_NEGATIVE_VARIANCE = 1, 2, 4
 IMAGE_BYTES = 224 * 224 * 3
 CKPT_NAMES = (["patch"] + [f"selector_{i:02d}" for i in range(1, 4)] +
               [f"block_{i:02d}" for i in range(1, 13)] + ["final_ln"])
@@ -28,6 +32,7 @@ class ModelResult:
     output_scale_exp: int
     checkpoints: dict
     selector_summary: tuple
+    warnings: int = 0          # engine warning bits of the forward
 
 
 @dataclass(frozen=True)
@@ -36,13 +41,15 @@ class BatchResult:
     output_scale_exp: int
     token_counts: np.ndarray   # [B][4]: rows entering block 1 and after each selector
     selector_state: np.ndarray  # [n_selectors][B][5]: count, package, kept, pruned, warnings
+    warnings: np.ndarray = None  # [B] engine warning bits of each image's forward
     checkpoints: list = None   # per image dict when requested
 
 
 class Engine:
     """Device-resident model plus a reusable workspace for batches of up to
     `max_batch` images.  `forward(images)` takes a device int8 tensor
-    [B][150528] and enqueues the whole forward on the current stream."""
+    [B][150528] and enqueues the whole forward on the current stream; it
+    returns device views (logits, token_counts, selector state, warnings)."""
 
     def __init__(self, params, max_batch, device="cuda"):
         self.model = params if isinstance(params, DeviceModel) else DeviceModel(params, device)
@@ -54,6 +61,7 @@ class Engine:
         self.logits = torch.empty((self.max_batch, 1000), dtype=torch.int32, device=dev)
         self.token_counts = torch.empty((self.max_batch, 4), dtype=torch.int32, device=dev)
         self.state = torch.zeros((3, self.max_batch, 5), dtype=torch.int32, device=dev)
+        self.warnings = torch.zeros(self.max_batch, dtype=torch.int32, device=dev)
 
     def forward(self, images, ckpt=None, ckpt_rows=None):
         b = images.shape[0]
@@ -66,12 +74,12 @@ class Engine:
             torch.zeros((3, b, 5), dtype=torch.int32, device=images.device)
         _lib.check(_lib.lib().hv_model_forward(
             self.model.struct, images.data_ptr(), b, self.logits.data_ptr(),
-            self.token_counts.data_ptr(), state.data_ptr(),
+            self.token_counts.data_ptr(), state.data_ptr(), self.warnings.data_ptr(),
             None if ckpt is None else ckpt.data_ptr(),
             None if ckpt_rows is None else ckpt_rows.data_ptr(),
             self.workspace.data_ptr(), self.workspace.numel(),
             torch.cuda.current_stream(images.device).cuda_stream), "model forward")
-        return self.logits[:b], self.token_counts[:b], state
+        return self.logits[:b], self.token_counts[:b], state, self.warnings[:b]
 
 
 def _images(images):
@@ -107,7 +115,7 @@ class HeatViTModel:
         if checkpoints:
             ck = torch.zeros((b, 17, 197, 192), dtype=torch.int8, device="cuda")
             ck_rows = torch.zeros((b, 17), dtype=torch.int32, device="cuda")
-        logits, counts, state = eng.forward(dev, ck, ck_rows)
+        logits, counts, state, warnings = eng.forward(dev, ck, ck_rows)
         n_sel = len(params.selectors)
         state = state.cpu().numpy()[:n_sel]
         if (state[:, :, 0] < 0).any():
@@ -124,7 +132,7 @@ class HeatViTModel:
                 cks.append(d)
         return BatchResult(logits=logits.cpu().numpy().copy(), output_scale_exp=LOGIT_SCALE_EXP,
                            token_counts=counts.cpu().numpy().copy(), selector_state=state.copy(),
-                           checkpoints=cks)
+                           warnings=warnings.cpu().numpy().copy(), checkpoints=cks)
 
     def infer(self, image, params):
         """HeatViTModel.infer (model.py:73): one image, all checkpoints."""
@@ -140,4 +148,4 @@ class HeatViTModel:
             prev = int(counts[s + 1])
         return ModelResult(logits=tuple(int(v) for v in res.logits[0]),
                            output_scale_exp=LOGIT_SCALE_EXP, checkpoints=res.checkpoints[0],
-                           selector_summary=tuple(summary))
+                           selector_summary=tuple(summary), warnings=int(res.warnings[0]))

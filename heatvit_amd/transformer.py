@@ -63,9 +63,11 @@ CHECKPOINT_KEYS = ("ln1", "fused_qkv", "qkv", "score", "prob", "context", "conca
                    "ln2", "hidden", "ffn_out", "z")
 
 
-def transformer_block_batch(xs, params, checkpoints=False):
+def transformer_block_batch(xs, params, checkpoints=False, warnings=False):
     """Runs one block over a ragged batch (each x is [N_i][192], N_i <= 197).
-    Returns the list of z arrays, plus per-image checkpoint dicts when asked."""
+    Returns the list of z arrays, plus per-image checkpoint dicts when asked,
+    plus (warnings=True) the per-image warning bits [B] int32
+    (WARN_LN_NEGATIVE_VARIANCE when LN1 or LN2 clamped a row's variance)."""
     if isinstance(params, DeviceBlock):
         dev = params
     elif isinstance(params, BlockParams):
@@ -82,6 +84,8 @@ def transformer_block_batch(xs, params, checkpoints=False):
     x = torch.from_numpy(np.concatenate(xs)).cuda()
     off = torch.from_numpy(offsets).cuda()
     z = torch.empty((t, 192), dtype=torch.int8, device="cuda")
+    status = torch.empty(b, dtype=torch.int32, device="cuda")
+    warn = torch.empty(b, dtype=torch.int32, device="cuda")
     L = _lib.lib()
     ws = torch.empty(L.hv_block_workspace_bytes(b, t), dtype=torch.uint8, device="cuda")
     ck = None
@@ -96,11 +100,17 @@ def transformer_block_batch(xs, params, checkpoints=False):
             "ln1", "fused_qkv", "concat", "msa", "y", "ln2", "hidden", "ffn_out", "score",
             "prob")])
     _lib.check(L.hv_block_forward(dev.struct, x.data_ptr(), off.data_ptr(), b, t, z.data_ptr(),
-                                  ck, ws.data_ptr(), ws.numel(), _stream()), "transformer_block")
+                                  ck, status.data_ptr(), warn.data_ptr(), ws.data_ptr(),
+                                  ws.numel(), _stream()), "transformer_block")
+    if status.any():
+        e = ValueError("transformer_block: token count outside [1, 197]")
+        e.error_class = _lib.HV_ERR_TOKEN_COUNT
+        raise e
     zs = z.cpu().numpy()
     outs = [zs[offsets[i]:offsets[i + 1]] for i in range(b)]
+    tail = (warn.cpu().numpy(),) if warnings else ()
     if not checkpoints:
-        return outs
+        return (outs, *tail) if tail else outs
     host = {k: v.cpu().numpy() for k, v in bufs.items()}
     per_image = []
     for i in range(b):
@@ -113,7 +123,7 @@ def transformer_block_batch(xs, params, checkpoints=False):
         d["context"] = d["concat"].reshape(n, 3, 64).transpose(1, 0, 2)
         d["z"] = outs[i]
         per_image.append(d)
-    return outs, per_image
+    return (outs, per_image, *tail)
 
 
 def transformer_block(x, params):

@@ -42,6 +42,24 @@ extern "C" {
 #define HV_EOVERFLOW (-3) /* accumulator outside int32 (OverflowError)    */
 #define HV_EHIP (-4)      /* HIP runtime error                           */
 
+/* Error codes of the reference engine (heatvit_pkg.sv:109-118; meanings
+ * docs/heatvit.md:751-763), recorded by every failing call and, for
+ * token counts found on the device, per image (hv_block_forward status;
+ * hv_selector_forward state token_count -1). */
+#define HV_ERR_NONE 0
+#define HV_ERR_OPCODE 1           /* unknown primitive, epilogue or A mode      */
+#define HV_ERR_DIMENSION 2        /* shape, batch, count or scale exponent      */
+#define HV_ERR_ADDRESS 3          /* null or misaligned pointer, short workspace */
+#define HV_ERR_TOKEN_COUNT 4      /* per-image token count outside its range     */
+#define HV_ERR_MEMORY_PROTOCOL 5  /* HIP runtime failure on a launch or copy     */
+#define HV_ERR_SOFTMAX_ZERO_SUM 6 /* never raised: a row maximum adds exp(0) = 2^16 */
+#define HV_ERR_BUSY_START 7       /* never raised: calls queue on their stream   */
+
+/* Warning bits of the reference engine (heatvit_pkg.sv:120-122). */
+#define HV_WARN_HEAD_DEN_ZERO 1        /* fuse: zero head-weight sum, equal weights */
+#define HV_WARN_PACKAGE_DEN_ZERO 2     /* finalize: zero package weight, plain mean */
+#define HV_WARN_LN_NEGATIVE_VARIANCE 4 /* LayerNorm variance clamped to zero        */
+
 #define HV_MAX_TOKENS 197 /* rows per image; attention tiles assume <= 208 */
 
 /* hipStream_t without pulling in the HIP headers. */
@@ -49,6 +67,9 @@ typedef void *hv_stream_t;
 
 /* Last error message of the calling thread ("" when none). */
 const char *hv_last_error(void);
+/* HV_ERR_* code of the calling thread's last failure (HV_ERR_NONE after a
+ * successful call). */
+int hv_last_error_class(void);
 /* ABI version, bumped on any incompatible change. */
 int hv_abi_version(void);
 
@@ -172,10 +193,16 @@ typedef struct {
   uint8_t *prob;  /* [B][3][197][197] */
 } hv_block_ckpt;
 
+/* status (optional, [B]): HV_ERR_TOKEN_COUNT for an image whose row count
+ * is outside [1, 197] or whose rows leave [0, max_rows) -- such an image
+ * is skipped by the attention and its z rows are unspecified -- else 0.
+ * warnings (optional, [B]): HV_WARN_LN_NEGATIVE_VARIANCE when a row of the
+ * image had a negative variance in LN1 or LN2, else 0. */
 size_t hv_block_workspace_bytes(int batch, int max_rows);
 int hv_block_forward(const hv_block_dev *p, const int8_t *x, const int32_t *offsets, int batch,
-                     int max_rows, int8_t *z, const hv_block_ckpt *ck, void *workspace,
-                     size_t workspace_bytes, hv_stream_t stream);
+                     int max_rows, int8_t *z, const hv_block_ckpt *ck, int32_t *status,
+                     int32_t *warnings, void *workspace, size_t workspace_bytes,
+                     hv_stream_t stream);
 
 /* ------------------------------------------------------------------ */
 /* selector.token_selector (selector.py:503-563) over a ragged batch.    */
@@ -183,7 +210,9 @@ int hv_block_forward(const hv_block_dev *p, const int8_t *x, const int32_t *offs
 /* pkg_in[b].  Outputs: out_tokens (compacted), out_offsets [B+1],       */
 /* pkg_out [B], fused [B][196] (Q0.16 per candidate), kept_index         */
 /* [B][196] (candidate index of each kept normal, -1 padded),            */
-/* state [B][5] = {token_count, package_present, kept, pruned, warnings}. */
+/* state [B][5] = {token_count, package_present, kept, pruned, warnings}; */
+/* token_count -1 marks an image the selector rejects (HV_ERR_TOKEN_COUNT: */
+/* fewer than two tokens, more than 197, or a package with no normal).    */
 /* ------------------------------------------------------------------ */
 
 /* Optional selector checkpoints (SelectorResult fields, selector.py:235-250);
@@ -225,6 +254,8 @@ int hv_patch_embedding(const hv_patch_dev *p, const int8_t *images, int batch, i
 /* images [B][224*224*3] NHWC int8; logits [B][1000] int32 at exp -14;   */
 /* token_counts [B][4]: rows entering block 1, and after each selector;  */
 /* state [3][B][5] per-selector state as in hv_selector_forward.         */
+/* warnings (optional, [B]): the engine's warning bits of each image's   */
+/* forward: HV_WARN_* of its three selectors and of its 25 LayerNorms.   */
 /* ckpt (optional): [B][17][197][192] int8 in the slot order patch,      */
 /* selector_01..03, block_01..12, final_ln, rows per slot in ckpt_rows   */
 /* [B][17].                                                              */
@@ -232,8 +263,9 @@ int hv_patch_embedding(const hv_patch_dev *p, const int8_t *images, int batch, i
 
 size_t hv_model_workspace_bytes(int batch);
 int hv_model_forward(const hv_model_dev *p, const int8_t *images, int batch, int32_t *logits,
-                     int32_t *token_counts, int32_t *state, int8_t *ckpt, int32_t *ckpt_rows,
-                     void *workspace, size_t workspace_bytes, hv_stream_t stream);
+                     int32_t *token_counts, int32_t *state, int32_t *warnings, int8_t *ckpt,
+                     int32_t *ckpt_rows, void *workspace, size_t workspace_bytes,
+                     hv_stream_t stream);
 
 /* ------------------------------------------------------------------ */
 /* Kernel-class timing with HIP events (for benchmarks).  While enabled, */

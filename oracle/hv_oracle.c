@@ -387,12 +387,18 @@ int hvo_patch_embedding(const int8_t *image, const hvo_patch *p, int8_t *out) {
   return rc;
 }
 
+/* LayerNorm over n rows; *warn (when given) gets HVO_WARN_LN_NEGATIVE_VARIANCE
+ * ORed in when any row's variance was negative (the engine's warning bit 2,
+ * heatvit_pkg.sv:122; the golden model returns the flag per row and its
+ * callers drop it, model.py:63, transformer.py:211, 338). */
 static int layernorm_rows(const int8_t *x, int n, const int8_t *g, const int8_t *b,
-                          int xe, int ge, int be, int oe, int8_t *out) {
+                          int xe, int ge, int be, int oe, int8_t *out, int32_t *warn) {
   for (int r = 0; r < n; r++) {
+    int neg = 0;
     int rc = hvo_layernorm(x + (size_t)r * HVO_D, g, b, xe, ge, be, oe,
-                           out + (size_t)r * HVO_D, NULL);
+                           out + (size_t)r * HVO_D, &neg);
     if (rc) return rc;
+    if (neg && warn) *warn |= HVO_WARN_LN_NEGATIVE_VARIANCE;
   }
   return HVO_OK;
 }
@@ -416,7 +422,7 @@ static int mhsa(const int8_t *x, int n, const hvo_block *p, int8_t *msa,
   int8_t *ctx = (int8_t *)malloc((size_t)n * 64);
 
   rc = layernorm_rows(x, n, p->ln1_gamma, p->ln1_beta, p->x_exp, p->gamma1_exp,
-                      p->beta1_exp, p->ln1_out_exp, ln1);
+                      p->beta1_exp, p->ln1_out_exp, ln1, ck ? ck->warnings : NULL);
   if (rc) goto done;
   rc = hvo_gemm(ln1, p->wqkv, p->bqkv, n, 576, HVO_D, 0, 0, acc);
   if (rc) goto done;
@@ -476,7 +482,7 @@ static int ffn(const int8_t *y, int n, const hvo_block *p, int8_t *z, hvo_block_
   int8_t *fo = (int8_t *)malloc((size_t)n * HVO_D);
   int64_t *acc = (int64_t *)malloc(sizeof(int64_t) * (size_t)n * HVO_FFN);
   rc = layernorm_rows(y, n, p->ln2_gamma, p->ln2_beta, p->ffn_x_exp, p->gamma2_exp,
-                      p->beta2_exp, p->ln2_out_exp, ln2);
+                      p->beta2_exp, p->ln2_out_exp, ln2, ck ? ck->warnings : NULL);
   if (rc) goto done;
   rc = hvo_gemm(ln2, p->w1, p->b1, n, HVO_FFN, HVO_D, 0, 0, acc);
   if (rc) goto done;
@@ -597,7 +603,7 @@ int hvo_finalize_tokens(const int8_t *cls, const int8_t *normal, int n_normal,
   int exists = n_part > 0;
   if (exists) {
     int8_t *pkg = out + (size_t)(1 + kept) * width;
-    if (den == 0) warnings |= 2;
+    if (den == 0) warnings |= HVO_WARN_PACKAGE_DEN_ZERO;
     for (int d = 0; d < width; d++) {
       int64_t num = 0;
       for (int i = 0; i < n_normal; i++)
@@ -716,7 +722,12 @@ int hvo_token_selector(const int8_t *tokens, int n, int package_present,
 
 /* model.HeatViTModel.infer (model.py:73-123). */
 int hvo_model_infer(const int8_t *image, const hvo_model *m, int32_t *logits,
-                    int8_t *ckpt, int32_t *ckpt_rows, hvo_selector_state *summary) {
+                    int8_t *ckpt, int32_t *ckpt_rows, hvo_selector_state *summary,
+                    int32_t *warnings) {
+  int32_t warn = 0;
+  hvo_block_ckpt bck;
+  memset(&bck, 0, sizeof bck);
+  bck.warnings = &warn;
   const size_t slot = (size_t)HVO_TOKENS * HVO_D;
   int8_t *x = (int8_t *)malloc(slot), *nx = (int8_t *)malloc(slot);
   int8_t *fln = (int8_t *)malloc(slot);
@@ -736,6 +747,7 @@ int hvo_model_infer(const int8_t *image, const hvo_model *m, int32_t *logits,
       rc = hvo_token_selector(x, n, pkg, &m->selectors[sel], nx, NULL, &st, NULL);
       if (rc) goto done;
       if (summary) summary[sel] = st;
+      warn |= st.warnings;
       n = st.token_count;
       pkg = st.package_present;
       memcpy(x, nx, (size_t)n * HVO_D);
@@ -743,14 +755,15 @@ int hvo_model_infer(const int8_t *image, const hvo_model *m, int32_t *logits,
       if (ckpt) memcpy(ckpt + (size_t)sel * slot, x, (size_t)n * HVO_D);
       if (ckpt_rows) ckpt_rows[sel] = n;
     }
-    rc = hvo_transformer_block(x, n, &m->blocks[b - 1], nx, NULL);
+    rc = hvo_transformer_block(x, n, &m->blocks[b - 1], nx, &bck);
     if (rc) goto done;
     memcpy(x, nx, (size_t)n * HVO_D);
     if (ckpt) memcpy(ckpt + (size_t)(3 + b) * slot, x, (size_t)n * HVO_D);
     if (ckpt_rows) ckpt_rows[3 + b] = n;
   }
   rc = layernorm_rows(x, n, m->final_gamma, m->final_beta, m->blocks[11].out_exp,
-                      m->final_gamma_exp, m->final_beta_exp, m->final_ln_out_exp, fln);
+                      m->final_gamma_exp, m->final_beta_exp, m->final_ln_out_exp, fln,
+                      &warn);
   if (rc) goto done;
   if (ckpt) memcpy(ckpt + (size_t)16 * slot, fln, (size_t)n * HVO_D);
   if (ckpt_rows) ckpt_rows[16] = n;
@@ -763,11 +776,13 @@ int hvo_model_infer(const int8_t *image, const hvo_model *m, int32_t *logits,
   }
 done:
   free(x); free(nx); free(fln);
+  if (warnings) *warnings = warn;
   return rc;
 }
 
 int hvo_model_infer_batch(const int8_t *images, int count, const hvo_model *m, int threads,
-                          int32_t *logits, int32_t *token_counts, int32_t *status) {
+                          int32_t *logits, int32_t *token_counts, int32_t *status,
+                          int32_t *warnings) {
   const size_t img = (size_t)m->patch.width * m->patch.height * 3;
   int worst = HVO_OK;
 #ifdef _OPENMP
@@ -777,7 +792,7 @@ int hvo_model_infer_batch(const int8_t *images, int count, const hvo_model *m, i
   for (int i = 0; i < count; i++) {
     int32_t rows[HVO_CKPT_SLOTS];
     int rc = hvo_model_infer(images + (size_t)i * img, m, logits + (size_t)i * HVO_CLASSES,
-                             NULL, rows, NULL);
+                             NULL, rows, NULL, warnings ? warnings + i : NULL);
     if (status) status[i] = rc;
     if (token_counts) {
       /* rows entering blocks 1, 4, 7, 10 */

@@ -26,6 +26,11 @@ extern "C" {
 #define HVO_EVALUE (-2)
 #define HVO_EOVERFLOW (-3)
 
+/* Warning bits of the reference engine (heatvit_pkg.sv:120-122). */
+#define HVO_WARN_HEAD_DEN_ZERO 1
+#define HVO_WARN_PACKAGE_DEN_ZERO 2
+#define HVO_WARN_LN_NEGATIVE_VARIANCE 4
+
 #define HVO_D 192
 #define HVO_HEADS 3
 #define HVO_HEAD_DIM 64
@@ -133,6 +138,7 @@ typedef struct {
   int8_t *ln2;       /* [N][192] */
   int8_t *hidden;    /* [N][768] */
   int8_t *ffn_out;   /* [N][192] */
+  int32_t *warnings; /* [1]: HVO_WARN_LN_NEGATIVE_VARIANCE ORed in by LN1/LN2 */
 } hvo_block_ckpt;
 
 /* Optional selector checkpoints (any pointer may be NULL); C = N - 1. */
@@ -167,16 +173,20 @@ int hvo_token_selector(const int8_t *tokens, int n, int package_present,
 /* Model checkpoint slots: 0 patch, 1..3 selector_01..03, 4..15 block_01..12,
  * 16 final_ln; each slot holds up to 197 rows of 192 bytes. */
 #define HVO_CKPT_SLOTS 17
+/* *warnings (optional): the engine's warning bits of the whole forward
+ * (heatvit_top.sv:5-6 OR-latch): the selectors' bits 0/1 and bit 2 when any
+ * LayerNorm row had a negative variance. */
 int hvo_model_infer(const int8_t *image, const hvo_model *m, int32_t *logits,
                     int8_t *ckpt /* [17][197][192] or NULL */,
                     int32_t *ckpt_rows /* [17] or NULL */,
-                    hvo_selector_state *summary /* [3] or NULL */);
+                    hvo_selector_state *summary /* [3] or NULL */,
+                    int32_t *warnings /* [1] or NULL */);
 /* Runs hvo_model_infer over `count` images (image stride 150528 B for the
  * default 224x224x3) with `threads` OpenMP threads; logits [count][1000],
  * token_counts [count][4] (input rows of the final LN per stage). */
 int hvo_model_infer_batch(const int8_t *images, int count, const hvo_model *m,
                           int threads, int32_t *logits, int32_t *token_counts,
-                          int32_t *status);
+                          int32_t *status, int32_t *warnings /* [count] or NULL */);
 
 #ifdef __cplusplus
 }

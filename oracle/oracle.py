@@ -20,6 +20,7 @@ HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "liboracle.so"
 
 OK, EVALUE, EOVERFLOW = 0, -2, -3
+WARN_HEAD_DEN_ZERO, WARN_PACKAGE_DEN_ZERO, WARN_LN_NEGATIVE_VARIANCE = 1, 2, 4
 
 _p8 = C.POINTER(C.c_int8)
 _pu8 = C.POINTER(C.c_uint8)
@@ -70,7 +71,7 @@ class Model(C.Structure):
 class BlockCkpt(C.Structure):
     _fields_ = [("ln1", _p8), ("fused_qkv", _p8), ("score", _p32), ("prob", _pu8),
                 ("context", _p8), ("concat", _p8), ("msa", _p8), ("y", _p8),
-                ("ln2", _p8), ("hidden", _p8), ("ffn_out", _p8)]
+                ("ln2", _p8), ("hidden", _p8), ("ffn_out", _p8), ("warnings", _p32)]
 
 
 class SelectorCkpt(C.Structure):
@@ -138,9 +139,9 @@ def lib():
                                          _p32, C.POINTER(SelectorState),
                                          C.POINTER(SelectorCkpt)]
         L.hvo_model_infer.argtypes = [_p8, C.POINTER(Model), _p32, _p8, _p32,
-                                      C.POINTER(SelectorState)]
+                                      C.POINTER(SelectorState), _p32]
         L.hvo_model_infer_batch.argtypes = [_p8, C.c_int, C.POINTER(Model), C.c_int,
-                                            _p32, _p32, _p32]
+                                            _p32, _p32, _p32, _p32]
         _LIB = L
     return _LIB
 
@@ -385,13 +386,16 @@ BLOCK_KEYS = ("ln1", "fused_qkv", "score", "prob", "context", "concat", "msa", "
 def transformer_block(x, bp, checkpoints=True):
     """Returns (z, checkpoints) with the reference's checkpoint keys
     (transformer.py:274-283, 378-383, 428-431); qkv is derived from
-    fused_qkv by layout.qkv_unpack semantics."""
+    fused_qkv by layout.qkv_unpack semantics.  checkpoints["warnings"] is
+    the engine's LayerNorm warning bit of the block (WARN_LN_NEGATIVE_VARIANCE
+    or 0)."""
     keep = _Keep()
     x = np.ascontiguousarray(x, np.int8).reshape(-1, 192)
     n = len(x)
     st = block_struct(bp, keep)
     z = np.zeros((n, 192), np.int8)
-    ck = None
+    warn = np.zeros(1, np.int32)
+    ck = BlockCkpt(warnings=_ptr(warn, _p32))
     bufs = {}
     if checkpoints:
         bufs = dict(ln1=np.zeros((n, 192), np.int8), fused_qkv=np.zeros((n, 576), np.int8),
@@ -402,12 +406,13 @@ def transformer_block(x, bp, checkpoints=True):
                     ffn_out=np.zeros((n, 192), np.int8))
         ck = BlockCkpt(*[
             _ptr(bufs[k], {np.int8: _p8, np.int32: _p32, np.uint8: _pu8}[bufs[k].dtype.type])
-            for k in BLOCK_KEYS])
+            for k in BLOCK_KEYS], _ptr(warn, _p32))
     _check(lib().hvo_transformer_block(_ptr(x, _p8), n, C.byref(st), _ptr(z, _p8),
-                                       C.byref(ck) if ck is not None else None), "block")
+                                       C.byref(ck)), "block")
     if checkpoints:
         bufs["qkv"] = bufs["fused_qkv"].reshape(n, 3, 3, 64).transpose(1, 2, 0, 3).copy()
         bufs["z"] = z
+    bufs["warnings"] = int(warn[0])
     return z, bufs
 
 
@@ -477,7 +482,8 @@ CKPT_NAMES = (["patch"] + [f"selector_{i:02d}" for i in range(1, 4)] +
 
 
 def model_infer(image, params, checkpoints=True):
-    """Returns (logits[1000] int32, checkpoints dict, selector summary list)."""
+    """Returns (logits[1000] int32, checkpoints dict, selector summary list,
+    warning bits of the forward)."""
     keep = _Keep()
     st = model_struct(params, keep)
     img = np.ascontiguousarray(image, np.int8).reshape(-1)
@@ -485,8 +491,10 @@ def model_infer(image, params, checkpoints=True):
     ck = np.zeros((17, 197, 192), np.int8) if checkpoints else None
     rows = np.zeros(17, np.int32)
     summ = (SelectorState * 3)()
+    warn = np.zeros(1, np.int32)
     _check(lib().hvo_model_infer(_ptr(img, _p8), C.byref(st), _ptr(logits, _p32),
-                                 _ptr(ck, _p8), _ptr(rows, _p32), summ), "infer")
+                                 _ptr(ck, _p8), _ptr(rows, _p32), summ, _ptr(warn, _p32)),
+           "infer")
     cks = {}
     if checkpoints:
         for i, name in enumerate(CKPT_NAMES):
@@ -496,12 +504,12 @@ def model_infer(image, params, checkpoints=True):
     summary = [dict(token_count=s.token_count, package_present=s.package_present,
                     kept_normal=s.kept_normal_count, pruned_normal=s.pruned_normal_count,
                     warnings=s.warnings) for s in list(summ)[:len(params.selectors)]]
-    return logits, cks, summary
+    return logits, cks, summary, int(warn[0])
 
 
 def model_infer_batch(images, params, threads=None):
     """Oracle over a batch with OpenMP; returns (logits [B][1000],
-    token_counts [B][4], status [B])."""
+    token_counts [B][4], status [B], warnings [B])."""
     keep = _Keep()
     st = model_struct(params, keep)
     imgs = np.ascontiguousarray(images, np.int8)
@@ -509,7 +517,9 @@ def model_infer_batch(images, params, threads=None):
     logits = np.zeros((b, 1000), np.int32)
     counts = np.zeros((b, 4), np.int32)
     status = np.zeros(b, np.int32)
+    warnings = np.zeros(b, np.int32)
     threads = threads or os.cpu_count() or 1
     lib().hvo_model_infer_batch(_ptr(imgs, _p8), b, C.byref(st), threads,
-                                _ptr(logits, _p32), _ptr(counts, _p32), _ptr(status, _p32))
-    return logits, counts, status
+                                _ptr(logits, _p32), _ptr(counts, _p32), _ptr(status, _p32),
+                                _ptr(warnings, _p32))
+    return logits, counts, status, warnings

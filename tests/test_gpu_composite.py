@@ -144,9 +144,10 @@ def test_throughput_batch_vs_oracle_and_deterministic(oracle):
     r2 = m.infer_batch(imgs, params)
     assert np.array_equal(r1.logits, r2.logits) and np.array_equal(r1.token_counts,
                                                                    r2.token_counts)
-    logits, counts, status = oracle.model_infer_batch(imgs, params)
+    logits, counts, status, warnings = oracle.model_infer_batch(imgs, params)
     assert not status.any()
     assert np.array_equal(r1.logits, logits)
+    assert np.array_equal(r1.warnings, warnings)
     assert np.array_equal(r1.token_counts, counts)
     # batch invariance: a sub-batch reproduces the same rows
     r3 = m.infer_batch(imgs[100:103], params)
@@ -158,7 +159,8 @@ def test_unpruned_control_vs_oracle(oracle):
     imgs, params = synth.throughput_workload(64)
     ctrl = synth.unpruned_control(params)
     r = HeatViTModel().infer_batch(imgs, ctrl)
-    logits, counts, status = oracle.model_infer_batch(imgs, ctrl)
+    logits, counts, status, warnings = oracle.model_infer_batch(imgs, ctrl)
     assert not status.any()
+    assert np.array_equal(r.warnings, warnings)
     assert np.array_equal(r.logits, logits)
     assert (r.token_counts == 197).all()

@@ -93,7 +93,8 @@ def _check_model(oracle, which, images, params, count=None):
     count = len(images) if count is None else count
     for i in range(count):
         assert gio.digest(images[i], np.int8) == meta["input_sha256"][i]
-        logits, cks, summary = oracle.model_infer(images[i], params)
+        logits, cks, summary, warnings = oracle.model_infer(images[i], params)
+        assert warnings == 0
         assert np.array_equal(logits, arrays["logits"][i]), i
         got = gio.model_checkpoint_digests(cks)
         assert got == meta["checkpoints"][i], (i, [k for k in got if got[k] != meta["checkpoints"][i].get(k)])
@@ -120,7 +121,8 @@ def test_pruned_model_matches_golden(oracle):
 def test_pruned_batch_logits_and_counts(oracle):
     meta, arrays = gio.load("pruned")
     imgs, params = synth.pruned_workload()
-    logits, counts, status = oracle.model_infer_batch(imgs, params)
+    logits, counts, status, warnings = oracle.model_infer_batch(imgs, params)
+    assert not warnings.any()
     assert not status.any()
     assert np.array_equal(logits, arrays["logits"])
     want = [[r["block_01"], r["block_04"], r["block_07"], r["block_10"]] for r in meta["rows"]]
