@@ -95,6 +95,8 @@ def main():
     ap.add_argument("--cpu-passes", type=int, default=2,
                     help="passes of the CPU oracle over the whole batch (0 skips it)")
     ap.add_argument("--no-control", action="store_true", help="skip the unpruned control")
+    ap.add_argument("--no-float", action="store_true",
+                    help="skip the float-image front-end measurement")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run three 64 MiB device-to-device copies (the reference "
                          "kernel for scaling HBM counters in a profiler run)")
@@ -196,6 +198,40 @@ def main():
                    "ms_per_step": round(c_wall, 4)}
         del ctrl
 
+    float_fe = None
+    if not args.no_float:
+        # The same images as preprocessed float CHW (q * 2^image_exp), which the
+        # front end quantises back to exactly q on its way into the patch rows.
+        exp = params.patch.image_scale_exp
+        fdev = dev.view(args.batch, 224, 224, 3).permute(0, 3, 1, 2).float().mul_(2.0 ** exp) \
+            .contiguous()
+        ref_logits = eng.logits[:args.batch].clone()
+
+        def timed_float(steps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                eng.forward(fdev)
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) * 1e3 / steps
+
+        for _ in range(args.warmup):
+            eng.forward(fdev)
+        f_wall = timed_float(args.steps)
+        same = bool(torch.equal(eng.logits[:args.batch], ref_logits))
+        L.hv_profile_enable(1)
+        eng.forward(fdev)
+        _lib.check(L.hv_profile_read(ms.ctypes.data, launches.ctypes.data, len(ms)), "profile")
+        L.hv_profile_enable(0)
+        fe_ms = float(ms[_lib.PROF_CLASSES.index("patch")])
+        fe_bytes = args.batch * (224 * 224 * 3 * 5) + hbm["patch"]
+        float_fe = {"workload": f"the same {args.batch} images as float32 CHW, quantised on the "
+                                "device into the patch rows", "value": round(args.batch / (f_wall / 1e3), 1),
+                    "ms_per_step": round(f_wall, 4), "logits_equal_int8_path": same,
+                    "front_end_ms": round(fe_ms, 4),
+                    "front_end_gbs": round(fe_bytes / (fe_ms * 1e-3) / 1e9, 1)}
+        del fdev
+
     cpu = None
     if args.cpu_passes > 0:
         threads = min(16, os.cpu_count() or 1)
@@ -224,6 +260,7 @@ def main():
                        "ms_per_step": round(gemm_ms, 4)},
         "kernels": per_class,
         "control": control,
+        "float_images": float_fe,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

@@ -126,6 +126,8 @@ def _declare(L):
     L.hv_model_workspace_bytes.argtypes = [C.c_int]
     L.hv_model_forward.argtypes = [C.POINTER(ModelDev), _vp, C.c_int, _vp, _vp, _vp, _vp, _vp,
                                    _vp, _vp, C.c_size_t, _vp]
+    L.hv_model_forward_f32.argtypes = L.hv_model_forward.argtypes
+    L.hv_quantize_images.argtypes = [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]
     L.hv_profile_enable.argtypes = [C.c_int]
     L.hv_profile_read.argtypes = [_vp, _vp, C.c_int]
 
@@ -151,4 +153,5 @@ def exported_symbols():
             "hv_layernorm_i8", "hv_gemm_i8", "hv_block_workspace_bytes", "hv_block_forward",
             "hv_selector_workspace_bytes", "hv_selector_forward", "hv_selector_finalize",
             "hv_patch_embedding", "hv_profile_enable", "hv_profile_read",
-            "hv_model_workspace_bytes", "hv_model_forward")
+            "hv_model_workspace_bytes", "hv_model_forward", "hv_model_forward_f32",
+            "hv_quantize_images")

@@ -444,12 +444,13 @@ size_t hv_model_workspace_bytes(int batch) {
   return cv.used + 256;
 }
 
-int hv_model_forward(const hv_model_dev *p, const int8_t *images, int batch, int32_t *logits,
-                     int32_t *token_counts, int32_t *state, int32_t *warnings, int8_t *ckpt,
-                     int32_t *ckpt_rows, void *workspace, size_t workspace_bytes,
-                     hv_stream_t stream) {
-  clear_error();
-  hipStream_t s = (hipStream_t)stream;
+// HeatViTModel.infer over a batch; images are int8 NHWC or, with
+// float_images, float CHW quantised at the patch's image exponent on the way
+// into the patch matrix.
+static int model_forward(const hv_model_dev *p, const void *images, bool float_images, int batch,
+                         int32_t *logits, int32_t *token_counts, int32_t *state,
+                         int32_t *warnings, int8_t *ckpt, int32_t *ckpt_rows, void *workspace,
+                         size_t workspace_bytes, hipStream_t s) {
   if (!p || !images || !logits) return fail(HV_EVALUE, HV_ERR_ADDRESS, "model: null argument");
   if (batch <= 0) return fail(HV_EVALUE, HV_ERR_DIMENSION, "model: empty batch");
   if ((long long)batch * HV_MAX_TOKENS * 768 > 0x7fffffffLL)
@@ -477,7 +478,14 @@ int hv_model_forward(const hv_model_dev *p, const int8_t *images, int batch, int
   if (rc) return rc;
   {
     ProfScope ps(HV_PROF_PATCH, s);
-    rc = launch_patch_embed(p->patch, images, batch, w.xa, s);
+    if (float_images) {
+      // the FFN hidden buffer ([B*197][768]) is free until block 1's FFN
+      rc = launch_image_front(static_cast<const float *>(images), batch, p->patch.image_exp,
+                              w.blk.hidden, true, s);
+      if (rc == HV_OK) rc = launch_patch_embed(p->patch, w.blk.hidden, batch, w.xa, s, true);
+    } else {
+      rc = launch_patch_embed(p->patch, static_cast<const int8_t *>(images), batch, w.xa, s);
+    }
   }
   if (rc) return rc;
   if (ckpt && (rc = launch_copy_ckpt(w.xa, w.off_a, batch, ckpt, ckpt_rows, 0, s))) return rc;
@@ -525,6 +533,34 @@ int hv_model_forward(const hv_model_dev *p, const int8_t *images, int batch, int
   g.shift_a = -14 - (p->final_ln_out_exp + p->head_w_exp);
   ProfScope ps(HV_PROF_HEAD, s);
   return launch_gemm(g, A_GATHER, HV_EPI_I32, s);
+}
+
+int hv_model_forward(const hv_model_dev *p, const int8_t *images, int batch, int32_t *logits,
+                     int32_t *token_counts, int32_t *state, int32_t *warnings, int8_t *ckpt,
+                     int32_t *ckpt_rows, void *workspace, size_t workspace_bytes,
+                     hv_stream_t stream) {
+  clear_error();
+  return model_forward(p, images, false, batch, logits, token_counts, state, warnings, ckpt,
+                       ckpt_rows, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int hv_model_forward_f32(const hv_model_dev *p, const float *images, int batch, int32_t *logits,
+                         int32_t *token_counts, int32_t *state, int32_t *warnings, int8_t *ckpt,
+                         int32_t *ckpt_rows, void *workspace, size_t workspace_bytes,
+                         hv_stream_t stream) {
+  clear_error();
+  return model_forward(p, images, true, batch, logits, token_counts, state, warnings, ckpt,
+                       ckpt_rows, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int hv_quantize_images(const float *images, int batch, int input_exp, int layout, int8_t *out,
+                       hv_stream_t stream) {
+  clear_error();
+  if (!images || !out) return fail(HV_EVALUE, HV_ERR_ADDRESS, "images: null argument");
+  if (layout != HV_IMAGE_NHWC && layout != HV_IMAGE_PATCHES)
+    return fail(HV_EVALUE, HV_ERR_OPCODE, "images: unknown layout %d", layout);
+  return launch_image_front(images, batch, input_exp, out, layout == HV_IMAGE_PATCHES,
+                            (hipStream_t)stream);
 }
 
 int hv_profile_enable(int on) {

@@ -593,8 +593,10 @@ static int run_lds(const GemmArgs &g, hipStream_t s) {
 template <int EPI>
 static int dispatch(const GemmArgs &g, int a_mode, hipStream_t s) {
   if constexpr (EPI == EPI_PATCH) {
-    if (a_mode != A_PATCH || g.k != 768)
+    // A from the NHWC images (gathered patches) or from patch rows [B*196][768]
+    if (g.k != 768 || (a_mode != A_PATCH && (a_mode != A_ROWS || g.lda != 768)))
       return fail(HV_EVALUE, HV_ERR_DIMENSION, "gemm: bad patch GEMM");
+    if (a_mode == A_ROWS) return run_lds<2, 1, 2, EPI_PATCH, A_ROWS, 24>(g, s);
     return run_lds<2, 1, 2, EPI_PATCH, A_PATCH, 24>(g, s);
   } else {
     if (a_mode == A_GATHER) return run<1, 1, 2, EPI, A_GATHER, 0>(g, s);
@@ -650,7 +652,7 @@ __global__ void k_cls_rows(const int8_t *cls, const int8_t *pos, int8_t *x, int 
 }
 
 int launch_patch_embed(const hv_patch_dev &p, const int8_t *images, int batch, int8_t *x,
-                       hipStream_t s) {
+                       hipStream_t s, bool patch_rows) {
   if (batch <= 0) return HV_OK;
   GemmArgs g{};
   g.a = images;
@@ -666,8 +668,8 @@ int launch_patch_embed(const hv_patch_dev &p, const int8_t *images, int batch, i
   g.mid_exp = p.activation_exp;
   g.res_exp = p.pos_exp;
   g.out_exp = p.tokens_exp;
-  g.lda = 0;
-  int rc = launch_gemm(g, A_PATCH, EPI_PATCH, s);
+  g.lda = patch_rows ? 768 : 0;
+  int rc = launch_gemm(g, patch_rows ? A_ROWS : A_PATCH, EPI_PATCH, s);
   if (rc) return rc;
   hv_launch(k_cls_rows, dim3(batch), dim3(192), 0, s, p.cls, p.pos, x, p.cls_exp,
                      p.pos_exp, p.tokens_exp);

@@ -56,9 +56,15 @@ int launch_gemm(const GemmArgs &g, int a_mode, int epilogue, hipStream_t s);
 void epilogue_limits_pub(GemmArgs &g, int epilogue);
 
 // Patch embedding (transformer.patch_embedding): A rows are gathered
-// patches of NHWC 224x224x3 images, epilogue adds the position rows, and the
-// CLS rows are written by a second small kernel.
+// patches of NHWC 224x224x3 images (or, with patch_rows, the patch matrix
+// [B*196][768] itself), epilogue adds the position rows, and the CLS rows
+// are written by a second small kernel.
 int launch_patch_embed(const hv_patch_dev &p, const int8_t *images, int batch, int8_t *x,
+                       hipStream_t s, bool patch_rows = false);
+
+// Image front end: float CHW [B][3][224][224] -> int8 at input_exp, as flat
+// NHWC images or (patch_rows) as the patch matrix [B*196][768].
+int launch_image_front(const float *chw, int batch, int input_exp, int8_t *out, bool patch_rows,
                        hipStream_t s);
 
 // Fills *ln for the int32 LayerNorm path (hv_device.h) when the exponents

@@ -17,6 +17,7 @@ import torch
 
 from . import _lib
 from .device import DeviceModel
+from .image import float_images
 from .params import HeatViTParams
 
 LOGIT_SCALE_EXP = -14
@@ -64,15 +65,23 @@ class Engine:
         self.warnings = torch.zeros(self.max_batch, dtype=torch.int32, device=dev)
 
     def forward(self, images, ckpt=None, ckpt_rows=None):
+        """images: int8 NHWC [B][150528], or float32 CHW [B][3][224][224]
+        quantised on the device at the patch's image_scale_exp."""
         b = images.shape[0]
         if b > self.max_batch:
             raise ValueError(f"batch {b} exceeds the engine's {self.max_batch}")
-        if images.dtype != torch.int8 or not images.is_contiguous() or \
+        if images.dtype == torch.float32:
+            if not images.is_contiguous() or tuple(images.shape[1:]) != (3, 224, 224):
+                raise ValueError("float images must be a contiguous tensor [B][3][224][224]")
+            entry = _lib.lib().hv_model_forward_f32
+        elif images.dtype != torch.int8 or not images.is_contiguous() or \
                 images.numel() != b * IMAGE_BYTES:
             raise ValueError("images must be a contiguous int8 device tensor [B][150528]")
+        else:
+            entry = _lib.lib().hv_model_forward
         state = self.state[:, :b] if b == self.max_batch else \
             torch.zeros((3, b, 5), dtype=torch.int32, device=images.device)
-        _lib.check(_lib.lib().hv_model_forward(
+        _lib.check(entry(
             self.model.struct, images.data_ptr(), b, self.logits.data_ptr(),
             self.token_counts.data_ptr(), state.data_ptr(), self.warnings.data_ptr(),
             None if ckpt is None else ckpt.data_ptr(),
@@ -107,10 +116,17 @@ class HeatViTModel:
         return self._cache[1]
 
     def infer_batch(self, images, params, checkpoints=False):
-        imgs = _images(images)
-        b = len(imgs)
+        return self._run(torch.from_numpy(_images(images)).cuda(), params, checkpoints)
+
+    def infer_float_batch(self, images, params, checkpoints=False):
+        """Forward from preprocessed float CHW images ([B][3][224][224]),
+        quantised on the device at params.patch.image_scale_exp
+        (p2_sim.forward_image's front end, tools/p2/p2_sim.py:536-543)."""
+        return self._run(float_images(images), params, checkpoints)
+
+    def _run(self, dev, params, checkpoints):
+        b = dev.shape[0]
         eng = self._engine(params, b)
-        dev = torch.from_numpy(imgs).cuda()
         ck = ck_rows = None
         if checkpoints:
             ck = torch.zeros((b, 17, 197, 192), dtype=torch.int8, device="cuda")
@@ -119,7 +135,9 @@ class HeatViTModel:
         n_sel = len(params.selectors)
         state = state.cpu().numpy()[:n_sel]
         if (state[:, :, 0] < 0).any():
-            raise ValueError("selector input invalid for some image (too few tokens)")
+            e = ValueError("selector input invalid for some image (too few tokens)")
+            e.error_class = _lib.HV_ERR_TOKEN_COUNT
+            raise e
         cks = None
         if checkpoints:
             ck, ck_rows = ck.cpu().numpy(), ck_rows.cpu().numpy()

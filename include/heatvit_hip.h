@@ -268,6 +268,28 @@ int hv_model_forward(const hv_model_dev *p, const int8_t *images, int batch, int
                      hv_stream_t stream);
 
 /* ------------------------------------------------------------------ */
+/* Image front end: preprocessed float images, CHW [B][3][224][224]     */
+/* (16-byte aligned), quantised to int8 q = clamp(round_half_even(x /   */
+/* 2^input_exp), -128, 127) as in p2_export_weights.real_image_list     */
+/* (tools/p2/p2_export_weights.py:246-251) and p2_sim.forward_image     */
+/* (tools/p2/p2_sim.py:536-543); NaN gives 0.                           */
+/* ------------------------------------------------------------------ */
+
+#define HV_IMAGE_NHWC 0    /* out [B][224*224*3]: the golden model's image      */
+#define HV_IMAGE_PATCHES 1 /* out [B*196][768]: layout.patchify rows (layout.py:31-72) */
+
+int hv_quantize_images(const float *images, int batch, int input_exp, int layout, int8_t *out,
+                       hv_stream_t stream);
+
+/* hv_model_forward from float CHW images, quantised at the patch's
+ * image_exp straight into the patch matrix (no NHWC copy); same outputs
+ * and workspace. */
+int hv_model_forward_f32(const hv_model_dev *p, const float *images, int batch, int32_t *logits,
+                         int32_t *token_counts, int32_t *state, int32_t *warnings, int8_t *ckpt,
+                         int32_t *ckpt_rows, void *workspace, size_t workspace_bytes,
+                         hv_stream_t stream);
+
+/* ------------------------------------------------------------------ */
 /* Kernel-class timing with HIP events (for benchmarks).  While enabled, */
 /* every kernel the forwards launch carries a start/stop event pair      */
 /* recorded by its own dispatch; hv_profile_read() waits for them and    */

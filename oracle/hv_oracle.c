@@ -16,6 +16,7 @@
  */
 #include "hv_oracle.h"
 
+#include <math.h>
 #include <stdlib.h>
 #include <string.h>
 #ifdef _OPENMP
@@ -350,15 +351,11 @@ static int8_t align_add(int64_t main, int main_exp, int64_t aux, int aux_exp,
   return (int8_t)requant128(s, common, out_exp, 8);
 }
 
-/* transformer.patch_embedding (transformer.py:104-145) with
- * layout.patchify (layout.py:31-72): raster patch order, within-patch
- * flatten (in_row, in_col, channel). */
-int hvo_patch_embedding(const int8_t *image, const hvo_patch *p, int8_t *out) {
-  int W = p->width, H = p->height, P = p->patch;
-  if (W <= 0 || P <= 0 || W % P || H % P) return HVO_EVALUE;
-  int pc_n = W / P, pr_n = H / P, np = pc_n * pr_n, kdim = P * P * 3;
-  if (np + 1 != HVO_TOKENS) return HVO_EVALUE;
-  int8_t *patches = (int8_t *)malloc((size_t)np * kdim);
+/* layout.patchify (layout.py:31-72): raster patch order, within-patch
+ * flatten (in_row, in_col, channel); patches [(H/P)*(W/P)][P*P*3]. */
+int hvo_patchify(const int8_t *image, int W, int H, int P, int8_t *patches) {
+  if (W <= 0 || P <= 0 || W % P || H <= 0 || H % P) return HVO_EVALUE;
+  int pc_n = W / P, pr_n = H / P, kdim = P * P * 3;
   for (int pr = 0; pr < pr_n; pr++)
     for (int pc = 0; pc < pc_n; pc++) {
       int8_t *v = patches + (size_t)(pr * pc_n + pc) * kdim;
@@ -368,6 +365,34 @@ int hvo_patch_embedding(const int8_t *image, const hvo_patch *p, int8_t *out) {
             v[(ir * P + ic) * 3 + ch] =
                 image[((size_t)(pr * P + ir) * W + pc * P + ic) * 3 + ch];
     }
+  return HVO_OK;
+}
+
+/* p2_export_weights.real_image_list (tools/p2/p2_export_weights.py:246-251):
+ * float CHW [3][H][W] -> int8 NHWC, q = clamp(round(x / 2^exp), -128, 127)
+ * with torch.round's ties-to-even (rintf in the default rounding mode) on
+ * the float32 quotient.  NaN (an undefined int8 cast there) gives 0. */
+int hvo_quantize_image(const float *chw, int W, int H, int input_exp, int8_t *nhwc) {
+  if (W <= 0 || H <= 0 || input_exp < -32 || input_exp > 31) return HVO_EVALUE;
+  const float step = ldexpf(1.0f, input_exp);
+  for (int y = 0; y < H; y++)
+    for (int x = 0; x < W; x++)
+      for (int ch = 0; ch < 3; ch++) {
+        float v = rintf(chw[((size_t)ch * H + y) * W + x] / step);
+        int q = v != v ? 0 : v < -128.f ? -128 : v > 127.f ? 127 : (int)v;
+        nhwc[((size_t)y * W + x) * 3 + ch] = (int8_t)q;
+      }
+  return HVO_OK;
+}
+
+/* transformer.patch_embedding (transformer.py:104-145) over hvo_patchify. */
+int hvo_patch_embedding(const int8_t *image, const hvo_patch *p, int8_t *out) {
+  int W = p->width, H = p->height, P = p->patch;
+  if (W <= 0 || P <= 0 || W % P || H % P) return HVO_EVALUE;
+  int pc_n = W / P, pr_n = H / P, np = pc_n * pr_n, kdim = P * P * 3;
+  if (np + 1 != HVO_TOKENS) return HVO_EVALUE;
+  int8_t *patches = (int8_t *)malloc((size_t)np * kdim);
+  hvo_patchify(image, W, H, P, patches);
   int64_t *acc = (int64_t *)malloc(sizeof(int64_t) * (size_t)np * HVO_D);
   int rc = hvo_gemm(patches, p->weight, p->bias, np, HVO_D, kdim, 0, 0, acc);
   if (rc == HVO_OK) {

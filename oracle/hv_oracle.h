@@ -156,6 +156,8 @@ typedef struct {
       warnings;
 } hvo_selector_state;
 
+int hvo_patchify(const int8_t *image, int width, int height, int patch, int8_t *patches);
+int hvo_quantize_image(const float *chw, int width, int height, int input_exp, int8_t *nhwc);
 int hvo_patch_embedding(const int8_t *image, const hvo_patch *p, int8_t *out);
 int hvo_transformer_block(const int8_t *x, int n, const hvo_block *p,
                           int8_t *z, hvo_block_ckpt *ck);

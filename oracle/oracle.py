@@ -138,6 +138,8 @@ def lib():
         L.hvo_token_selector.argtypes = [_p8, C.c_int, C.c_int, C.POINTER(Selector), _p8,
                                          _p32, C.POINTER(SelectorState),
                                          C.POINTER(SelectorCkpt)]
+        L.hvo_patchify.argtypes = [_p8, C.c_int, C.c_int, C.c_int, _p8]
+        L.hvo_quantize_image.argtypes = [C.POINTER(C.c_float), C.c_int, C.c_int, C.c_int, _p8]
         L.hvo_model_infer.argtypes = [_p8, C.POINTER(Model), _p32, _p8, _p32,
                                       C.POINTER(SelectorState), _p32]
         L.hvo_model_infer_batch.argtypes = [_p8, C.c_int, C.POINTER(Model), C.c_int,
@@ -369,6 +371,25 @@ def model_struct(params, keep):
 
 
 # ---------------------------------------------------------------- composites
+
+def quantize_image(chw, input_exp):
+    """p2_export_weights.real_image_list: float CHW [3][H][W] -> int8 NHWC
+    [H*W*3]."""
+    chw = np.ascontiguousarray(chw, np.float32)
+    _, h, w = chw.shape
+    out = np.zeros(h * w * 3, np.int8)
+    _check(lib().hvo_quantize_image(chw.ctypes.data_as(C.POINTER(C.c_float)), w, h, input_exp,
+                                    _ptr(out, _p8)), "quantize_image")
+    return out
+
+
+def patchify(image, width=224, height=224, patch=16):
+    """layout.patchify: flat NHWC int8 image -> [(H/P)*(W/P)][P*P*3]."""
+    img = np.ascontiguousarray(image, np.int8).reshape(-1)
+    out = np.zeros(((height // patch) * (width // patch), patch * patch * 3), np.int8)
+    _check(lib().hvo_patchify(_ptr(img, _p8), width, height, patch, _ptr(out, _p8)), "patchify")
+    return out
+
 
 def patch_embedding(image, pp):
     keep = _Keep()
