@@ -10,6 +10,7 @@ HeatViTModel.infer_batch and Engine run many images per launch sequence;
 pruned images keep ragged token counts on the device.
 """
 
+import dataclasses
 from dataclasses import dataclass
 
 import numpy as np
@@ -151,6 +152,17 @@ class HeatViTModel:
         return BatchResult(logits=logits.cpu().numpy().copy(), output_scale_exp=LOGIT_SCALE_EXP,
                            token_counts=counts.cpu().numpy().copy(), selector_state=state.copy(),
                            warnings=warnings.cpu().numpy().copy(), checkpoints=cks)
+
+    def forward_batch(self, images, params, prune=True):
+        """The reference's accuracy engine (p2_sim.forward_image per image,
+        tools/p2/p2_sim.py:527-;  p2_sim_ivit.forward_batch_cfg without
+        pruning, tools/p2/p2_sim_ivit.py:563-624) over a batch of float CHW
+        images: returns (logits [B][1000] int32, token_counts [B][4],
+        LOGIT_SCALE_EXP).  prune=False skips the selectors."""
+        if not prune:
+            params = dataclasses.replace(params, selectors=(), selector_blocks=())
+        r = self.infer_float_batch(images, params)
+        return r.logits, r.token_counts, LOGIT_SCALE_EXP
 
     def infer(self, image, params):
         """HeatViTModel.infer (model.py:73): one image, all checkpoints."""
