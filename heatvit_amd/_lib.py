@@ -70,6 +70,28 @@ class ModelDev(C.Structure):
                 ("final_ln_out_exp", _i32), ("head_w_exp", _i32)]
 
 
+SCHEDULE_BLOCK_TENSORS = ("gamma1", "beta1", "wqkv", "bqkv", "wproj", "bproj", "gamma2", "beta2",
+                          "w1", "b1", "w2", "b2")
+SCHEDULE_SELECTOR_TENSORS = ("local_w", "local_b", "score_w1", "score_b1", "score_w2", "score_b2",
+                             "score_w3", "score_b3", "hw_w1", "hw_b1", "hw_w2", "hw_b2")
+HV_DESC_WORD_BYTES = 40
+
+
+class ScheduleBlock(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in SCHEDULE_BLOCK_TENSORS]
+
+
+class ScheduleSelector(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in SCHEDULE_SELECTOR_TENSORS]
+
+
+class Schedule(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("patch_w", "patch_b", "cls", "pos")] + [
+        ("blocks", ScheduleBlock * 12), ("selectors", ScheduleSelector * 3)] + [
+        (n, C.c_uint32) for n in ("final_gamma", "final_beta", "head_w", "head_b")] + [
+        ("weight_bytes", C.c_uint64), ("model", ModelDev)]
+
+
 class SelectorCkpt(C.Structure):
     _fields_ = [(n, _vp) for n in ("local", "global_", "head_scores", "head_stats",
                                    "head_weights")]
@@ -128,6 +150,11 @@ def _declare(L):
                                    _vp, _vp, C.c_size_t, _vp]
     L.hv_model_forward_f32.argtypes = L.hv_model_forward.argtypes
     L.hv_quantize_images.argtypes = [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]
+    L.hv_schedule_compile.argtypes = [_vp, C.c_int, C.POINTER(Schedule)]
+    L.hv_schedule_packed_bytes.restype = C.c_size_t
+    L.hv_schedule_packed_bytes.argtypes = [C.POINTER(Schedule)]
+    L.hv_schedule_bind.argtypes = [C.POINTER(Schedule), _vp, C.c_size_t, _vp, C.c_size_t,
+                                   C.POINTER(ModelDev), _vp]
     L.hv_profile_enable.argtypes = [C.c_int]
     L.hv_profile_read.argtypes = [_vp, _vp, C.c_int]
 
@@ -154,4 +181,5 @@ def exported_symbols():
             "hv_selector_workspace_bytes", "hv_selector_forward", "hv_selector_finalize",
             "hv_patch_embedding", "hv_profile_enable", "hv_profile_read",
             "hv_model_workspace_bytes", "hv_model_forward", "hv_model_forward_f32",
-            "hv_quantize_images")
+            "hv_quantize_images", "hv_schedule_compile", "hv_schedule_packed_bytes",
+            "hv_schedule_bind")

@@ -28,7 +28,7 @@ int check_hip(hipError_t e, const char *what) {
   return fail(HV_EHIP, HV_ERR_MEMORY_PROTOCOL, "%s: %s", what, hipGetErrorString(e));
 }
 
-static void clear_error() {
+void clear_error() {
   g_err[0] = 0;
   g_err_class = HV_ERR_NONE;
 }

@@ -12,6 +12,7 @@ namespace hv {
 
 // Error reporting: a thread-local message and HV_ERR_* class (hv_capi.hip).
 int fail(int status, int cls, const char *fmt, ...);
+void clear_error();  // entry points start with a clean record
 int check_hip(hipError_t e, const char *what);
 
 // Kernel launch.  While kernel-class profiling is on and a class is active

@@ -54,7 +54,8 @@ class Engine:
     returns device views (logits, token_counts, selector state, warnings)."""
 
     def __init__(self, params, max_batch, device="cuda"):
-        self.model = params if isinstance(params, DeviceModel) else DeviceModel(params, device)
+        # a DeviceModel, a compiled-ROM model (heatvit_amd.schedule), or params
+        self.model = params if hasattr(params, "struct") else DeviceModel(params, device)
         self.max_batch = int(max_batch)
         L = _lib.lib()
         dev = self.model.device

@@ -183,6 +183,43 @@ typedef struct {
 } hv_model_dev;
 
 /* ------------------------------------------------------------------ */
+/* Descriptor front end.  The reference engine executes a ROM of 320-bit */
+/* descriptors (rtl/generated/heatvit_descriptors.mem; fields            */
+/* descriptor.py:131-161, sequence generate_descriptors.py:222-480) over */
+/* a four-region memory image.  hv_schedule_compile validates the ROM    */
+/* as the engine does (HV_ERR_OPCODE / _DIMENSION / _ADDRESS), checks     */
+/* that it is the HeatViT-T sequence (patch, 12 blocks, up to three       */
+/* selectors, final LayerNorm, classifier) with chained scale exponents,  */
+/* and returns every tensor's weight-region offset and the exponents;    */
+/* hv_schedule_bind repacks a device copy of the weight region into      */
+/* `packed` and fills an hv_model_dev for hv_model_forward.  Images are  */
+/* the input region (NHWC int8), logits the output region (int32).       */
+/* ------------------------------------------------------------------ */
+
+#define HV_DESC_WORD_BYTES 40 /* one descriptor, little-endian: bit i in byte i/8 */
+
+typedef struct {
+  uint32_t gamma1, beta1, wqkv, bqkv, wproj, bproj, gamma2, beta2, w1, b1, w2, b2;
+} hv_schedule_block;
+typedef struct {
+  uint32_t local_w, local_b, score_w1, score_b1, score_w2, score_b2, score_w3, score_b3, hw_w1,
+      hw_b1, hw_w2, hw_b2;
+} hv_schedule_selector;
+typedef struct {
+  uint32_t patch_w, patch_b, cls, pos; /* weight-region byte offsets */
+  hv_schedule_block blocks[12];
+  hv_schedule_selector selectors[3];
+  uint32_t final_gamma, final_beta, head_w, head_b;
+  uint64_t weight_bytes; /* end of the last tensor the schedule reads */
+  hv_model_dev model;    /* exponents, selector count and placement; NULL pointers */
+} hv_schedule;
+
+int hv_schedule_compile(const uint8_t *words, int n_desc, hv_schedule *out);
+size_t hv_schedule_packed_bytes(const hv_schedule *s);
+int hv_schedule_bind(const hv_schedule *s, const uint8_t *weights, size_t weight_bytes,
+                     void *packed, size_t packed_bytes, hv_model_dev *model, hv_stream_t stream);
+
+/* ------------------------------------------------------------------ */
 /* transformer.transformer_block (transformer.py:401-431) over a ragged  */
 /* batch: image b owns rows offsets[b] .. offsets[b+1] of x.             */
 /* ------------------------------------------------------------------ */
