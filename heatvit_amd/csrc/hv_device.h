@@ -256,6 +256,29 @@ __host__ __device__ __forceinline__ unsigned softmax_recip(u64 sum) {
   return (unsigned)(2 * r >= sum ? q + 1 : q);
 }
 
+// The same for 65554 <= sum < 2^24 (rows of at most 255 exponentials, each
+// <= exp(0) = 65554) in 32-bit lanes without branches: the float quotient
+// 2^32 * rcp(sum) is within 2^-7 of 2^32 / sum < 2^16, so its truncation q
+// is within one of the floor; the remainder r = 2^32 - q * sum then lies in
+// [-sum, 2 * sum), exact in wrapping 32-bit arithmetic (q, sum < 2^24 make
+// q * sum a 24-bit multiply), and one correction each way plus the rounding
+// test finish the division.
+template <typename R>
+__host__ __device__ __forceinline__ unsigned softmax_recip24_r(unsigned sum) {
+  unsigned q = (unsigned)(4294967296.0f * R::rcp((float)sum));
+  int r = (int)(0u - mul_u24(q, sum));
+  const int lo = r >> 31;  // r < 0: q was one too large
+  q += (unsigned)lo;
+  r += (int)(sum & (unsigned)lo);
+  const unsigned hi = r >= (int)sum ? 1u : 0u;  // q was one too small
+  q += hi;
+  r -= (int)(sum & (0u - hi));
+  return q + (2u * (unsigned)r >= sum ? 1u : 0u);
+}
+__device__ __forceinline__ unsigned softmax_recip24(unsigned sum) {
+  return softmax_recip24_r<RcpHw>(sum);
+}
+
 // ratio = rsa(e * recip, 16); with delta2 = 65536 the scaled value equals
 // the ratio (nonlinear.py:120-121).  e, recip < 2^17.
 __host__ __device__ __forceinline__ unsigned softmax_ratio(unsigned e, unsigned recip) {

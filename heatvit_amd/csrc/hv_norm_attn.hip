@@ -330,7 +330,7 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
     }
     sum += __shfl_xor(sum, 16);
     sum += __shfl_xor(sum, 32);
-    const unsigned recip = softmax_recip(sum);
+    const unsigned recip = softmax_recip24(sum);  // sum <= 197 * 65554 < 2^24
     v4i pk_hi[4], pk_lo[4];
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {

@@ -207,7 +207,7 @@ __global__ __launch_bounds__(256) void k_selector_head(hv_selector_dev p, const 
       }
       const int mx = qv[0] > qv[1] ? qv[0] : qv[1];
       const unsigned e0 = softmax_exp(qv[0] - mx), e1 = softmax_exp(qv[1] - mx);
-      const unsigned ratio = softmax_ratio(e1, softmax_recip((u64)e0 + e1));
+      const unsigned ratio = softmax_ratio(e1, softmax_recip24(e0 + e1));
       const int hsv = (int)(ratio > 65536u ? 65536u : ratio);
       hs_out[((size_t)b * 3 + h) * kMaxCand + c] = hsv;
       if (ck.head_scores) ck.head_scores[((size_t)b * 3 + h) * kMaxCand + c] = hsv;

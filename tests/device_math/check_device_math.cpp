@@ -6,7 +6,8 @@
 //            exact and perturbed by one ulp either way (the hardware rcp is
 //            only ulp-accurate), against hvo_gelu;
 //   softmax  the 32-bit exp / reciprocal / ratio path against
-//            hvo_softmax_attention and hvo_softmax_selector on random rows;
+//            hvo_softmax_attention and hvo_softmax_selector on random rows,
+//            and the branch-free 32-bit reciprocal over all its row sums;
 //   layernorm the int32 limb-split normalisation (ln_row_consts / ln_norm)
 //            against hvo_layernorm on random and degenerate rows over the
 //            exponent range the kernel takes it for.
@@ -36,6 +37,19 @@ static long check_gelu() {
     if (gelu_q16_r<RcpExact>(x) != ref || gelu_q16_r<RcpLo>(x) != ref || gelu_q16_r<RcpHi>(x) != ref) {
       if (++bad < 5) std::printf("gelu mismatch at x=%d (ref %d)\n", x, ref);
     }
+  }
+  return bad;
+}
+
+// softmax_recip24 against the 64-bit softmax_recip over every row sum it
+// takes (65554 .. 2^24 - 1), reciprocal estimate exact and +-1 ulp.
+static long check_recip24() {
+  long bad = 0;
+  for (unsigned s = 65554; s < (1u << 24); ++s) {
+    const unsigned ref = softmax_recip(s);
+    if (softmax_recip24_r<RcpExact>(s) != ref || softmax_recip24_r<RcpLo>(s) != ref ||
+        softmax_recip24_r<RcpHi>(s) != ref)
+      if (++bad < 5) std::printf("recip24 mismatch at sum=%u (ref %u)\n", s, ref);
   }
   return bad;
 }
@@ -119,7 +133,8 @@ static long check_layernorm(int rows) {
 
 int main(int argc, char **argv) {
   const int rows = argc > 1 ? std::atoi(argv[1]) : 100000;
-  const long g = check_gelu(), s = check_softmax(rows), l = check_layernorm(rows);
+  const long g = check_gelu(), s = check_softmax(rows) + check_recip24(),
+             l = check_layernorm(rows);
   std::printf("gelu_bad=%ld softmax_bad=%ld layernorm_bad=%ld\n", g, s, l);
   return (g || s || l) ? 1 : 0;
 }
