@@ -45,8 +45,11 @@ enum { EPI_I8 = HV_EPI_I8, EPI_I32 = HV_EPI_I32, EPI_GELU = HV_EPI_GELU,
 static constexpr int kPatchesPerImage = 196;
 static constexpr int kTokens = 197;
 static constexpr int kImageBytes = 224 * 224 * 3;
-static constexpr int kGridCap = 256 * 8;     // workgroups: 256 CUs x 8 resident
-static constexpr int kLdsGridCap = 256 * 2;  // LDS-staged kernel: 2 per CU
+// Direct kernel: one workgroup per tile (the grid is not capped), so the
+// hardware dispatcher balances the tiles over the resident slots; a capped
+// grid with static tile striding left a partial last round per workgroup.
+static constexpr int kGridCap = 1 << 20;
+static constexpr int kLdsGridCap = 256 * 2;  // LDS-staged kernel: 2 per CU, persistent
 
 template <int AMODE>
 __device__ __forceinline__ const int8_t *a_row(const GemmArgs &g, int r) {
