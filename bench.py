@@ -32,6 +32,7 @@ sys.path.insert(0, str(ROOT))
 
 MI355X_INT8_TOPS = 5000.0   # dense int8 MFMA, TOPS
 MI355X_HBM_GBS = 8000.0     # HBM3E, GB/s
+MI355X_VALU_GINST = 614.4   # 256 CUs x 1 wavefront VALU instruction / cycle x 2.4 GHz
 METRIC = "images/sec (batch 256, pruned HeatViT-T, 1 MI355X); % int8 MFMA peak; bit-exact"
 
 
@@ -186,6 +187,16 @@ def main():
     roofline["traffic"] = None
     if traffic_file.exists():
         roofline["traffic"] = json.loads(traffic_file.read_text()).get("bytes_per_launch")
+    # Instruction-issue bound of the dominant kernel: its wavefront VALU
+    # instructions per launch (rocprofv3 SQ_INSTS_VALU, same workload) over
+    # the launch time, against 256 CUs x 1 wavefront instruction per cycle.
+    valu_file = ROOT / "profiles" / f"valu_{dom}.json"
+    if valu_file.exists():
+        insts = json.loads(valu_file.read_text())["valu_insts_per_launch"]
+        rate = insts / (d["avg_launch_us"] * 1e-6) / 1e9
+        roofline["valu"] = {"insts_per_launch": insts, "achieved": round(rate, 1),
+                            "peak": MI355X_VALU_GINST, "unit": "G wavefront-instr/s",
+                            "frac": round(rate / MI355X_VALU_GINST, 4)}
 
     control = None
     if not args.no_control:

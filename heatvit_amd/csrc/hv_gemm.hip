@@ -145,11 +145,14 @@ __device__ __forceinline__ void epi_tile(const GemmArgs &g, const v16i (&acc)[MT
     const int c0 = (ct0 + nt) * 32 + 16 * h;
     bool narrow = FAST;
     if (FAST) {
+      // |b| <= acc_lim for the lane's 16 biases, from their range
+      int bmax = bias4[nt][0][0], bmin = bmax;
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int b = bias4[nt][j >> 2][j & 3];
-        narrow = narrow && b <= g.acc_lim && b >= -g.acc_lim;
+      for (int j = 1; j < 16; ++j) {
+        bmax = max(bmax, bias4[nt][j >> 2][j & 3]);
+        bmin = min(bmin, bias4[nt][j >> 2][j & 3]);
       }
+      narrow = bmax <= g.acc_lim && bmin >= -g.acc_lim;
     }
     // Uniform per wavefront: the int32 form only when every lane qualifies.
     const bool fast = FAST && __all(narrow);
