@@ -19,7 +19,7 @@ HV_WARN_HEAD_DEN_ZERO, HV_WARN_PACKAGE_DEN_ZERO, HV_WARN_LN_NEGATIVE_VARIANCE = 
 HV_PRIM_REQUANT, HV_PRIM_GELU, HV_PRIM_PLAN, HV_PRIM_RSA = 0, 1, 2, 3
 HV_EPI_I8, HV_EPI_I32, HV_EPI_GELU, HV_EPI_RESIDUAL = 0, 1, 2, 3
 HV_A_ROWS, HV_A_GATHER = 0, 1
-ABI_VERSION = 3
+ABI_VERSION = 4
 PROF_CLASSES = ("patch", "layernorm", "gemm_qkv", "attention", "gemm_proj", "gemm_ffn1",
                 "gemm_ffn2", "selector", "head", "other")
 
@@ -132,6 +132,8 @@ def _declare(L):
     L.hv_softmax_rows.argtypes = [_vp, _vp, C.c_int, _vp, _vp, _vp]
     L.hv_layernorm_i8.argtypes = [_vp, _vp, _vp, _vp, C.c_int, _vp, C.c_int, C.c_int, C.c_int,
                                   C.c_int, _vp, _vp]
+    L.hv_attention_i8.argtypes = [_vp, _vp, C.c_int, C.c_int, _vp, _vp, _vp, C.c_int, C.c_int,
+                                  C.c_int, C.c_int, _vp, _vp]
     L.hv_gemm_i8.argtypes = [C.POINTER(GemmDesc), _vp]
     L.hv_block_workspace_bytes.restype = C.c_size_t
     L.hv_block_workspace_bytes.argtypes = [C.c_int, C.c_int]
@@ -177,7 +179,7 @@ def exported_symbols():
     """Names declared in include/heatvit_hip.h (checked by the CPU tests)."""
     return ("hv_last_error", "hv_last_error_class", "hv_abi_version", "hv_eval_primitive",
             "hv_softmax_rows",
-            "hv_layernorm_i8", "hv_gemm_i8", "hv_block_workspace_bytes", "hv_block_forward",
+            "hv_layernorm_i8", "hv_attention_i8", "hv_gemm_i8", "hv_block_workspace_bytes", "hv_block_forward",
             "hv_selector_workspace_bytes", "hv_selector_forward", "hv_selector_finalize",
             "hv_patch_embedding", "hv_profile_enable", "hv_profile_read",
             "hv_model_workspace_bytes", "hv_model_forward", "hv_model_forward_f32",

@@ -271,7 +271,7 @@ const char *hv_last_error(void) { return g_err; }
 
 int hv_last_error_class(void) { return g_err_class; }
 
-int hv_abi_version(void) { return 3; }
+int hv_abi_version(void) { return 4; }
 
 int hv_eval_primitive(int op, const int64_t *in, int64_t *out, int64_t n, int a, int b, int c,
                       hv_stream_t stream) {
@@ -291,6 +291,32 @@ int hv_layernorm_i8(const int8_t *x, const int8_t *gamma, const int8_t *beta, in
   clear_error();
   return launch_layernorm(x, gamma, beta, y, rows, rows_dev, x_exp, gamma_exp, beta_exp,
                           out_exp, neg_var, LnWarn{}, (hipStream_t)stream);
+}
+
+int hv_attention_i8(const int8_t *qkv, const int32_t *offsets, int batch, int rows, int8_t *ctx,
+                    int32_t *score, uint8_t *prob, int qkv_exp, int score_exp, int prob_exp,
+                    int context_exp, int32_t *status, hv_stream_t stream) {
+  clear_error();
+  if (!qkv || !offsets || !ctx) return fail(HV_EVALUE, HV_ERR_ADDRESS, "attention: null argument");
+  if (batch <= 0 || rows <= 0)
+    return fail(HV_EVALUE, HV_ERR_DIMENSION, "attention: empty batch");
+  for (int v : {qkv_exp, score_exp, prob_exp, context_exp})
+    if (!exp_ok(v))
+      return fail(HV_EVALUE, HV_ERR_DIMENSION, "attention scale exponent %d outside [-32, 31]",
+                  v);
+  if (((uintptr_t)qkv & 15) || ((uintptr_t)ctx & 3))
+    return fail(HV_EVALUE, HV_ERR_ADDRESS,
+                "attention: qkv must be 16-byte and ctx 4-byte aligned");
+  const hipStream_t s = (hipStream_t)stream;
+  int rc = launch_image_check(offsets, batch, rows, status, nullptr, s);
+  if (rc) return rc;
+  AttnArgs a{};
+  a.qkv = qkv; a.offsets = offsets; a.ctx = ctx; a.batch = batch; a.rows_cap = rows;
+  a.score = score; a.prob = prob;
+  a.score_shift = score_exp - 2 * qkv_exp;
+  a.q16_shift = -(score_exp + 13);
+  a.ctx_shift = context_exp - (prob_exp + qkv_exp);
+  return launch_attention(a, s);
 }
 
 int hv_gemm_i8(const hv_gemm_desc *d, hv_stream_t stream) {

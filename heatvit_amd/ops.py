@@ -5,6 +5,7 @@ fixed.py / nonlinear.py / gemm.py functions on whole arrays.
   gelu, plan_sigmoid             nonlinear.py:60-95
   softmax_attention/_selector    nonlinear.py:109-133 (ragged batches of rows)
   layernorm_rows                 nonlinear.py:136-186
+  attention                      mhsa's attention core (transformer.py:228-266)
   gemm_writeback                 gemm.gemm_numpy + gemm_writeback (gemm.py:93-139)
 
 Inputs are array-likes on the host or torch tensors on the GPU; results
@@ -109,6 +110,40 @@ def layernorm_rows(x, gamma, beta, x_scale, gamma_scale, beta_scale, out_scale):
                                           beta_scale, out_scale, neg.data_ptr(), _stream()),
                "layernorm")
     return y.cpu().numpy(), neg.cpu().numpy().astype(bool)
+
+
+def attention(fused_qkv, qkv_exp, score_exp, prob_exp, context_exp):
+    """The attention core of transformer.mhsa (transformer.py:228-266) for
+    a batch of images: fused_qkv is one [N][576] int8 array per image (Q,
+    K, V column blocks, heads of 64).  Returns one (score [3][N][N] int32,
+    prob [3][N][N] uint8, concat [N][192] int8) per image, the `score`,
+    `prob` and `concat` checkpoints of mhsa."""
+    mats = [np.asarray(q) for q in fused_qkv]
+    if not mats:
+        return []
+    for q in mats:
+        if q.ndim != 2 or q.shape[1] != 576:
+            raise ValueError("fused_qkv rows must have 576 channels")
+        if not 1 <= len(q) <= 197:
+            raise ValueError(f"token count {len(q)} outside [1, 197]")
+    lens = [len(q) for q in mats]
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    qkv = _to_dev(np.concatenate(mats), torch.int8)
+    off = _to_dev(offsets, torch.int32)
+    b, rows = len(mats), int(offsets[-1])
+    ctx = torch.empty((rows, 192), dtype=torch.int8, device="cuda")
+    score = torch.zeros((b, 3, 197, 197), dtype=torch.int32, device="cuda")
+    prob = torch.zeros((b, 3, 197, 197), dtype=torch.uint8, device="cuda")
+    status = torch.zeros(b, dtype=torch.int32, device="cuda")
+    _lib.check(_lib.lib().hv_attention_i8(qkv.data_ptr(), off.data_ptr(), b, rows, ctx.data_ptr(),
+                                          score.data_ptr(), prob.data_ptr(), qkv_exp, score_exp,
+                                          prob_exp, context_exp, status.data_ptr(), _stream()),
+               "attention")
+    if status.any():
+        raise ValueError("attention: token count outside [1, 197]")
+    ctx, score, prob = ctx.cpu().numpy(), score.cpu().numpy(), prob.cpu().numpy()
+    return [(score[i, :, :n, :n], prob[i, :, :n, :n], ctx[offsets[i]:offsets[i + 1]])
+            for i, n in enumerate(lens)]
 
 
 def gemm_writeback(a, w, bias, src_exp, dst_exp, output_bits, *, epilogue=None, mid_exp=0,

@@ -105,6 +105,26 @@ int hv_layernorm_i8(const int8_t *x, const int8_t *gamma, const int8_t *beta, in
                     int beta_exp, int out_exp, uint8_t *neg_var, hv_stream_t stream);
 
 /* ------------------------------------------------------------------ */
+/* Attention core of mhsa (transformer.py:228-266)                      */
+/* ------------------------------------------------------------------ */
+
+/* Image b owns rows offsets[b] .. offsets[b+1] of qkv [rows][576] (the
+ * fused QKV projection: Q, K, V column blocks, heads of 64 lanes,
+ * layout.qkv_unpack, layout.py:92-129).  Per head h:
+ *   score = requant(Q_h K_h^T, 2*qkv_exp, score_exp, 32)
+ *   prob  = softmax_attention(sat24(rsa(score, -(score_exp + 13))))   UQ0.8
+ *   ctx   = requant(prob V_h, prob_exp + qkv_exp, context_exp, 8)
+ * with the heads concatenated lane-wise (layout.head_concat,
+ * layout.py:132-155) into ctx [rows][192].  score / prob, when non-NULL,
+ * receive the [B][3][197][197] checkpoints (row and column stride 197).
+ * status (optional, [B]) gets HV_ERR_TOKEN_COUNT for an image whose token
+ * count is outside [1, 197] or whose rows fall outside `rows`; such images
+ * are skipped.  qkv must be 16-byte aligned, ctx 4-byte aligned. */
+int hv_attention_i8(const int8_t *qkv, const int32_t *offsets, int batch, int rows, int8_t *ctx,
+                    int32_t *score, uint8_t *prob, int qkv_exp, int score_exp, int prob_exp,
+                    int context_exp, int32_t *status, hv_stream_t stream);
+
+/* ------------------------------------------------------------------ */
 /* int8 GEMM with fused epilogues (gemm.gemm_numpy + gemm_writeback,    */
 /* gemm.py:93-139; transformer.py:349-358 GELU; transformer.py:96-101   */
 /* residual align-add)                                                  */

@@ -269,6 +269,32 @@ def gemm_writeback(acc, src_exp, dst_exp, bits):
     return out
 
 
+def attention(fused_qkv, qkv_exp, score_exp, prob_exp, context_exp):
+    """The attention core of mhsa (transformer.py:228-266) composed from the
+    primitives above, for one image: fused_qkv [N][576] int8 with Q, K, V
+    column blocks and heads of 64 lanes (layout.qkv_unpack,
+    layout.py:92-129).  Returns (score [3][N][N] int32, prob [3][N][N]
+    uint8, concat [N][192] int8), concat in head-major lane order
+    (layout.head_concat, layout.py:132-155)."""
+    x = np.ascontiguousarray(fused_qkv, np.int8)
+    n = len(x)
+    score = np.zeros((3, n, n), np.int32)
+    prob = np.zeros((3, n, n), np.uint8)
+    concat = np.zeros((n, 192), np.int8)
+    for h in range(3):
+        q, k, v = (x[:, blk * 192 + h * 64: blk * 192 + h * 64 + 64] for blk in range(3))
+        # transformer.py:230-234
+        score[h] = gemm_writeback(gemm(q, k, None, transpose_b=True), 2 * qkv_exp, score_exp, 32)
+        # transformer.py:236-254: q16 = sat24(rsa(score, -(score_exp + 13)))
+        q16 = requant_array(score[h], 0, -(score_exp + 13), 24)
+        for r in range(n):
+            prob[h, r] = softmax_attention(q16[r])
+        # transformer.py:256-264
+        concat[:, h * 64:(h + 1) * 64] = gemm_writeback(
+            gemm(prob[h], v, None, a_unsigned=True), prob_exp + qkv_exp, context_exp, 8)
+    return score, prob, concat
+
+
 # ---------------------------------------------------------------- params
 
 class _Keep:

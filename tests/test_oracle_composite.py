@@ -53,6 +53,30 @@ def test_block_residual_identities(oracle):
 
 
 @pytest.mark.skipif(not gio.available("selector"), reason="selector fixture not generated")
+@pytest.mark.parametrize("exps", [None, dict(score_scale_exp=-6), dict(score_scale_exp=-31),
+                                  dict(qkv_out_scale_exp=-7, context_out_scale_exp=-12),
+                                  dict(context_out_scale_exp=20)])
+def test_attention_core_matches_block(oracle, exps):
+    # The composed attention (score GEMM, q16, softmax rows, P.V) gives the
+    # block's score / prob / concat checkpoints, and at the fixture's own
+    # exponents the golden digests.
+    import dataclasses
+    meta, _ = gio.load("block")
+    x, bp = synth.block_workload()
+    if exps:
+        bp = dataclasses.replace(bp, mhsa=dataclasses.replace(bp.mhsa, **exps))
+    rng = np.random.default_rng(4)
+    for xi in (x, rng.integers(-128, 128, (37, 192)).astype(np.int8)):
+        _, ck = oracle.transformer_block(xi, bp)
+        m = bp.mhsa
+        got = oracle.attention(ck["fused_qkv"], m.qkv_out_scale_exp, m.score_scale_exp,
+                               m.prob_scale_exp, m.context_out_scale_exp)
+        for key, arr in zip(("score", "prob", "concat"), got):
+            assert np.array_equal(arr, ck[key]), key
+            if exps is None and xi is x:
+                assert gio.digest(arr, gio.BLOCK_DTYPES[key]) == meta["checkpoints"][key], key
+
+
 def test_selector_matches_golden(oracle):
     meta, arrays = gio.load("selector")
     tokens, sp = synth.selector_workload()
