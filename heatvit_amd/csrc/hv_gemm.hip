@@ -591,11 +591,13 @@ static int run_lds(const GemmArgs &g, hipStream_t s) {
   return launch_epi<LdsK<MT, NT, WM, EPI, AMODE, KTC>::template K>(g, EPI, grid, n_blocks, s);
 }
 
-// Shapes (measured at 50432 rows): K = 192 GEMMs use the direct kernel with
-// 128x64 tiles (64x64 for GELU, whose epilogue holds more registers); K =
-// 768 (FFN2, patch embedding) the LDS-staged kernel with 128x64 tiles and
-// two workgroups per CU; other K and the gathered head rows the runtime-K
-// direct kernel.
+// Shapes (measured on the pruned batch-256 forward): the GELU GEMM (K = 192)
+// uses the direct kernel with 64x64 tiles (its epilogue holds more
+// registers); the other K = 192 and the K = 768 GEMMs (QKV, proj, FFN2,
+// patch embedding) the LDS-staged kernel with 128x64 tiles and two
+// persistent workgroups per CU (three per CU, one workgroup per tile,
+// 128x128 tiles and 64x128 tiles were slower); other K and the gathered
+// head rows the runtime-K direct kernel.
 template <int EPI>
 static int dispatch(const GemmArgs &g, int a_mode, hipStream_t s) {
   if constexpr (EPI == EPI_PATCH) {
@@ -610,7 +612,7 @@ static int dispatch(const GemmArgs &g, int a_mode, hipStream_t s) {
     if constexpr (EPI == EPI_GELU) {
       if (g.k == 192) return run<1, 1, 2, EPI, A_ROWS, 6>(g, s);
     } else if constexpr (EPI != EPI_I32) {
-      if (g.k == 192) return run<2, 1, 2, EPI, A_ROWS, 6>(g, s);
+      if (g.k == 192) return run_lds<2, 1, 2, EPI, A_ROWS, 6>(g, s);
       if (g.k == 768) return run_lds<2, 1, 2, EPI, A_ROWS, 24>(g, s);
     }
     return run<1, 1, 2, EPI, A_ROWS, 0>(g, s);
