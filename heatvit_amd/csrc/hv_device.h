@@ -143,19 +143,25 @@ __host__ __device__ __forceinline__ unsigned mul_u24(unsigned a, unsigned b) {
   return (a & 0xFFFFFFu) * (b & 0xFFFFFFu);
 }
 
-// Device operations behind gelu_q16_r: the single-precision reciprocal the
-// quotient estimate uses (any value within a few ulp of 1/d works, the
-// correction step is exact), and v >> 1 as a bit-field extract, which keeps
-// the compiler from rewriting ip + (ip >> 1) into a 64-bit average.
+// Device operations behind gelu_q16_r: the single-precision reciprocal of
+// the quotient estimate (any value within a few ulp of 1/d works, the
+// correction step is exact), and an empty register constraint on ip that
+// emits nothing but keeps the compiler from evaluating (3 * ip) >> 1 as a
+// 64-bit average of ip's summands.
 struct RcpHw {
   __device__ static float rcp(float d) { return __builtin_amdgcn_rcpf(d); }
-  __device__ static int sar1(int v) { return __builtin_amdgcn_sbfe(v, 1, 31); }
+  __device__ static int opaque(int v) {
+    asm("" : "+v"(v));
+    return v;
+  }
 };
 
 template <typename R>
 __host__ __device__ __forceinline__ int gelu_q16_r(int x) {
-  const int ip = x + (x >> 1) + (x >> 3) + (x >> 4);
-  const int ip2 = ip + R::sar1(ip) - (ip >> 4);
+  const int ip = R::opaque(x + (x >> 1) + (x >> 3) + (x >> 4));
+  // ip + (ip >> 1) == (3 * ip) >> 1 for every integer ip (floor of 1.5 ip);
+  // |3 ip| < 2^26.
+  const int ip2 = ((3 * ip) >> 1) - (ip >> 4);
   const unsigned a = (unsigned)(ip2 < 0 ? -ip2 : ip2);
   const unsigned q = a >> 16;
   const unsigned frac = (mul_u24(a & 0xFFFFu, 11u) + 15u) >> 4;
@@ -165,11 +171,11 @@ __host__ __device__ __forceinline__ int gelu_q16_r(int x) {
   const unsigned e_pos = sh < (1u << 23) - 1 ? sh : (1u << 23) - 1;
   const unsigned e = ip2 < 0 ? e_neg : e_pos;
   const unsigned den = 65536u + e;
+  // e / den < 1, so the estimate stays below 65536.5 plus a few ulp and
+  // sig <= 65536; with den < 2^24 the product below is a 24-bit multiply
+  // whose low 32 bits are all the wrapping remainder needs.
   const float est = (float)e * 65536.0f * R::rcp((float)den) + 0.5f;
-  // sig < 2^17 and den < 2^24: the product below is a 24-bit multiply whose
-  // low 32 bits are all the wrapping remainder needs.
   unsigned sig = (unsigned)est;
-  sig = sig < 0x1FFFFu ? sig : 0x1FFFFu;
   const int rem = (int)((e << 16) + (den >> 1) - mul_u24(sig, den));
   sig = sig + (rem >= (int)den ? 1u : 0u) + (unsigned)(rem >> 31);
   const unsigned ax = (unsigned)(x < 0 ? -x : x);

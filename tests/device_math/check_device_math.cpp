@@ -25,7 +25,7 @@ using namespace hv;
 
 struct RcpExact {
   static float rcp(float d) { return 1.0f / d; }
-  static int sar1(int v) { return v >> 1; }
+  static int opaque(int v) { return v; }
 };
 struct RcpLo : RcpExact { static float rcp(float d) { return std::nextafter(1.0f / d, 0.0f); } };
 struct RcpHi : RcpExact { static float rcp(float d) { return std::nextafter(1.0f / d, 1.0f); } };
