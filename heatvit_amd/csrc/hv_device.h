@@ -217,6 +217,14 @@ __device__ __forceinline__ int rq_dir(int v, const Rq &r) {
   return min(max(t, r.lo), r.hi);
 }
 
+// rq_dir for a v whose left shift cannot leave int32 (|v| <= (2^31 - 1) >>
+// -s, which the caller guarantees): the shift needs no pre-clamp.
+template <bool LEFT>
+__device__ __forceinline__ int rq_dir_nowrap(int v, const Rq &r) {
+  const int t = LEFT ? (int)((unsigned)v << -r.s) : (v + r.rnd + (v >> 31)) >> r.s;
+  return min(max(t, r.lo), r.hi);
+}
+
 // requant(gelu(requant(v, src, -16, 24)), -16, dst, 8): the GEMM+GELU
 // post-op of ffn (transformer.py:349-358) and selector._gemm_gelu
 // (selector.py:89-99).  shift_in = -16 - src_exp, shift_out = dst_exp + 16.

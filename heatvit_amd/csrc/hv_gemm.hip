@@ -32,8 +32,10 @@
 // The int32 form of each epilogue is taken when the launch's shifts lie in
 // [-30, 30], the align-add shifts are at most 21, and every bias of the
 // wavefront's columns satisfies |bias| <= 2^30 - 1 - K*2^14 (so v, the
-// aligned sums and every rounding addend stay below 2^31); the other cases
-// call the exact 64/128-bit form, kept out of line.
+// aligned sums and every rounding addend stay below 2^31) and, when the
+// first requant shifts left by k, |bias| <= ((2^31 - 1) >> k) - K*2^14 (so
+// v << k stays inside int32); the other cases call the exact 64/128-bit
+// form, kept out of line.
 #include "hv_device.h"
 #include "hv_internal.h"
 
@@ -172,11 +174,11 @@ __device__ __forceinline__ void epi_tile(const GemmArgs &g, const v16i (&acc)[MT
           const int v = acc[mt][nt][j] + bias4[nt][j >> 2][j & 3];
           constexpr bool LA = DIRS & 1, LB = (DIRS >> 1) & 1;
           if (EPI == EPI_I8) {
-            o[j] = rq_dir<LA>(v, rq_a);
+            o[j] = rq_dir_nowrap<LA>(v, rq_a);
           } else if (EPI == EPI_GELU) {
-            o[j] = rq_dir<LB>(gelu_q16(rq_dir<LA>(v, rq_a)), rq_b);
+            o[j] = rq_dir<LB>(gelu_q16(rq_dir_nowrap<LA>(v, rq_a)), rq_b);
           } else if (RESLIKE) {
-            const int t8 = rq_dir<LA>(v, rq_a);
+            const int t8 = rq_dir_nowrap<LA>(v, rq_a);
             const int r8 = (int)(int8_t)(res4[mt][nt][j >> 2] >> (8 * (j & 3)));
             const int s = EPI == EPI_RES ? r8 * (1 << g.da) + t8 * (1 << g.db)
                                          : t8 * (1 << g.da) + r8 * (1 << g.db);
@@ -497,7 +499,14 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g, int n_blocks) {
 // Host-side set-up of the epilogue preconditions.
 void epilogue_limits_pub(GemmArgs &g, int epi) {
   const long long acc_max = (long long)g.k * 128 * 128;  // |A W| bound (int8 x int8)
-  const long long lim = (1ll << 30) - 1 - acc_max;
+  long long lim = (1ll << 30) - 1 - acc_max;
+  if (g.shift_a < 0) {
+    // the first requant shifts v = acc + bias left by -shift_a: keep that
+    // shift inside int32
+    const int sl = -g.shift_a;
+    const long long lim_l = sl >= 31 ? -1 : (((1ll << 31) - 1) >> sl) - acc_max;
+    lim = lim < lim_l ? lim : lim_l;
+  }
   g.acc_lim = lim > 0 ? (int)lim : -1;
   g.narrow_ok = g.acc_lim > 0;
   g.da = g.db = g.os = 0;
