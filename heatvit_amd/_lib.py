@@ -17,6 +17,8 @@ HV_OK, HV_EVALUE, HV_EOVERFLOW, HV_EHIP = 0, -2, -3, -4
  HV_ERR_MEMORY_PROTOCOL, HV_ERR_SOFTMAX_ZERO_SUM, HV_ERR_BUSY_START) = range(8)
 HV_WARN_HEAD_DEN_ZERO, HV_WARN_PACKAGE_DEN_ZERO, HV_WARN_LN_NEGATIVE_VARIANCE = 1, 2, 4
 HV_PRIM_REQUANT, HV_PRIM_GELU, HV_PRIM_PLAN, HV_PRIM_RSA = 0, 1, 2, 3
+HV_PRIM_GELU_POST, HV_PRIM_GELU_TABLE = 4, 5
+GELU_TABLE_SO = range(3, 13)
 HV_EPI_I8, HV_EPI_I32, HV_EPI_GELU, HV_EPI_RESIDUAL = 0, 1, 2, 3
 HV_A_ROWS, HV_A_GATHER = 0, 1
 ABI_VERSION = 4

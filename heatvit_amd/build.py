@@ -4,6 +4,7 @@ Every .hip file is compiled to an object in parallel, then linked into one
 shared library next to this file.  Run `python -m heatvit_amd.build`.
 """
 
+import hashlib
 import os
 import subprocess
 import sys
@@ -22,7 +23,7 @@ FLAGS = [
     "-Wno-unused-function", "-Wno-unused-variable",
     # Packed FP32 instructions are kept out of every code object.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-I", str(HERE.parent / "include"),
+    "-I", str(HERE.parent / "include"), "-I", str(OBJ),
 ]
 
 
@@ -35,8 +36,23 @@ def _compile(src):
     return src.name, r.returncode, errs, obj
 
 
+def _gelu_tables():
+    """Writes _obj/gelu_lut.inc with gen_gelu_lut.py unless the file was
+    made by the same generator source (its SHA-256 on the first line)."""
+    gen = CSRC / "gen_gelu_lut.py"
+    out = OBJ / "gelu_lut.inc"
+    tag = "// generator " + hashlib.sha256(gen.read_bytes()).hexdigest() + "\n"
+    if out.exists() and out.read_text().startswith(tag):
+        return
+    tmp = out.with_suffix(".tmp")
+    subprocess.run([sys.executable, str(gen), str(tmp)], check=True)
+    out.write_text(tag + tmp.read_text())
+    tmp.unlink()
+
+
 def build(verbose=True):
     OBJ.mkdir(exist_ok=True)
+    _gelu_tables()
     sources = sorted(CSRC.glob("*.hip"))
     with ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
         results = list(ex.map(_compile, sources))

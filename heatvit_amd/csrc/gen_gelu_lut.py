@@ -1,0 +1,159 @@
+"""Generates gelu_lut.inc: step tables of the GEMM+GELU post-op
+
+    G_so(q) = sat8(round_shift_away(gelu(q), so))       q: 24-bit signed Q8.16
+
+(requant(gelu(q), -16, dst, 8) with so = dst + 16; nonlinear.py:60-80 and
+fixed.py:15-45 / transformer.py:349-358), one table per so in [3, 12].
+
+G_so is a step function of q with a few hundred changes.  Table layout
+(32-bit words):
+  L1[b], b = u >> 9 with u = clamp(q, qlo, qhi) - qlo: bits 0..23 the index
+      of the coarse bucket's first L2 entry, bits 24..27 s2;
+  L2 (two words per entry), one entry per 2^s2 values of u: G at the
+      entry's first u (bits 0..7 of word 0, signed) and up to three changes
+      inside the entry, each an offset (9 bits, 511 = none) and the signed
+      7-bit step taken from that offset on:
+        word 0: T[0:8] B1[8:17] D1[17:24]
+        word 1: B2[0:9] D2[9:16] B3[16:25] D3[25:32]
+  G is constant for q <= qlo and for q >= qhi.  s2 is the largest value in
+  [0, 9] that leaves at most three changes inside every entry of the bucket.
+
+The generator restates gelu in numpy, builds each table, emulates the
+lookup for every q of the 24-bit domain and refuses to write a table that
+differs from G_so anywhere.
+
+Run:  python gen_gelu_lut.py OUT.inc
+"""
+
+import sys
+
+import numpy as np
+
+SO_MIN, SO_MAX = 3, 12
+S1, K = 9, 3
+
+
+def gelu_q16(x):
+    """nonlinear.gelu (nonlinear.py:60-80) over an int64 array."""
+    x = np.asarray(x, np.int64)
+    ip = x + (x >> 1) + (x >> 3) + (x >> 4)
+    ip2 = ip + (ip >> 1) - (ip >> 4)
+    a = np.abs(ip2)
+    q = a >> 16
+    frac = ((a & 0xFFFF) * 11 + 15) >> 4
+    e_neg = np.where(q <= 16, (65536 - frac) >> np.minimum(q, 16), 0)
+    e_pos = np.where(q <= 7, np.minimum((65536 + frac) << np.minimum(q, 7), (1 << 23) - 1),
+                     (1 << 23) - 1)
+    e = np.where(ip2 < 0, e_neg, e_pos)
+    den = 65536 + e
+    sig = ((e << 16) + (den >> 1)) // den
+    return np.clip(rsa(x * sig, 16), -(1 << 23), (1 << 23) - 1)
+
+
+def rsa(v, s):
+    """round_shift_away (fixed.py:15-26) for s >= 1."""
+    h = 1 << (s - 1)
+    return np.where(v >= 0, (v + h) >> s, -((-v + h) >> s))
+
+
+def post(y, so):
+    return np.clip(rsa(y, so), -128, 127)
+
+
+def build_table(so, q, o):
+    """(qlo, qhi, L1 words, L2 words) of G_so given o = G_so(q) over the
+    whole domain q (ascending)."""
+    ch = np.nonzero(np.diff(o))[0] + 1          # o[i] != o[i - 1]
+    qlo, qhi = int(q[ch[0]] - 1), int(q[ch[-1]])
+    base = qlo - int(q[0])
+    span = qhi - qlo
+    uo = o[base:base + span + 1]                # G at u = 0 .. span
+    cu = ch - base                              # change positions in u
+    n1 = span // (1 << S1) + 1
+    l1 = np.zeros(n1, np.uint32)
+    l2 = []
+    for b in range(n1):
+        lo = b << S1
+        sel = cu[(cu >= lo) & (cu < lo + (1 << S1))] - lo
+
+        def worst(s2):
+            inner = sel[(sel & ((1 << s2) - 1)) != 0]
+            return int(np.bincount(inner >> s2).max()) if len(inner) else 0
+
+        s2 = S1
+        while s2 > 0 and worst(s2) > K:
+            s2 -= 1
+        if worst(s2) > K:
+            raise RuntimeError(f"so={so}: more than {K} changes at one offset")
+        l1[b] = (len(l2) // 2) | (s2 << 24)
+        for fb in range(1 << (S1 - s2)):
+            u0 = lo + (fb << s2)
+            fields = []
+            for c in sel[(sel >> s2) == fb]:
+                d = int(c) - (fb << s2)
+                if d == 0:
+                    continue                    # T already holds it
+                step = int(uo[lo + c] - uo[lo + c - 1])
+                if not -64 <= step < 64:
+                    raise RuntimeError(f"so={so}: step {step} exceeds 7 bits")
+                fields.append((d, step & 127))
+            fields += [(511, 0)] * (K - len(fields))
+            t = int(uo[min(u0, span)]) & 255
+            w0 = t | (fields[0][0] << 8) | (fields[0][1] << 17)
+            w1 = fields[1][0] | (fields[1][1] << 9) | (fields[2][0] << 16) | (fields[2][1] << 25)
+            l2 += [w0, w1]
+    return qlo, qhi, l1, np.array(l2, np.uint32)
+
+
+def lookup(qlo, qhi, l1, l2, q):
+    """The device lookup, restated over an array of q."""
+    def sx(v, bits):
+        v = v.astype(np.int64)
+        return np.where(v >= 1 << (bits - 1), v - (1 << bits), v)
+
+    u = np.clip(q, qlo, qhi) - qlo
+    w1 = l1[u >> S1].astype(np.int64)
+    s2 = w1 >> 24
+    f = (w1 & 0xFFFFFF) + ((u & ((1 << S1) - 1)) >> s2)
+    off = u & ((1 << s2) - 1)
+    a, b = l2[2 * f].astype(np.int64), l2[2 * f + 1].astype(np.int64)
+    o = sx(a & 255, 8)
+    o = o + np.where(off >= ((a >> 8) & 511), sx((a >> 17) & 127, 7), 0)
+    o = o + np.where(off >= (b & 511), sx((b >> 9) & 127, 7), 0)
+    o = o + np.where(off >= ((b >> 16) & 511), sx((b >> 25) & 127, 7), 0)
+    return o
+
+
+def main(out):
+    q = np.arange(-(1 << 23), 1 << 23, dtype=np.int64)
+    y = gelu_q16(q)
+    words, info = [], []
+    for so in range(SO_MIN, SO_MAX + 1):
+        o = post(y, so)
+        qlo, qhi, l1, l2 = build_table(so, q, o)
+        if not np.array_equal(lookup(qlo, qhi, l1, l2, q), o):
+            raise RuntimeError(f"so={so}: table lookup differs from the post-op")
+        n1e = len(l1) + (len(l1) & 1)
+        info.append((qlo, qhi, n1e, len(l2) // 2, len(words)))
+        words += list(l1) + [0] * (n1e - len(l1)) + list(l2)
+    lines = [
+        "// Generated by gen_gelu_lut.py: step tables of",
+        "// sat8(round_shift_away(gelu(q), so)) for so in "
+        f"[{SO_MIN}, {SO_MAX}] (layout in the generator).",
+        "namespace hv {",
+        f"constexpr int kGeluLutSoMin = {SO_MIN}, kGeluLutSoMax = {SO_MAX};",
+        "struct GeluLutInfo { int qlo, qhi, n1e, n2, off; };",
+        "constexpr GeluLutInfo kGeluLutInfo[] = {",
+    ]
+    lines += [f"  {{{a}, {b}, {c}, {d}, {e}}}," for a, b, c, d, e in info]
+    lines += ["};", f"constexpr int kGeluLutWords = {len(words)};",
+              "__device__ const unsigned kGeluLut[kGeluLutWords] = {"]
+    for i in range(0, len(words), 8):
+        lines.append("  " + " ".join(f"0x{int(w):08x}u," for w in words[i:i + 8]))
+    lines += ["};", "}  // namespace hv", ""]
+    with open(out, "w") as fh:
+        fh.write("\n".join(lines))
+
+
+if __name__ == "__main__":
+    main(sys.argv[1])

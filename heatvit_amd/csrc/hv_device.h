@@ -217,6 +217,13 @@ __device__ __forceinline__ int rq_dir(int v, const Rq &r) {
   return min(max(t, r.lo), r.hi);
 }
 
+// The shift of rq_dir_nowrap without the final clamp (for a consumer that
+// clamps to a narrower range itself).
+template <bool LEFT>
+__device__ __forceinline__ int shift_nowrap(int v, const Rq &r) {
+  return LEFT ? (int)((unsigned)v << -r.s) : (v + r.rnd + (v >> 31)) >> r.s;
+}
+
 // rq_dir for a v whose left shift cannot leave int32 (|v| <= (2^31 - 1) >>
 // -s, which the caller guarantees): the shift needs no pre-clamp.
 template <bool LEFT>

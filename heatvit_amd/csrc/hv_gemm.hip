@@ -29,6 +29,13 @@
 //                                                    transformer.py:96-101
 //   EPI_PATCH    t = requant(v, img+w, act, 8); out = align_add(t, pos[p+1])
 //                into row b*197 + 1 + p                transformer.py:120-145
+// The GELU epilogue with an output shift so = dst + 16 in [3, 12] looks the
+// post-op requant(gelu(q), -16, dst, 8) up in a step table of q instead of
+// evaluating it (gen_gelu_lut.py writes the tables and checks each against
+// the post-op over the whole 24-bit domain): the table (about 10-13 KB) is
+// staged in LDS per workgroup, and one lookup is two LDS reads and a dozen
+// integer operations against about forty for the evaluation.
+//
 // The int32 form of each epilogue is taken when the launch's shifts lie in
 // [-30, 30], the align-add shifts are at most 21, and every bias of the
 // wavefront's columns satisfies |bias| <= 2^30 - 1 - K*2^14 (so v, the
@@ -38,6 +45,7 @@
 // form, kept out of line.
 #include "hv_device.h"
 #include "hv_internal.h"
+#include "gelu_lut.inc"  // generated at build time by gen_gelu_lut.py
 
 namespace hv {
 
@@ -52,6 +60,9 @@ static constexpr int kImageBytes = 224 * 224 * 3;
 // grid with static tile striding left a partial last round per workgroup.
 static constexpr int kGridCap = 1 << 20;
 static constexpr int kLdsGridCap = 256 * 2;  // LDS-staged kernel: 2 per CU, persistent
+// GELU step-table launches: persistent, four workgroups per CU (each stages
+// the table once; two or eight per CU, or one workgroup per tile, were slower)
+static constexpr int kLutGridCap = 256 * 4;
 
 template <int AMODE>
 __device__ __forceinline__ const int8_t *a_row(const GemmArgs &g, int r) {
@@ -83,6 +94,30 @@ __device__ __noinline__ v2i epi_exact(int epi, int acc, int bias, int res, int s
   return v2i{epi == EPI_RES ? align_add_pre(res, t, da, db, os, false)
                             : align_add_pre(t, res, da, db, os, false),
              t};
+}
+
+// requant(gelu(q), -16, dst, 8) from the step table in LDS (layout in
+// gen_gelu_lut.py): the coarse word of u = clamp(q) - qlo names the first
+// fine entry and its width 2^s2; the fine entry holds the value at its
+// start and up to three (offset, step) changes inside it.
+__device__ __forceinline__ int gelu_lut(int q, const unsigned *lut, int qhi, const GemmArgs &g) {
+  const int u = min(max(q, g.lut_qlo), qhi) - g.lut_qlo;
+  const unsigned w1 = lut[u >> 9];
+  const unsigned s2 = w1 >> 24;
+  const unsigned f = (w1 & 0xFFFFFFu) + (((unsigned)u & 511u) >> s2);
+  const unsigned off = (unsigned)u & ((1u << s2) - 1u);
+  const uint2 w2 = reinterpret_cast<const uint2 *>(lut + g.lut_n1e)[f];
+  int o = __builtin_amdgcn_sbfe((int)w2.x, 0, 8);
+  o += off >= __builtin_amdgcn_ubfe(w2.x, 8, 9) ? __builtin_amdgcn_sbfe((int)w2.x, 17, 7) : 0;
+  o += off >= __builtin_amdgcn_ubfe(w2.y, 0, 9) ? __builtin_amdgcn_sbfe((int)w2.y, 9, 7) : 0;
+  o += off >= __builtin_amdgcn_ubfe(w2.y, 16, 9) ? __builtin_amdgcn_sbfe((int)w2.y, 25, 7) : 0;
+  return o;
+}
+
+// Stages the launch's GELU step table in LDS (all threads, then a barrier).
+__device__ __forceinline__ void stage_lut(const GemmArgs &g, unsigned *lut) {
+  for (int i = threadIdx.x; i < g.lut_words; i += blockDim.x) lut[i] = kGeluLut[g.lut_off + i];
+  __syncthreads();
 }
 
 __device__ __forceinline__ int pack4(int a, int b, int c, int d) {
@@ -140,8 +175,12 @@ template <int MT, int NT, int EPI, bool FAST, int DIRS>
 __device__ __forceinline__ void epi_tile(const GemmArgs &g, const v16i (&acc)[MT][NT],
                                          const v4i (&bias4)[NT][4], const v4i (&res4)[MT][NT],
                                          int r0, int ct0, int M, int h, int l32, const Rq &rq_a,
-                                         const Rq &rq_b) {
+                                         const Rq &rq_b, const unsigned *lut) {
   constexpr bool RESLIKE = EPI == EPI_RES || EPI == EPI_PATCH;
+  // the table's upper clamp in a vector register: with both bounds in
+  // scalar registers the clamp cannot be a single med3
+  int qhi = g.lut_qhi;
+  if constexpr (EPI == EPI_GELU && (DIRS & 4)) asm("" : "+v"(qhi));
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int c0 = (ct0 + nt) * 32 + 16 * h;
@@ -175,6 +214,9 @@ __device__ __forceinline__ void epi_tile(const GemmArgs &g, const v16i (&acc)[MT
           constexpr bool LA = DIRS & 1, LB = (DIRS >> 1) & 1;
           if (EPI == EPI_I8) {
             o[j] = rq_dir_nowrap<LA>(v, rq_a);
+          } else if (EPI == EPI_GELU && (DIRS & 4)) {
+            // the table's clamp [qlo, qhi] lies inside the 24-bit range
+            o[j] = gelu_lut(shift_nowrap<LA>(v, rq_a), lut, qhi, g);
           } else if (EPI == EPI_GELU) {
             o[j] = rq_dir<LB>(gelu_q16(rq_dir_nowrap<LA>(v, rq_a)), rq_b);
           } else if (RESLIKE) {
@@ -254,6 +296,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
   const Rq rq_a = rq_setup(g.shift_a, EPI == EPI_GELU ? -(1 << 23) : -128,
                            EPI == EPI_GELU ? (1 << 23) - 1 : 127);
   const Rq rq_b = rq_setup(EPI == EPI_GELU ? g.shift_b : g.os, -128, 127);
+  extern __shared__ __attribute__((aligned(16))) unsigned lut[];
+  if constexpr (EPI == EPI_GELU && (DIRS & 4)) stage_lut(g, lut);
 
   // The grid is a multiple of 8, so t & 7 (the XCD) is fixed per workgroup
   // and XCD x works through logical tiles [x*T8, (x+1)*T8).
@@ -373,7 +417,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
       }
     }
 
-    epi_tile<MT, NT, EPI, FAST, DIRS>(g, acc, bias4, res4, r0, ct0, M, h, l32, rq_a, rq_b);
+    epi_tile<MT, NT, EPI, FAST, DIRS>(g, acc, bias4, res4, r0, ct0, M, h, l32, rq_a, rq_b, lut);
   }
 }
 
@@ -480,7 +524,8 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g, int n_blocks) {
           acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bcur[nt][kt], af, acc[mt][nt], 0, 0, 0);
       }
     if (last_chunk) {
-      epi_tile<MT, NT, EPI, FAST, DIRS>(g, acc, bias4, res4, r0, ct0, M, h, l32, rq_a, rq_b);
+      epi_tile<MT, NT, EPI, FAST, DIRS>(g, acc, bias4, res4, r0, ct0, M, h, l32, rq_a, rq_b,
+                                        nullptr);
       if (!more) break;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
@@ -545,14 +590,26 @@ static int epilogue_dirs(const GemmArgs &g, int epi) {
 }
 
 // Launches kernel template K with FAST = false, or FAST = true and the
-// launch's requant directions.
-template <template <bool, int> class K>
-static int launch_epi(const GemmArgs &g, int epi, long long grid, int n_blocks, hipStream_t s) {
+// launch's requant directions (bit 2: the GELU post-op from its step table,
+// staged in dynamic LDS; direct kernel only).
+template <int EPI, template <bool, int> class K>
+static int launch_epi(const GemmArgs &g, long long grid, int n_blocks, hipStream_t s) {
   const dim3 gd((unsigned)grid), bd(256);
-  if (!fast_epilogue(g, epi)) {
+  if (!fast_epilogue(g, EPI)) {
     hv_launch(K<false, 0>::fn(), gd, bd, 0, s, g, n_blocks);
   } else {
-    switch (epilogue_dirs(g, epi)) {
+    const int dirs = epilogue_dirs(g, EPI);
+    if constexpr (EPI == EPI_GELU && K<true, 4>::kTable) {
+      if (g.lut_words > 0) {
+        // persistent: each workgroup stages the table once
+        const dim3 gp((unsigned)(grid < kLutGridCap ? grid : kLutGridCap));
+        const size_t lds = (size_t)g.lut_words * 4;
+        if (dirs & 1) hv_launch(K<true, 5>::fn(), gp, bd, lds, s, g, n_blocks);
+        else hv_launch(K<true, 4>::fn(), gp, bd, lds, s, g, n_blocks);
+        return check_hip(hipGetLastError(), "k_gemm launch");
+      }
+    }
+    switch (dirs) {
       case 0: hv_launch(K<true, 0>::fn(), gd, bd, 0, s, g, n_blocks); break;
       case 1: hv_launch(K<true, 1>::fn(), gd, bd, 0, s, g, n_blocks); break;
       case 2: hv_launch(K<true, 2>::fn(), gd, bd, 0, s, g, n_blocks); break;
@@ -566,6 +623,7 @@ template <int MT, int NT, int WM, int EPI, int AMODE, int KTC>
 struct DirectK {
   template <bool FAST, int DIRS>
   struct K {
+    static constexpr bool kTable = true;
     static auto fn() { return &k_gemm<MT, NT, WM, EPI, AMODE, KTC, FAST, FAST ? DIRS : 0>; }
   };
 };
@@ -574,7 +632,8 @@ template <int MT, int NT, int WM, int EPI, int AMODE, int KTC>
 struct LdsK {
   template <bool FAST, int DIRS>
   struct K {
-    static auto fn() { return &k_gemm_lds<MT, NT, WM, EPI, AMODE, KTC, FAST, FAST ? DIRS : 0>; }
+    static constexpr bool kTable = false;
+    static auto fn() { return &k_gemm_lds<MT, NT, WM, EPI, AMODE, KTC, FAST, FAST ? DIRS & 3 : 0>; }
   };
 };
 
@@ -586,7 +645,7 @@ static int run(const GemmArgs &g, hipStream_t s) {
   if (tiles <= 0) return HV_OK;
   long long grid = (tiles + 7) / 8 * 8;
   if (grid > kGridCap) grid = kGridCap;
-  return launch_epi<DirectK<MT, NT, WM, EPI, AMODE, KTC>::template K>(g, EPI, grid, n_blocks, s);
+  return launch_epi<EPI, DirectK<MT, NT, WM, EPI, AMODE, KTC>::template K>(g, grid, n_blocks, s);
 }
 
 template <int MT, int NT, int WM, int EPI, int AMODE, int KTC>
@@ -597,7 +656,7 @@ static int run_lds(const GemmArgs &g, hipStream_t s) {
   if (tiles <= 0) return HV_OK;
   long long grid = (tiles + 7) / 8 * 8;
   if (grid > kLdsGridCap) grid = kLdsGridCap;
-  return launch_epi<LdsK<MT, NT, WM, EPI, AMODE, KTC>::template K>(g, EPI, grid, n_blocks, s);
+  return launch_epi<EPI, LdsK<MT, NT, WM, EPI, AMODE, KTC>::template K>(g, grid, n_blocks, s);
 }
 
 // Shapes (measured on the pruned batch-256 forward): the GELU GEMM (K = 192)
@@ -643,6 +702,15 @@ int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
     return fail(HV_EVALUE, HV_ERR_ADDRESS, "gemm: bias must be 16-byte aligned");
   if (g.k > 131071)
     return fail(HV_EOVERFLOW, HV_ERR_DIMENSION, "gemm: K=%d may overflow int32", g.k);
+  g.lut_words = 0;
+  if (epi == EPI_GELU && g.shift_b >= kGeluLutSoMin && g.shift_b <= kGeluLutSoMax) {
+    const GeluLutInfo &t = kGeluLutInfo[g.shift_b - kGeluLutSoMin];
+    g.lut_off = t.off;
+    g.lut_words = t.n1e + 2 * t.n2;
+    g.lut_n1e = t.n1e;
+    g.lut_qlo = t.qlo;
+    g.lut_qhi = t.qhi;
+  }
   const int esz = epi == EPI_I32 ? 4 : 1;
   g.vec_out = ((uintptr_t)g.c & 15) == 0 && (g.ldc * esz) % 16 == 0 &&
               (!g.aux || ((uintptr_t)g.aux & 15) == 0);
@@ -656,6 +724,43 @@ int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
     case EPI_PATCH: return dispatch<EPI_PATCH>(g, a_mode, s);
     default: return fail(HV_EVALUE, HV_ERR_OPCODE, "gemm: bad epilogue %d", epi);
   }
+}
+
+// The GELU post-op of the FFN epilogue over int64 Q8.16 values (saturated
+// to 24 bits): evaluated as the int32 epilogue does, or from the step table.
+__global__ __launch_bounds__(256) void k_gelu_post(int table, const int64_t *in, int64_t *out,
+                                                   int64_t n, int so, GemmArgs g) {
+  extern __shared__ __attribute__((aligned(16))) unsigned lut[];
+  if (table) stage_lut(g, lut);
+  const Rq rb = rq_setup(so, -128, 127);
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t v = in[i];
+    const int q = (int)(v < -(1 << 23) ? -(1 << 23) : (v > (1 << 23) - 1 ? (1 << 23) - 1 : v));
+    out[i] = table ? gelu_lut(q, lut, g.lut_qhi, g) : rq(gelu_q16(q), rb);
+  }
+}
+
+int launch_gelu_post(bool table, const int64_t *in, int64_t *out, int64_t n, int so,
+                     hipStream_t s) {
+  if (so < -30 || so > 30)
+    return fail(HV_EVALUE, HV_ERR_DIMENSION, "GELU post-op shift %d outside [-30, 30]", so);
+  GemmArgs g{};
+  if (table) {
+    if (so < kGeluLutSoMin || so > kGeluLutSoMax)
+      return fail(HV_EVALUE, HV_ERR_DIMENSION, "no GELU step table for shift %d (tables: [%d, %d])",
+                  so, kGeluLutSoMin, kGeluLutSoMax);
+    const GeluLutInfo &t = kGeluLutInfo[so - kGeluLutSoMin];
+    g.lut_off = t.off;
+    g.lut_words = t.n1e + 2 * t.n2;
+    g.lut_n1e = t.n1e;
+    g.lut_qlo = t.qlo;
+    g.lut_qhi = t.qhi;
+  }
+  if (n <= 0) return HV_OK;
+  const int64_t blocks = (n + 255) / 256;
+  hv_launch(k_gelu_post, dim3((unsigned)(blocks < 2048 ? blocks : 2048)), dim3(256),
+            (size_t)g.lut_words * 4, s, table ? 1 : 0, in, out, n, so, g);
+  return check_hip(hipGetLastError(), "k_gelu_post launch");
 }
 
 // CLS rows: row b*197 = align_add(cls @ cls_exp, pos[0] @ pos_exp -> tokens)

@@ -49,12 +49,20 @@ struct GemmArgs {
   int da, db, os;  // residual / patch align-add shifts
   int vec_out;     // c (and aux) allow 16-byte row stores
   int vec_res;     // res (or pos) allow 16-byte row loads
+  // GELU post-op step table (gen_gelu_lut.py), staged in LDS when
+  // lut_words > 0: words [lut_off, lut_off + lut_words) of kGeluLut.
+  int lut_off, lut_words, lut_n1e, lut_qlo, lut_qhi;
 };
 
 // epilogue: HV_EPI_* or 4 (patch: A_PATCH gather, position-row residual).
 int launch_gemm(const GemmArgs &g, int a_mode, int epilogue, hipStream_t s);
 // Fills acc_lim / narrow_ok / da / db / os of the int32 epilogue paths.
 void epilogue_limits_pub(GemmArgs &g, int epilogue);
+
+// HV_PRIM_GELU_POST / HV_PRIM_GELU_TABLE (table = true) over n int64 Q8.16
+// values with output shift so.
+int launch_gelu_post(bool table, const int64_t *in, int64_t *out, int64_t n, int so,
+                     hipStream_t s);
 
 // Patch embedding (transformer.patch_embedding): A rows are gathered
 // patches of NHWC 224x224x3 images (or, with patch_rows, the patch matrix

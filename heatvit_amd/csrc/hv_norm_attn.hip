@@ -486,6 +486,8 @@ __global__ void k_primitive(int op, const int64_t *in, int64_t *out, int64_t n, 
 
 int launch_primitive(int op, const int64_t *in, int64_t *out, int64_t n, int a, int b, int c,
                      hipStream_t s) {
+  if (op == HV_PRIM_GELU_POST || op == HV_PRIM_GELU_TABLE)
+    return launch_gelu_post(op == HV_PRIM_GELU_TABLE, in, out, n, a, s);
   if (op < 0 || op > HV_PRIM_RSA) return fail(HV_EVALUE, HV_ERR_OPCODE, "unknown primitive %d", op);
   if (op == HV_PRIM_REQUANT && (c < 2 || c > 63))
     return fail(HV_EVALUE, HV_ERR_DIMENSION, "requant bits must be in [2, 63]");

@@ -59,6 +59,13 @@ def gelu(values):
     return _prim(_lib.HV_PRIM_GELU, values)
 
 
+def gelu_post(values, so, table=False):
+    """requant(gelu(q), -16, so - 16, 8), the FFN GELU post-op, over Q8.16
+    values (saturated to 24 bits); table=True reads the step tables the
+    FFN GEMM uses (so in [3, 12])."""
+    return _prim(_lib.HV_PRIM_GELU_TABLE if table else _lib.HV_PRIM_GELU_POST, values, so)
+
+
 def plan_sigmoid(values):
     return _prim(_lib.HV_PRIM_PLAN, values)
 

@@ -82,6 +82,12 @@ int hv_abi_version(void);
 #define HV_PRIM_GELU 1    /* out = gelu(in)                      nonlinear.py:60 */
 #define HV_PRIM_PLAN 2    /* out = plan_sigmoid(in)              nonlinear.py:83 */
 #define HV_PRIM_RSA 3     /* out = round_shift_away(in, a)       fixed.py:15  */
+/* GEMM+GELU post-op on Q8.16 inputs (saturated to 24 bits first):
+ * out = requant(gelu(in), -16, a - 16, 8), transformer.py:349-358.  _POST
+ * computes it, _TABLE looks it up in the step tables the FFN GEMM uses for
+ * a in [3, 12] (HV_EVALUE outside). */
+#define HV_PRIM_GELU_POST 4
+#define HV_PRIM_GELU_TABLE 5
 
 /* Element-wise: out[i] = op(in[i]; a, b, c) over n int64 values. */
 int hv_eval_primitive(int op, const int64_t *in, int64_t *out, int64_t n, int a, int b,
