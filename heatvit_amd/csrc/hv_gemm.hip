@@ -96,22 +96,9 @@ __device__ __noinline__ v2i epi_exact(int epi, int acc, int bias, int res, int s
              t};
 }
 
-// requant(gelu(q), -16, dst, 8) from the step table in LDS (layout in
-// gen_gelu_lut.py): the coarse word of u = clamp(q) - qlo names the first
-// fine entry and its width 2^s2; the fine entry holds the value at its
-// start and up to three (offset, step) changes inside it.
+// The launch's GELU step table in LDS (gelu_table in hv_device.h).
 __device__ __forceinline__ int gelu_lut(int q, const unsigned *lut, int qhi, const GemmArgs &g) {
-  const int u = min(max(q, g.lut_qlo), qhi) - g.lut_qlo;
-  const unsigned w1 = lut[u >> 9];
-  const unsigned s2 = w1 >> 24;
-  const unsigned f = (w1 & 0xFFFFFFu) + (((unsigned)u & 511u) >> s2);
-  const unsigned off = (unsigned)u & ((1u << s2) - 1u);
-  const uint2 w2 = reinterpret_cast<const uint2 *>(lut + g.lut_n1e)[f];
-  int o = __builtin_amdgcn_sbfe((int)w2.x, 0, 8);
-  o += off >= __builtin_amdgcn_ubfe(w2.x, 8, 9) ? __builtin_amdgcn_sbfe((int)w2.x, 17, 7) : 0;
-  o += off >= __builtin_amdgcn_ubfe(w2.y, 0, 9) ? __builtin_amdgcn_sbfe((int)w2.y, 9, 7) : 0;
-  o += off >= __builtin_amdgcn_ubfe(w2.y, 16, 9) ? __builtin_amdgcn_sbfe((int)w2.y, 25, 7) : 0;
-  return o;
+  return gelu_table(q, lut, reinterpret_cast<const uint2 *>(lut + g.lut_n1e), g.lut_qlo, qhi);
 }
 
 // Stages the launch's GELU step table in LDS (all threads, then a barrier).
