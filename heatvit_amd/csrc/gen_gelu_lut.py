@@ -9,14 +9,18 @@ G_so is a step function of q with a few hundred changes.  Table layout
 (32-bit words):
   L1[b], b = u >> 9 with u = clamp(q, qlo, qhi) - qlo: bits 0..23 the index
       of the coarse bucket's first L2 entry, bits 24..27 s2;
-  L2 (two words per entry), one entry per 2^s2 values of u: G at the
-      entry's first u (bits 0..7 of word 0, signed) and up to three changes
-      inside the entry, each an offset (9 bits, 511 = none) and the signed
-      7-bit step taken from that offset on:
+  L2, one entry per 2^s2 values of u: G at the entry's first u and up to K
+      changes inside the entry, each an offset (9 bits, 511 = none) and the
+      signed 7-bit step taken from that offset on.  K = 1: one word per entry,
+        T[0:8] B1[8:17] D1[17:24];
+      K = 3: two words per entry,
         word 0: T[0:8] B1[8:17] D1[17:24]
-        word 1: B2[0:9] D2[9:16] B3[16:25] D3[25:32]
+        word 1: B2[0:9] D2[9:16] B3[16:25] D3[25:32].
   G is constant for q <= qlo and for q >= qhi.  s2 is the largest value in
-  [0, 9] that leaves at most three changes inside every entry of the bucket.
+  [0, 9] that leaves at most K changes inside every entry of the bucket.
+  Each so gets the one-change form when that table fits in 16 KB (fewer
+  operations per lookup), the three-change form otherwise (a smaller table
+  where the rounding of rsa makes G wiggle).
 
 The generator restates gelu in numpy, builds each table, emulates the
 lookup for every q of the 24-bit domain and refuses to write a table that
@@ -30,7 +34,8 @@ import sys
 import numpy as np
 
 SO_MIN, SO_MAX = 3, 12
-S1, K = 9, 3
+S1 = 9
+K1_MAX_BYTES = 16384
 
 
 def gelu_q16(x):
@@ -60,9 +65,10 @@ def post(y, so):
     return np.clip(rsa(y, so), -128, 127)
 
 
-def build_table(so, q, o):
-    """(qlo, qhi, L1 words, L2 words) of G_so given o = G_so(q) over the
-    whole domain q (ascending)."""
+def build_table(so, q, o, K):
+    """(qlo, qhi, L1 words, L2 words) of G_so with at most K (1 or 3)
+    changes per entry, given o = G_so(q) over the whole domain q
+    (ascending)."""
     ch = np.nonzero(np.diff(o))[0] + 1          # o[i] != o[i - 1]
     qlo, qhi = int(q[ch[0]] - 1), int(q[ch[-1]])
     base = qlo - int(q[0])
@@ -85,7 +91,7 @@ def build_table(so, q, o):
             s2 -= 1
         if worst(s2) > K:
             raise RuntimeError(f"so={so}: more than {K} changes at one offset")
-        l1[b] = (len(l2) // 2) | (s2 << 24)
+        l1[b] = (len(l2) // (2 if K == 3 else 1)) | (s2 << 24)
         for fb in range(1 << (S1 - s2)):
             u0 = lo + (fb << s2)
             fields = []
@@ -100,12 +106,15 @@ def build_table(so, q, o):
             fields += [(511, 0)] * (K - len(fields))
             t = int(uo[min(u0, span)]) & 255
             w0 = t | (fields[0][0] << 8) | (fields[0][1] << 17)
-            w1 = fields[1][0] | (fields[1][1] << 9) | (fields[2][0] << 16) | (fields[2][1] << 25)
-            l2 += [w0, w1]
+            if K == 1:
+                l2.append(w0)
+            else:
+                w1 = fields[1][0] | (fields[1][1] << 9) | (fields[2][0] << 16) | (fields[2][1] << 25)
+                l2 += [w0, w1]
     return qlo, qhi, l1, np.array(l2, np.uint32)
 
 
-def lookup(qlo, qhi, l1, l2, q):
+def lookup(qlo, qhi, l1, l2, q, K):
     """The device lookup, restated over an array of q."""
     def sx(v, bits):
         v = v.astype(np.int64)
@@ -116,11 +125,13 @@ def lookup(qlo, qhi, l1, l2, q):
     s2 = w1 >> 24
     f = (w1 & 0xFFFFFF) + ((u & ((1 << S1) - 1)) >> s2)
     off = u & ((1 << s2) - 1)
-    a, b = l2[2 * f].astype(np.int64), l2[2 * f + 1].astype(np.int64)
+    a = l2[(2 if K == 3 else 1) * f].astype(np.int64)
     o = sx(a & 255, 8)
     o = o + np.where(off >= ((a >> 8) & 511), sx((a >> 17) & 127, 7), 0)
-    o = o + np.where(off >= (b & 511), sx((b >> 9) & 127, 7), 0)
-    o = o + np.where(off >= ((b >> 16) & 511), sx((b >> 25) & 127, 7), 0)
+    if K == 3:
+        b = l2[2 * f + 1].astype(np.int64)
+        o = o + np.where(off >= (b & 511), sx((b >> 9) & 127, 7), 0)
+        o = o + np.where(off >= ((b >> 16) & 511), sx((b >> 25) & 127, 7), 0)
     return o
 
 
@@ -130,11 +141,15 @@ def main(out):
     words, info = [], []
     for so in range(SO_MIN, SO_MAX + 1):
         o = post(y, so)
-        qlo, qhi, l1, l2 = build_table(so, q, o)
-        if not np.array_equal(lookup(qlo, qhi, l1, l2, q), o):
+        K = 1
+        qlo, qhi, l1, l2 = build_table(so, q, o, K)
+        if 4 * (len(l1) + len(l2)) > K1_MAX_BYTES:
+            K = 3
+            qlo, qhi, l1, l2 = build_table(so, q, o, K)
+        if not np.array_equal(lookup(qlo, qhi, l1, l2, q, K), o):
             raise RuntimeError(f"so={so}: table lookup differs from the post-op")
         n1e = len(l1) + (len(l1) & 1)
-        info.append((qlo, qhi, n1e, len(l2) // 2, len(words)))
+        info.append((qlo, qhi, n1e, len(l2) // (2 if K == 3 else 1), len(words), K))
         words += list(l1) + [0] * (n1e - len(l1)) + list(l2)
     lines = [
         "// Generated by gen_gelu_lut.py: step tables of",
@@ -142,10 +157,11 @@ def main(out):
         f"[{SO_MIN}, {SO_MAX}] (layout in the generator).",
         "namespace hv {",
         f"constexpr int kGeluLutSoMin = {SO_MIN}, kGeluLutSoMax = {SO_MAX};",
-        "struct GeluLutInfo { int qlo, qhi, n1e, n2, off; };",
+        "// n2 entries of k words (k = 1 or 3 changes per entry: 1 or 2 words)",
+        "struct GeluLutInfo { int qlo, qhi, n1e, n2, off, k; };",
         "constexpr GeluLutInfo kGeluLutInfo[] = {",
     ]
-    lines += [f"  {{{a}, {b}, {c}, {d}, {e}}}," for a, b, c, d, e in info]
+    lines += [f"  {{{a}, {b}, {c}, {d}, {e}, {k}}}," for a, b, c, d, e, k in info]
     lines += ["};", f"constexpr int kGeluLutWords = {len(words)};",
               "__device__ const unsigned kGeluLut[kGeluLutWords] = {"]
     for i in range(0, len(words), 8):

@@ -241,24 +241,31 @@ __device__ __forceinline__ int gelu_post(i64 v, int shift_in, int shift_out) {
 }
 
 // requant(gelu(q), -16, so - 16, 8) from a GELU step table (layout in
-// gen_gelu_lut.py) staged in LDS: l1 the coarse words, l2 the fine
-// entries, [qlo, qhi] the table's clamp.  The coarse word of
-// u = clamp(q) - qlo names the first fine entry and its width 2^s2; the
-// fine entry holds the value at its start and up to three (offset, step)
-// changes inside it.
-__device__ __forceinline__ int gelu_table(int q, const unsigned *l1, const uint2 *l2, int qlo,
+// gen_gelu_lut.py) staged in LDS: l1 the coarse words, l2 the fine entries
+// (K = 1: one word each, K = 3: two), [qlo, qhi] the table's clamp.  The
+// coarse word of u = clamp(q) - qlo names the first fine entry and its
+// width 2^s2; the fine entry holds the value at its start and up to K
+// (offset, step) changes inside it.
+template <int K>
+__device__ __forceinline__ int gelu_table(int q, const unsigned *l1, const unsigned *l2, int qlo,
                                           int qhi) {
   const int u = min(max(q, qlo), qhi) - qlo;
   const unsigned w1 = l1[u >> 9];
   const unsigned s2 = w1 >> 24;
   const unsigned f = (w1 & 0xFFFFFFu) + (((unsigned)u & 511u) >> s2);
   const unsigned off = (unsigned)u & ((1u << s2) - 1u);
-  const uint2 w2 = l2[f];
-  int o = __builtin_amdgcn_sbfe((int)w2.x, 0, 8);
-  o += off >= __builtin_amdgcn_ubfe(w2.x, 8, 9) ? __builtin_amdgcn_sbfe((int)w2.x, 17, 7) : 0;
-  o += off >= __builtin_amdgcn_ubfe(w2.y, 0, 9) ? __builtin_amdgcn_sbfe((int)w2.y, 9, 7) : 0;
-  o += off >= __builtin_amdgcn_ubfe(w2.y, 16, 9) ? __builtin_amdgcn_sbfe((int)w2.y, 25, 7) : 0;
-  return o;
+  if constexpr (K == 1) {
+    const unsigned w = l2[f];
+    const int o = __builtin_amdgcn_sbfe((int)w, 0, 8);
+    return o + (off >= __builtin_amdgcn_ubfe(w, 8, 9) ? __builtin_amdgcn_sbfe((int)w, 17, 7) : 0);
+  } else {
+    const uint2 w2 = reinterpret_cast<const uint2 *>(l2)[f];
+    int o = __builtin_amdgcn_sbfe((int)w2.x, 0, 8);
+    o += off >= __builtin_amdgcn_ubfe(w2.x, 8, 9) ? __builtin_amdgcn_sbfe((int)w2.x, 17, 7) : 0;
+    o += off >= __builtin_amdgcn_ubfe(w2.y, 0, 9) ? __builtin_amdgcn_sbfe((int)w2.y, 9, 7) : 0;
+    o += off >= __builtin_amdgcn_ubfe(w2.y, 16, 9) ? __builtin_amdgcn_sbfe((int)w2.y, 25, 7) : 0;
+    return o;
+  }
 }
 
 // plan_sigmoid (nonlinear.py:83-95).

@@ -97,8 +97,9 @@ __device__ __noinline__ v2i epi_exact(int epi, int acc, int bias, int res, int s
 }
 
 // The launch's GELU step table in LDS (gelu_table in hv_device.h).
+template <int K>
 __device__ __forceinline__ int gelu_lut(int q, const unsigned *lut, int qhi, const GemmArgs &g) {
-  return gelu_table(q, lut, reinterpret_cast<const uint2 *>(lut + g.lut_n1e), g.lut_qlo, qhi);
+  return gelu_table<K>(q, lut, lut + g.lut_n1e, g.lut_qlo, qhi);
 }
 
 // Stages the launch's GELU step table in LDS (all threads, then a barrier).
@@ -203,7 +204,7 @@ __device__ __forceinline__ void epi_tile(const GemmArgs &g, const v16i (&acc)[MT
             o[j] = rq_dir_nowrap<LA>(v, rq_a);
           } else if (EPI == EPI_GELU && (DIRS & 4)) {
             // the table's clamp [qlo, qhi] lies inside the 24-bit range
-            o[j] = gelu_lut(shift_nowrap<LA>(v, rq_a), lut, qhi, g);
+            o[j] = gelu_lut<(DIRS & 8) ? 1 : 3>(shift_nowrap<LA>(v, rq_a), lut, qhi, g);
           } else if (EPI == EPI_GELU) {
             o[j] = rq_dir<LB>(gelu_q16(rq_dir_nowrap<LA>(v, rq_a)), rq_b);
           } else if (RESLIKE) {
@@ -578,7 +579,8 @@ static int epilogue_dirs(const GemmArgs &g, int epi) {
 
 // Launches kernel template K with FAST = false, or FAST = true and the
 // launch's requant directions (bit 2: the GELU post-op from its step table,
-// staged in dynamic LDS; direct kernel only).
+// staged in dynamic LDS, direct kernel only; bit 3: that table has one
+// change per entry).
 template <int EPI, template <bool, int> class K>
 static int launch_epi(const GemmArgs &g, long long grid, int n_blocks, hipStream_t s) {
   const dim3 gd((unsigned)grid), bd(256);
@@ -591,8 +593,13 @@ static int launch_epi(const GemmArgs &g, long long grid, int n_blocks, hipStream
         // persistent: each workgroup stages the table once
         const dim3 gp((unsigned)(grid < kLutGridCap ? grid : kLutGridCap));
         const size_t lds = (size_t)g.lut_words * 4;
-        if (dirs & 1) hv_launch(K<true, 5>::fn(), gp, bd, lds, s, g, n_blocks);
-        else hv_launch(K<true, 4>::fn(), gp, bd, lds, s, g, n_blocks);
+        if (g.lut_k == 1) {
+          if (dirs & 1) hv_launch(K<true, 13>::fn(), gp, bd, lds, s, g, n_blocks);
+          else hv_launch(K<true, 12>::fn(), gp, bd, lds, s, g, n_blocks);
+        } else {
+          if (dirs & 1) hv_launch(K<true, 5>::fn(), gp, bd, lds, s, g, n_blocks);
+          else hv_launch(K<true, 4>::fn(), gp, bd, lds, s, g, n_blocks);
+        }
         return check_hip(hipGetLastError(), "k_gemm launch");
       }
     }
@@ -693,7 +700,8 @@ int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
   if (epi == EPI_GELU && g.shift_b >= kGeluLutSoMin && g.shift_b <= kGeluLutSoMax) {
     const GeluLutInfo &t = kGeluLutInfo[g.shift_b - kGeluLutSoMin];
     g.lut_off = t.off;
-    g.lut_words = t.n1e + 2 * t.n2;
+    g.lut_k = t.k;
+    g.lut_words = t.n1e + (t.k == 1 ? 1 : 2) * t.n2;
     g.lut_n1e = t.n1e;
     g.lut_qlo = t.qlo;
     g.lut_qhi = t.qhi;
@@ -723,7 +731,8 @@ __global__ __launch_bounds__(256) void k_gelu_post(int table, const int64_t *in,
   for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
     const int64_t v = in[i];
     const int q = (int)(v < -(1 << 23) ? -(1 << 23) : (v > (1 << 23) - 1 ? (1 << 23) - 1 : v));
-    out[i] = table ? gelu_lut(q, lut, g.lut_qhi, g) : rq(gelu_q16(q), rb);
+    out[i] = !table ? rq(gelu_q16(q), rb)
+                    : g.lut_k == 1 ? gelu_lut<1>(q, lut, g.lut_qhi, g) : gelu_lut<3>(q, lut, g.lut_qhi, g);
   }
 }
 
@@ -738,7 +747,8 @@ int launch_gelu_post(bool table, const int64_t *in, int64_t *out, int64_t n, int
                   so, kGeluLutSoMin, kGeluLutSoMax);
     const GeluLutInfo &t = kGeluLutInfo[so - kGeluLutSoMin];
     g.lut_off = t.off;
-    g.lut_words = t.n1e + 2 * t.n2;
+    g.lut_k = t.k;
+    g.lut_words = t.n1e + (t.k == 1 ? 1 : 2) * t.n2;
     g.lut_n1e = t.n1e;
     g.lut_qlo = t.qlo;
     g.lut_qhi = t.qhi;

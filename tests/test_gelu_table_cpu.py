@@ -41,14 +41,14 @@ def test_post_op_matches_requant(oracle, gen, domain):
         assert np.array_equal(gen.post(y[idx], so), want), so
 
 
-@pytest.mark.parametrize("so", [3, 12])
-def test_table_lookup_is_exact_and_checked(gen, domain, so):
+@pytest.mark.parametrize("so,k", [(3, 1), (3, 3), (7, 3), (12, 1)])
+def test_table_lookup_is_exact_and_checked(gen, domain, so, k):
     q, y = domain
     o = gen.post(y, so)
-    qlo, qhi, l1, l2 = gen.build_table(so, q, o)
-    assert np.array_equal(gen.lookup(qlo, qhi, l1, l2, q), o)
+    qlo, qhi, l1, l2 = gen.build_table(so, q, o, k)
+    assert np.array_equal(gen.lookup(qlo, qhi, l1, l2, q, k), o)
     # G is constant outside [qlo, qhi]
     assert (o[q <= qlo] == o[q == qlo][0]).all() and (o[q >= qhi] == o[q == qhi][0]).all()
     bad = l2.copy()
-    bad[2 * (int(l1[0]) & 0xFFFFFF)] ^= 1          # value at qlo, off by one
-    assert not np.array_equal(gen.lookup(qlo, qhi, l1, bad, q), o)
+    bad[(2 if k == 3 else 1) * (int(l1[0]) & 0xFFFFFF)] ^= 1   # value at qlo, off by one
+    assert not np.array_equal(gen.lookup(qlo, qhi, l1, bad, q, k), o)
