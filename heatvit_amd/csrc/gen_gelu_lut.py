@@ -18,7 +18,7 @@ G_so is a step function of q with a few hundred changes.  Table layout
         word 1: B2[0:9] D2[9:16] B3[16:25] D3[25:32].
   G is constant for q <= qlo and for q >= qhi.  s2 is the largest value in
   [0, 9] that leaves at most K changes inside every entry of the bucket.
-  Each so gets the one-change form when that table fits in 16 KB (fewer
+  Each so gets the one-change form when that table fits in 32 KB (fewer
   operations per lookup), the three-change form otherwise (a smaller table
   where the rounding of rsa makes G wiggle).
 
@@ -35,7 +35,7 @@ import numpy as np
 
 SO_MIN, SO_MAX = 3, 12
 S1 = 9
-K1_MAX_BYTES = 16384
+K1_MAX_BYTES = 32768
 
 
 def gelu_q16(x):
