@@ -52,3 +52,25 @@ def test_table_range_is_checked():
     with pytest.raises(ValueError):
         gelu_post([0, 1], 13, table=True)
     assert _lib.lib().hv_last_error_class() == _lib.HV_ERR_DIMENSION
+
+
+@pytest.mark.parametrize("src", [-14, -19])
+def test_ffn_gemm_gelu_every_table(oracle, src):
+    # The FFN1 shape (K = 192, N = 768) through the GEMM's GELU epilogue for
+    # every output shift with a step table (so = dst + 16 in [3, 12], one-
+    # and three-change tables) and the evaluated neighbours (so = 2, 13);
+    # src = -14 shifts the product left, -19 right.
+    from heatvit_amd import ops
+    rng = np.random.default_rng(-src)
+    m, k, n = 300, 192, 768
+    a = rng.integers(-128, 128, (m, k))
+    a[::7] //= 64                      # rows whose q stays near zero
+    w = rng.integers(-128, 128, (k, n))
+    bias = rng.integers(-(1 << 18), 1 << 18, n)
+    acc = oracle.gemm(a, w, bias)
+    q = oracle.requant_array(acc, src, -16, 24)
+    y = oracle.gelu_array(q).astype(np.int64)
+    for dst in range(-14, -2):
+        want = oracle.requant_array(y, -16, dst, 8)
+        got = ops.gemm_writeback(a, w, bias, src, dst, 8, epilogue="gelu")
+        assert np.array_equal(got, want), (src, dst)
