@@ -188,6 +188,8 @@ static int64_t softmax_exp(int64_t xt) {
   return z >= 63 ? 0 : e >> z;
 }
 
+int64_t hvo_softmax_exp(int64_t xt) { return softmax_exp(xt); }
+
 /* nonlinear.softmax_scaled (nonlinear.py:109-121). */
 int hvo_softmax_scaled(const int32_t *x, int n, int32_t delta2, int32_t *out) {
   if (n <= 0) return HVO_EVALUE;

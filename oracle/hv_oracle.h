@@ -50,6 +50,8 @@ uint64_t hvo_isqrt(uint64_t radicand, uint64_t *rem);
 int32_t hvo_gelu(int32_t x);
 int32_t hvo_plan_sigmoid(int32_t x);
 void hvo_gelu_array(const int32_t *x, int32_t *out, int64_t n);
+/* nonlinear._softmax_exp (nonlinear.py:98-106) of one x_tilde <= 0. */
+int64_t hvo_softmax_exp(int64_t xt);
 int hvo_softmax_scaled(const int32_t *x, int n, int32_t delta2, int32_t *out);
 int hvo_softmax_attention(const int32_t *x, int n, uint8_t *out);
 int hvo_softmax_selector(const int32_t *x, int n, int32_t *out);

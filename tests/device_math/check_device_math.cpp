@@ -7,7 +7,9 @@
 //            only ulp-accurate), against hvo_gelu;
 //   softmax  the 32-bit exp / reciprocal / ratio path against
 //            hvo_softmax_attention and hvo_softmax_selector on random rows,
-//            and the branch-free 32-bit reciprocal over all its row sums;
+//            the branch-free 32-bit reciprocal over all its row sums, and
+//            the exp alone against hvo_softmax_exp for every x_tilde in
+//            [-2^25, 0] plus a million larger magnitudes;
 //   layernorm the int32 limb-split normalisation (ln_row_consts / ln_norm)
 //            against hvo_layernorm on random and degenerate rows over the
 //            exponent range the kernel takes it for.
@@ -50,6 +52,22 @@ static long check_recip24() {
     if (softmax_recip24_r<RcpExact>(s) != ref || softmax_recip24_r<RcpLo>(s) != ref ||
         softmax_recip24_r<RcpHi>(s) != ref)
       if (++bad < 5) std::printf("recip24 mismatch at sum=%u (ref %u)\n", s, ref);
+  }
+  return bad;
+}
+
+// softmax_exp against the oracle for every x_tilde in [-2^25, 0] and a
+// spread of larger magnitudes down to -(2^31 - 1).
+static long check_exp() {
+  long bad = 0;
+  for (int x = -(1 << 25); x <= 0; ++x)
+    if ((long long)softmax_exp(x) != hvo_softmax_exp(x))
+      if (++bad < 5) std::printf("softmax_exp mismatch at %d\n", x);
+  std::mt19937_64 rng(9);
+  for (int i = 0; i < 1000000; ++i) {
+    const int x = -(int)(rng() % 2147483647u);
+    if ((long long)softmax_exp(x) != hvo_softmax_exp(x))
+      if (++bad < 5) std::printf("softmax_exp mismatch at %d\n", x);
   }
   return bad;
 }
@@ -133,7 +151,7 @@ static long check_layernorm(int rows) {
 
 int main(int argc, char **argv) {
   const int rows = argc > 1 ? std::atoi(argv[1]) : 100000;
-  const long g = check_gelu(), s = check_softmax(rows) + check_recip24(),
+  const long g = check_gelu(), s = check_softmax(rows) + check_recip24() + check_exp(),
              l = check_layernorm(rows);
   std::printf("gelu_bad=%ld softmax_bad=%ld layernorm_bad=%ld\n", g, s, l);
   return (g || s || l) ? 1 : 0;
