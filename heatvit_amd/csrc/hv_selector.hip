@@ -3,10 +3,11 @@
 //
 // k_selector_head, one workgroup per (image, head): local MLP + head
 //   statistic (:253, :358), candidate mean (:273), concat + 64->32->16->2
-//   score MLP + 2-way selector softmax (:292, :307, :338).  One thread owns
-//   one candidate chain; the tiny GEMMs (K = 64/32/16) run on v_dot4_i32_i8
-//   from LDS-held, output-major weights.  Head scores and statistics go to
-//   a workspace.
+//   score MLP + 2-way selector softmax (:292, :307, :338).  Two adjacent
+//   lanes own one candidate, each computing half of every layer's outputs
+//   and swapping halves by a lane shuffle; the tiny GEMMs (K = 64/32/16)
+//   run on v_dot4_i32_i8 from LDS-held, output-major weights.  Head scores
+//   and statistics go to a workspace.
 // k_selector_keep, one wavefront per image: head-weight MLP with PLAN
 //   (:370) and the head fuse (:392) per candidate (skipped when the fused
 //   scores are given), then the stable keep list (fused >= 32768) and the
@@ -42,7 +43,9 @@ __device__ __forceinline__ int sel_gelu(int acc, int bias, bool fast, const Rq &
   return gelu_exact(acc, bias, sh_in, sh_out);
 }
 
-__global__ __launch_bounds__(256) void k_selector_head(hv_selector_dev p, const int8_t *tokens,
+constexpr int kHeadThreads = 512;  // two lanes per candidate, kMaxCand <= 256
+
+__global__ __launch_bounds__(kHeadThreads) void k_selector_head(hv_selector_dev p, const int8_t *tokens,
                                                        const int32_t *offsets,
                                                        const uint8_t *pkg_in, int32_t *hs_out,
                                                        int8_t *stats_out, int fast_shifts,
@@ -54,7 +57,7 @@ __global__ __launch_bounds__(256) void k_selector_head(hv_selector_dev p, const 
   __shared__ int bl[32], bb1[32], bb2[16];
   __shared__ int local_s[kMaxCand * 8];  // [C][32] int8 as words
   __shared__ int glob[8];                 // [32] int8 as words
-  __shared__ int hbuf[12 * 256];          // per thread: h1 (8 words), h2 (4 words)
+  __shared__ int hbuf[kHeadThreads];      // partial channel sums of the candidate mean
 
   const int b = blockIdx.x / 3, h = blockIdx.x - 3 * (blockIdx.x / 3), tid = threadIdx.x;
   const int row0 = offsets[b], N = offsets[b + 1] - row0, C = N - 1;
@@ -63,9 +66,9 @@ __global__ __launch_bounds__(256) void k_selector_head(hv_selector_dev p, const 
 
   {
     const int *src = reinterpret_cast<const int *>(p.local_wt) + h * 512;
-    for (int i = tid; i < 512; i += 256) wl[i] = src[i];
+    for (int i = tid; i < 512; i += kHeadThreads) wl[i] = src[i];
     src = reinterpret_cast<const int *>(p.w1t) + h * 512;
-    for (int i = tid; i < 512; i += 256) w1[i] = src[i];
+    for (int i = tid; i < 512; i += kHeadThreads) w1[i] = src[i];
     src = reinterpret_cast<const int *>(p.w2t) + h * 128;
     if (tid < 128) w2[tid] = src[tid];
     src = reinterpret_cast<const int *>(p.w3t) + h * 8;
@@ -91,7 +94,8 @@ __global__ __launch_bounds__(256) void k_selector_head(hv_selector_dev p, const 
   {
     const int sh_in = -16 - (p.in_exp + p.local_w_exp), sh_out = p.local_out_exp + 16;
     const Rq ra = rq_setup(sh_in, -(1 << 23), (1 << 23) - 1), rb = rq_setup(sh_out, -128, 127);
-    for (int c = tid; c < C; c += 256) {
+    const int half = tid & 1;
+    for (int c = tid >> 1; c < C; c += kHeadThreads / 2) {
       int x[16];
       const v4i *src = reinterpret_cast<const v4i *>(cand + (size_t)c * 192 + h * 64);
 #pragma unroll
@@ -99,14 +103,17 @@ __global__ __launch_bounds__(256) void k_selector_head(hv_selector_dev p, const 
         const v4i v = src[k];
         x[4 * k] = v[0]; x[4 * k + 1] = v[1]; x[4 * k + 2] = v[2]; x[4 * k + 3] = v[3];
       }
-      int lane_sum = 0;
+      if (half == 0) {
+        int lane_sum = 0;
 #pragma unroll
-      for (int k = 0; k < 16; ++k) lane_sum = dot4(x[k], 0x01010101, lane_sum);
-      const int8_t stat = (int8_t)sat_bits(round_div_pos(lane_sum, 64), 8);
-      stats_out[((size_t)b * kMaxCand + c) * 3 + h] = stat;
-      if (ck.head_stats) ck.head_stats[((size_t)b * kMaxCand + c) * 3 + h] = stat;
+        for (int k = 0; k < 16; ++k) lane_sum = dot4(x[k], 0x01010101, lane_sum);
+        const int8_t stat = (int8_t)sat_bits(round_div_pos(lane_sum, 64), 8);
+        stats_out[((size_t)b * kMaxCand + c) * 3 + h] = stat;
+        if (ck.head_stats) ck.head_stats[((size_t)b * kMaxCand + c) * 3 + h] = stat;
+      }
+      // this lane: output words 4*half .. 4*half + 3 (channels 16*half ..)
 #pragma unroll 1
-      for (int jg = 0; jg < 8; ++jg) {
+      for (int jg = 4 * half; jg < 4 * half + 4; ++jg) {
         int word = 0;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
@@ -125,20 +132,21 @@ __global__ __launch_bounds__(256) void k_selector_head(hv_selector_dev p, const 
     }
   }
   __syncthreads();
-  // Stage 2: global feature = sat8(round_div(sum_c local, C)); eight
+  // Stage 2: global feature = sat8(round_div(sum_c local, C)); sixteen
   // partial sums per channel, then one thread per channel.
   {
+    constexpr int kParts = kHeadThreads / 32;
     const int8_t *l8 = reinterpret_cast<const int8_t *>(local_s);
     const int ch = tid & 31, part = tid >> 5;
     int s = 0;
-    for (int c = part; c < C; c += 8) s += l8[c * 32 + ch];
+    for (int c = part; c < C; c += kParts) s += l8[c * 32 + ch];
     hbuf[tid] = s;
   }
   __syncthreads();
   if (tid < 32) {
     int s = 0;
 #pragma unroll
-    for (int part = 0; part < 8; ++part) s += hbuf[part * 32 + tid];
+    for (int part = 0; part < kHeadThreads / 32; ++part) s += hbuf[part * 32 + tid];
     const int8_t gv = (int8_t)sat_bits(round_div_pos(s, C), 8);
     reinterpret_cast<int8_t *>(glob)[tid] = gv;
     if (ck.global) ck.global[((size_t)b * 3 + h) * 32 + tid] = gv;
@@ -152,19 +160,21 @@ __global__ __launch_bounds__(256) void k_selector_head(hv_selector_dev p, const 
     const int sq = -16 - p.logits_out_exp;
     const Rq r1a = rq_setup(s1_in, -(1 << 23), (1 << 23) - 1), r1b = rq_setup(s1_out, -128, 127);
     const Rq r2a = rq_setup(s2_in, -(1 << 23), (1 << 23) - 1), r2b = rq_setup(s2_out, -128, 127);
-    for (int c = tid; c < C; c += 256) {
+    const int half = tid & 1;
+    for (int c = tid >> 1; c < C; c += kHeadThreads / 2) {
       int lg[16];
 #pragma unroll
       for (int k = 0; k < 8; ++k) lg[k] = local_s[c * 8 + k];
 #pragma unroll
       for (int k = 0; k < 8; ++k) lg[8 + k] = glob[k];
-      int *hb = &hbuf[tid];  // word i of this thread at hb[256 * i]
+      // layer 1: this lane's four output words, the partner's by shuffle
+      int mine[4];
 #pragma unroll 1
-      for (int jg = 0; jg < 8; ++jg) {
+      for (int q = 0; q < 4; ++q) {
         int word = 0;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const int j = jg * 4 + jj;
+          const int j = (4 * half + q) * 4 + jj;
           int acc = 0;
           const int *w = &w1[j * 16];
 #pragma unroll
@@ -172,17 +182,23 @@ __global__ __launch_bounds__(256) void k_selector_head(hv_selector_dev p, const 
           const int v = sel_gelu(acc, bb1[j], fast, r1a, r1b, s1_in, s1_out);
           word |= (v & 0xFF) << (8 * jj);
         }
-        hb[256 * jg] = word;
+        mine[q] = word;
       }
       int h1[8];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) h1[k] = hb[256 * k];
+      for (int q = 0; q < 4; ++q) {
+        const int other = __shfl_xor(mine[q], 1);
+        h1[q] = half ? other : mine[q];
+        h1[4 + q] = half ? mine[q] : other;
+      }
+      // layer 2: two output words per lane
+      int mine2[2];
 #pragma unroll 1
-      for (int jg = 0; jg < 4; ++jg) {
+      for (int q = 0; q < 2; ++q) {
         int word = 0;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const int j = jg * 4 + jj;
+          const int j = (2 * half + q) * 4 + jj;
           int acc = 0;
           const int *w = &w2[j * 8];
 #pragma unroll
@@ -190,27 +206,34 @@ __global__ __launch_bounds__(256) void k_selector_head(hv_selector_dev p, const 
           const int v = sel_gelu(acc, bb2[j], fast, r2a, r2b, s2_in, s2_out);
           word |= (v & 0xFF) << (8 * jj);
         }
-        hb[256 * (8 + jg)] = word;
+        mine2[q] = word;
       }
       int h2[4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) h2[k] = hb[256 * (8 + k)];
-      int qv[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        int acc = 0;
-        const int *w = &w3[j * 4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) acc = dot4(h2[k], w[k], acc);
-        const int logit = (int)requant_shift((i64)acc + p.b3[h * 2 + j], s3, 8);
-        qv[j] = (int)requant_shift(logit, sq, 24);
+      for (int q = 0; q < 2; ++q) {
+        const int other = __shfl_xor(mine2[q], 1);
+        h2[q] = half ? other : mine2[q];
+        h2[2 + q] = half ? mine2[q] : other;
       }
+      // layer 3: logit `half` here, the other by shuffle
+      int acc = 0;
+      const int *w = &w3[half * 4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc = dot4(h2[k], w[k], acc);
+      const int logit = (int)requant_shift((i64)acc + p.b3[h * 2 + half], s3, 8);
+      const int qmine = (int)requant_shift(logit, sq, 24);
+      const int qother = __shfl_xor(qmine, 1);
+      int qv[2];
+      qv[0] = half ? qother : qmine;
+      qv[1] = half ? qmine : qother;
       const int mx = qv[0] > qv[1] ? qv[0] : qv[1];
       const unsigned e0 = softmax_exp(qv[0] - mx), e1 = softmax_exp(qv[1] - mx);
       const unsigned ratio = softmax_ratio(e1, softmax_recip24(e0 + e1));
       const int hsv = (int)(ratio > 65536u ? 65536u : ratio);
-      hs_out[((size_t)b * 3 + h) * kMaxCand + c] = hsv;
-      if (ck.head_scores) ck.head_scores[((size_t)b * 3 + h) * kMaxCand + c] = hsv;
+      if (half == 0) {
+        hs_out[((size_t)b * 3 + h) * kMaxCand + c] = hsv;
+        if (ck.head_scores) ck.head_scores[((size_t)b * 3 + h) * kMaxCand + c] = hsv;
+      }
     }
   }
 }
@@ -418,7 +441,7 @@ int launch_selector(const SelectorArgs &a, hipStream_t s) {
     const int fast = in(-16 - (p.in_exp + p.local_w_exp)) && in(p.local_out_exp + 16) &&
                      in(-16 - (p.concat_out_exp + p.score_w1_exp)) && in(p.h1_out_exp + 16) &&
                      in(-16 - (p.h1_out_exp + p.score_w2_exp)) && in(p.h2_out_exp + 16);
-    hv_launch(k_selector_head, dim3(a.batch * 3), dim3(256), 0, s, p, a.tokens,
+    hv_launch(k_selector_head, dim3(a.batch * 3), dim3(kHeadThreads), 0, s, p, a.tokens,
                        a.offsets, a.pkg_in, a.hs, a.stats, fast, a.ck);
     if ((rc = check_hip(hipGetLastError(), "k_selector_head launch"))) return rc;
   }
