@@ -21,6 +21,8 @@
 // GELU layers use the int32 requant/GELU path when the host finds every
 // shift in [-30, 30] and each layer's biases satisfy |b| <= 2^30 - 1 -
 // K*2^14 (checked per workgroup, uniform); otherwise the exact 64-bit form.
+#include <type_traits>
+
 #include "hv_device.h"
 #include "hv_internal.h"
 
@@ -94,42 +96,48 @@ __global__ __launch_bounds__(kHeadThreads) void k_selector_head(hv_selector_dev 
   {
     const int sh_in = -16 - (p.in_exp + p.local_w_exp), sh_out = p.local_out_exp + 16;
     const Rq ra = rq_setup(sh_in, -(1 << 23), (1 << 23) - 1), rb = rq_setup(sh_out, -128, 127);
-    const int half = tid & 1;
-    for (int c = tid >> 1; c < C; c += kHeadThreads / 2) {
-      int x[16];
-      const v4i *src = reinterpret_cast<const v4i *>(cand + (size_t)c * 192 + h * 64);
+    // LPC lanes per candidate: four when the candidates fit (shorter
+    // chains), else two.
+    auto stage1 = [&](auto lpc) {
+      constexpr int LPC = decltype(lpc)::value, WPL = 8 / LPC;  // output words per lane
+      const int sub = tid & (LPC - 1);
+      for (int c = tid / LPC; c < C; c += kHeadThreads / LPC) {
+        int x[16];
+        const v4i *src = reinterpret_cast<const v4i *>(cand + (size_t)c * 192 + h * 64);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const v4i v = src[k];
-        x[4 * k] = v[0]; x[4 * k + 1] = v[1]; x[4 * k + 2] = v[2]; x[4 * k + 3] = v[3];
-      }
-      if (half == 0) {
-        int lane_sum = 0;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) lane_sum = dot4(x[k], 0x01010101, lane_sum);
-        const int8_t stat = (int8_t)sat_bits(round_div_pos(lane_sum, 64), 8);
-        stats_out[((size_t)b * kMaxCand + c) * 3 + h] = stat;
-        if (ck.head_stats) ck.head_stats[((size_t)b * kMaxCand + c) * 3 + h] = stat;
-      }
-      // this lane: output words 4*half .. 4*half + 3 (channels 16*half ..)
-#pragma unroll 1
-      for (int jg = 4 * half; jg < 4 * half + 4; ++jg) {
-        int word = 0;
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int j = jg * 4 + jj;
-          int acc = 0;
-          const int *w = &wl[j * 16];
-#pragma unroll
-          for (int k = 0; k < 16; ++k) acc = dot4(x[k], w[k], acc);
-          const int v = sel_gelu(acc, bl[j], fast, ra, rb, sh_in, sh_out);
-          word |= (v & 0xFF) << (8 * jj);
+        for (int k = 0; k < 4; ++k) {
+          const v4i v = src[k];
+          x[4 * k] = v[0]; x[4 * k + 1] = v[1]; x[4 * k + 2] = v[2]; x[4 * k + 3] = v[3];
         }
-        local_s[c * 8 + jg] = word;
-        if (ck.local)
-          reinterpret_cast<int *>(ck.local + (((size_t)b * 3 + h) * kMaxCand + c) * 32)[jg] = word;
+        if (sub == 0) {
+          int lane_sum = 0;
+#pragma unroll
+          for (int k = 0; k < 16; ++k) lane_sum = dot4(x[k], 0x01010101, lane_sum);
+          const int8_t stat = (int8_t)sat_bits(round_div_pos(lane_sum, 64), 8);
+          stats_out[((size_t)b * kMaxCand + c) * 3 + h] = stat;
+          if (ck.head_stats) ck.head_stats[((size_t)b * kMaxCand + c) * 3 + h] = stat;
+        }
+#pragma unroll 1
+        for (int jg = WPL * sub; jg < WPL * sub + WPL; ++jg) {
+          int word = 0;
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int j = jg * 4 + jj;
+            int acc = 0;
+            const int *w = &wl[j * 16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) acc = dot4(x[k], w[k], acc);
+            const int v = sel_gelu(acc, bl[j], fast, ra, rb, sh_in, sh_out);
+            word |= (v & 0xFF) << (8 * jj);
+          }
+          local_s[c * 8 + jg] = word;
+          if (ck.local)
+            reinterpret_cast<int *>(ck.local + (((size_t)b * 3 + h) * kMaxCand + c) * 32)[jg] = word;
+        }
       }
-    }
+    };
+    if (C <= kHeadThreads / 4) stage1(std::integral_constant<int, 4>{});
+    else stage1(std::integral_constant<int, 2>{});
   }
   __syncthreads();
   // Stage 2: global feature = sat8(round_div(sum_c local, C)); sixteen
@@ -160,81 +168,83 @@ __global__ __launch_bounds__(kHeadThreads) void k_selector_head(hv_selector_dev 
     const int sq = -16 - p.logits_out_exp;
     const Rq r1a = rq_setup(s1_in, -(1 << 23), (1 << 23) - 1), r1b = rq_setup(s1_out, -128, 127);
     const Rq r2a = rq_setup(s2_in, -(1 << 23), (1 << 23) - 1), r2b = rq_setup(s2_out, -128, 127);
-    const int half = tid & 1;
-    for (int c = tid >> 1; c < C; c += kHeadThreads / 2) {
-      int lg[16];
+    auto stage3 = [&](auto lpc) {
+      constexpr int LPC = decltype(lpc)::value;
+      constexpr int W1 = 8 / LPC, W2 = 4 / LPC;  // layer-1 / layer-2 words per lane
+      const int sub = tid & (LPC - 1), base = (tid & 63) & ~(LPC - 1);
+      for (int c = tid / LPC; c < C; c += kHeadThreads / LPC) {
+        int lg[16];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) lg[k] = local_s[c * 8 + k];
+        for (int k = 0; k < 8; ++k) lg[k] = local_s[c * 8 + k];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) lg[8 + k] = glob[k];
-      // layer 1: this lane's four output words, the partner's by shuffle
-      int mine[4];
+        for (int k = 0; k < 8; ++k) lg[8 + k] = glob[k];
+        // layer 1: this lane's output words, the group's others by shuffle
+        int mine[W1];
 #pragma unroll 1
-      for (int q = 0; q < 4; ++q) {
-        int word = 0;
+        for (int q = 0; q < W1; ++q) {
+          int word = 0;
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int j = (4 * half + q) * 4 + jj;
-          int acc = 0;
-          const int *w = &w1[j * 16];
+          for (int jj = 0; jj < 4; ++jj) {
+            const int j = (W1 * sub + q) * 4 + jj;
+            int acc = 0;
+            const int *w = &w1[j * 16];
 #pragma unroll
-          for (int k = 0; k < 16; ++k) acc = dot4(lg[k], w[k], acc);
-          const int v = sel_gelu(acc, bb1[j], fast, r1a, r1b, s1_in, s1_out);
-          word |= (v & 0xFF) << (8 * jj);
+            for (int k = 0; k < 16; ++k) acc = dot4(lg[k], w[k], acc);
+            const int v = sel_gelu(acc, bb1[j], fast, r1a, r1b, s1_in, s1_out);
+            word |= (v & 0xFF) << (8 * jj);
+          }
+          mine[q] = word;
         }
-        mine[q] = word;
-      }
-      int h1[8];
+        int h1[8];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int other = __shfl_xor(mine[q], 1);
-        h1[q] = half ? other : mine[q];
-        h1[4 + q] = half ? mine[q] : other;
-      }
-      // layer 2: two output words per lane
-      int mine2[2];
+        for (int o = 0; o < LPC; ++o)
+#pragma unroll
+          for (int q = 0; q < W1; ++q) h1[o * W1 + q] = __shfl(mine[q], base + o);
+        // layer 2
+        int mine2[W2];
 #pragma unroll 1
-      for (int q = 0; q < 2; ++q) {
-        int word = 0;
+        for (int q = 0; q < W2; ++q) {
+          int word = 0;
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int j = (2 * half + q) * 4 + jj;
-          int acc = 0;
-          const int *w = &w2[j * 8];
+          for (int jj = 0; jj < 4; ++jj) {
+            const int j = (W2 * sub + q) * 4 + jj;
+            int acc = 0;
+            const int *w = &w2[j * 8];
 #pragma unroll
-          for (int k = 0; k < 8; ++k) acc = dot4(h1[k], w[k], acc);
-          const int v = sel_gelu(acc, bb2[j], fast, r2a, r2b, s2_in, s2_out);
-          word |= (v & 0xFF) << (8 * jj);
+            for (int k = 0; k < 8; ++k) acc = dot4(h1[k], w[k], acc);
+            const int v = sel_gelu(acc, bb2[j], fast, r2a, r2b, s2_in, s2_out);
+            word |= (v & 0xFF) << (8 * jj);
+          }
+          mine2[q] = word;
         }
-        mine2[q] = word;
-      }
-      int h2[4];
+        int h2[4];
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const int other = __shfl_xor(mine2[q], 1);
-        h2[q] = half ? other : mine2[q];
-        h2[2 + q] = half ? mine2[q] : other;
-      }
-      // layer 3: logit `half` here, the other by shuffle
-      int acc = 0;
-      const int *w = &w3[half * 4];
+        for (int o = 0; o < LPC; ++o)
 #pragma unroll
-      for (int k = 0; k < 4; ++k) acc = dot4(h2[k], w[k], acc);
-      const int logit = (int)requant_shift((i64)acc + p.b3[h * 2 + half], s3, 8);
-      const int qmine = (int)requant_shift(logit, sq, 24);
-      const int qother = __shfl_xor(qmine, 1);
-      int qv[2];
-      qv[0] = half ? qother : qmine;
-      qv[1] = half ? qmine : qother;
-      const int mx = qv[0] > qv[1] ? qv[0] : qv[1];
-      const unsigned e0 = softmax_exp(qv[0] - mx), e1 = softmax_exp(qv[1] - mx);
-      const unsigned ratio = softmax_ratio(e1, softmax_recip24(e0 + e1));
-      const int hsv = (int)(ratio > 65536u ? 65536u : ratio);
-      if (half == 0) {
-        hs_out[((size_t)b * 3 + h) * kMaxCand + c] = hsv;
-        if (ck.head_scores) ck.head_scores[((size_t)b * 3 + h) * kMaxCand + c] = hsv;
+          for (int q = 0; q < W2; ++q) h2[o * W2 + q] = __shfl(mine2[q], base + o);
+        // layer 3: logit (sub & 1) here; the group's first two lanes hold both
+        const int lj = sub & 1;
+        int acc = 0;
+        const int *w = &w3[lj * 4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc = dot4(h2[k], w[k], acc);
+        const int logit = (int)requant_shift((i64)acc + p.b3[h * 2 + lj], s3, 8);
+        const int qmine = (int)requant_shift(logit, sq, 24);
+        int qv[2];
+        qv[0] = __shfl(qmine, base);
+        qv[1] = __shfl(qmine, base + 1);
+        const int mx = qv[0] > qv[1] ? qv[0] : qv[1];
+        const unsigned e0 = softmax_exp(qv[0] - mx), e1 = softmax_exp(qv[1] - mx);
+        const unsigned ratio = softmax_ratio(e1, softmax_recip24(e0 + e1));
+        const int hsv = (int)(ratio > 65536u ? 65536u : ratio);
+        if (sub == 0) {
+          hs_out[((size_t)b * 3 + h) * kMaxCand + c] = hsv;
+          if (ck.head_scores) ck.head_scores[((size_t)b * 3 + h) * kMaxCand + c] = hsv;
+        }
       }
-    }
+    };
+    if (C <= kHeadThreads / 4) stage3(std::integral_constant<int, 4>{});
+    else stage3(std::integral_constant<int, 2>{});
   }
 }
 
