@@ -16,7 +16,8 @@ G_so is a step function of q with a few hundred changes.  Table layout
       K = 3: two words per entry,
         word 0: T[0:8] B1[8:17] D1[17:24]
         word 1: B2[0:9] D2[9:16] B3[16:25] D3[25:32].
-  G is constant for q <= qlo and for q >= qhi.  s2 is the largest value in
+  G is constant for q <= qlo and for q >= qhi.  Each table is padded to a
+  multiple of four words, so tables start on 16-byte boundaries.  s2 is the largest value in
   [0, 9] that leaves at most K changes inside every entry of the bucket.
   Each so gets the one-change form when that table fits in 32 KB (fewer
   operations per lookup), the three-change form otherwise (a smaller table
@@ -149,21 +150,26 @@ def main(out):
         if not np.array_equal(lookup(qlo, qhi, l1, l2, q, K), o):
             raise RuntimeError(f"so={so}: table lookup differs from the post-op")
         n1e = len(l1) + (len(l1) & 1)
-        info.append((qlo, qhi, n1e, len(l2) // (2 if K == 3 else 1), len(words), K))
-        words += list(l1) + [0] * (n1e - len(l1)) + list(l2)
+        body = list(l1) + [0] * (n1e - len(l1)) + list(l2)
+        body += [0] * (-len(body) % 4)          # 16-byte multiples
+        info.append((qlo, qhi, n1e, len(l2) // (2 if K == 3 else 1), len(words), K, len(body)))
+        words += body
     lines = [
         "// Generated by gen_gelu_lut.py: step tables of",
         "// sat8(round_shift_away(gelu(q), so)) for so in "
         f"[{SO_MIN}, {SO_MAX}] (layout in the generator).",
         "namespace hv {",
         f"constexpr int kGeluLutSoMin = {SO_MIN}, kGeluLutSoMax = {SO_MAX};",
-        "// n2 entries of k words (k = 1 or 3 changes per entry: 1 or 2 words)",
-        "struct GeluLutInfo { int qlo, qhi, n1e, n2, off, k; };",
+        "// n2 entries of k words (k = 1 or 3 changes per entry: 1 or 2 words);",
+        "// a table is `words` words from `off`, both multiples of 4",
+        "struct GeluLutInfo { int qlo, qhi, n1e, n2, off, k, words; };",
         "constexpr GeluLutInfo kGeluLutInfo[] = {",
     ]
-    lines += [f"  {{{a}, {b}, {c}, {d}, {e}, {k}}}," for a, b, c, d, e, k in info]
+    lines += [f"  {{{', '.join(str(v) for v in t)}}}," for t in info]
+    max_words = max(t[-1] for t in info)
     lines += ["};", f"constexpr int kGeluLutWords = {len(words)};",
-              "__device__ const unsigned kGeluLut[kGeluLutWords] = {"]
+              f"constexpr int kGeluLutMaxWords = {max_words};",
+              "__device__ const unsigned kGeluLut[kGeluLutWords] __attribute__((aligned(16))) = {"]
     for i in range(0, len(words), 8):
         lines.append("  " + " ".join(f"0x{int(w):08x}u," for w in words[i:i + 8]))
     lines += ["};", "}  // namespace hv", ""]

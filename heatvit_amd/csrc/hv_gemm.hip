@@ -103,8 +103,23 @@ __device__ __forceinline__ int gelu_lut(int q, const unsigned *lut, int qhi, con
 }
 
 // Stages the launch's GELU step table in LDS (all threads, then a barrier).
+// Copies the launch's step table into LDS with 16-byte loads, four rounds
+// of loads in flight before their LDS writes (one L2 latency per 16 KB, not
+// one per word).  Tables start on 16-byte boundaries and hold a multiple of
+// four words; blockDim.x is 256.
 __device__ __forceinline__ void stage_lut(const GemmArgs &g, unsigned *lut) {
-  for (int i = threadIdx.x; i < g.lut_words; i += blockDim.x) lut[i] = kGeluLut[g.lut_off + i];
+  const v4i *src = reinterpret_cast<const v4i *>(kGeluLut + g.lut_off);
+  v4i *dst = reinterpret_cast<v4i *>(lut);
+  const int n4 = g.lut_words >> 2;
+  for (int base = threadIdx.x; base < n4; base += 1024) {
+    v4i v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = src[min(base + r * 256, n4 - 1)];
+    // Lanes past the end rewrite the last vector with its own value, so
+    // no write is predicated and no load sinks behind one.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dst[min(base + r * 256, n4 - 1)] = v[r];
+  }
   __syncthreads();
 }
 
@@ -701,7 +716,7 @@ int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
     const GeluLutInfo &t = kGeluLutInfo[g.shift_b - kGeluLutSoMin];
     g.lut_off = t.off;
     g.lut_k = t.k;
-    g.lut_words = t.n1e + (t.k == 1 ? 1 : 2) * t.n2;
+    g.lut_words = t.words;
     g.lut_n1e = t.n1e;
     g.lut_qlo = t.qlo;
     g.lut_qhi = t.qhi;
@@ -748,7 +763,7 @@ int launch_gelu_post(bool table, const int64_t *in, int64_t *out, int64_t n, int
     const GeluLutInfo &t = kGeluLutInfo[so - kGeluLutSoMin];
     g.lut_off = t.off;
     g.lut_k = t.k;
-    g.lut_words = t.n1e + (t.k == 1 ? 1 : 2) * t.n2;
+    g.lut_words = t.words;
     g.lut_n1e = t.n1e;
     g.lut_qlo = t.qlo;
     g.lut_qhi = t.qhi;
