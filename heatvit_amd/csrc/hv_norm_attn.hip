@@ -116,18 +116,26 @@ __global__ __launch_bounds__(256) void k_layernorm32(const int8_t *__restrict__ 
                                                      int rows, const int32_t *rows_dev,
                                                      uint8_t *neg_var, LnWarn lw) {
   const int sub = threadIdx.x & 7;
-  const int R = rows_dev ? min(*rows_dev, rows) : rows;
-  int gm[6], bt[6];
-  ln32_params(ln, sub, gm, bt);
-  for (int row = blockIdx.x * 32 + (threadIdx.x >> 3); row < R; row += gridDim.x * 32) {
+  auto load_row = [&](int row, int (&w)[6]) {
     const int2 *xr = reinterpret_cast<const int2 *>(x + (size_t)row * 192 + sub * 24);
-    int w[6], out[6];
 #pragma unroll
     for (int q = 0; q < 3; ++q) {
       const int2 v = xr[q];
       w[2 * q] = v.x;
       w[2 * q + 1] = v.y;
     }
+  };
+  // The first row, gamma and beta are loaded before the device row count
+  // arrives (the buffers hold `rows` rows), so the loads overlap.
+  int row = blockIdx.x * 32 + (threadIdx.x >> 3);
+  int w[6] = {0, 0, 0, 0, 0, 0};
+  if (row < rows) load_row(row, w);
+  int gm[6], bt[6];
+  ln32_params(ln, sub, gm, bt);
+  const int R = rows_dev ? min(*rows_dev, rows) : rows;
+  for (; row < R; row += gridDim.x * 32) {
+    int out[6];
+    if (row != blockIdx.x * 32 + (int)(threadIdx.x >> 3)) load_row(row, w);
     const bool neg = ln32_row(w, gm, bt, ln, out);
     int2 *yr = reinterpret_cast<int2 *>(ln.out + (size_t)row * 192 + sub * 24);
 #pragma unroll

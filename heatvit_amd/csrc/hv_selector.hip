@@ -285,14 +285,16 @@ __device__ int fuse_candidate(const hv_selector_dev &p, const int8_t *stats, con
 // Optional head fuse, then the stable keep list of the normal candidates
 // (fused >= 32768, input order) and the per-image state {token_count,
 // package_present, kept, pruned, warnings} (selector.py:456-500).  One
-// wavefront per image.
-__global__ __launch_bounds__(64) void k_selector_keep(const int32_t *offsets,
-                                                      const uint8_t *pkg_in, int32_t *fused,
-                                                      int32_t *kept_index, int32_t *state,
-                                                      hv_selector_dev p, const int32_t *hs,
-                                                      const int8_t *stats, int32_t *weights_ck,
-                                                      int32_t *img_warn) {
-  const int b = blockIdx.x, lane = threadIdx.x;
+// workgroup per image, one thread per candidate (at most 196).
+__global__ __launch_bounds__(256) void k_selector_keep(const int32_t *offsets,
+                                                       const uint8_t *pkg_in, int32_t *fused,
+                                                       int32_t *kept_index, int32_t *state,
+                                                       hv_selector_dev p, const int32_t *hs,
+                                                       const int8_t *stats, int32_t *weights_ck,
+                                                       int32_t *img_warn) {
+  __shared__ int w_kept[4], w_warn[4];
+  __shared__ i64 w_den[4];
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int C = offsets[b + 1] - offsets[b] - 1;
   const int pkg = pkg_in ? (pkg_in[b] ? 1 : 0) : 0;
   int32_t *st = state + (size_t)b * 5;
@@ -300,56 +302,64 @@ __global__ __launch_bounds__(64) void k_selector_keep(const int32_t *offsets,
     // token_selector needs CLS plus one candidate (selector.py:513-514) and
     // an incoming package needs a normal candidate beside it (:448-449);
     // the state's token count -1 reports the ValueError.
-    if (lane == 0) { st[0] = -1; st[1] = 0; st[2] = 0; st[3] = 0; st[4] = 0; }
+    if (tid == 0) { st[0] = -1; st[1] = 0; st[2] = 0; st[3] = 0; st[4] = 0; }
     return;
   }
   int32_t *f = fused + (size_t)b * kMaxCand;
   const int n_norm = C - pkg;
-  int kept = 0;
-  i64 den = 0;
-  bool warn_any = false;
-  for (int base = 0; base < C; base += 64) {
-    const int c = base + lane;
-    const bool in = c < C;
-    int fc = 0;
-    if (hs) {
-      if (in) {
-        bool warn = false;
-        fc = fuse_candidate(p, stats + ((size_t)b * kMaxCand + c) * 3,
-                            hs + (size_t)b * 3 * kMaxCand + c, C, c,
-                            weights_ck ? weights_ck + ((size_t)b * kMaxCand + c) * 3 : nullptr,
-                            &warn);
-        warn_any = warn_any || warn;
-        f[c] = fc;
-      }
-    } else {
-      fc = in ? f[c] : 0;
+  const int c = tid;
+  const bool in = c < C;
+  int fc = 0;
+  bool warn = false;
+  if (hs) {
+    if (in) {
+      fc = fuse_candidate(p, stats + ((size_t)b * kMaxCand + c) * 3,
+                          hs + (size_t)b * 3 * kMaxCand + c, C, c,
+                          weights_ck ? weights_ck + ((size_t)b * kMaxCand + c) * 3 : nullptr,
+                          &warn);
+      f[c] = fc;
     }
-    const bool is_norm = c < n_norm;
-    const bool keep = is_norm && fc >= 32768;
-    const bool part = (is_norm && !keep) || (pkg && c == C - 1);
-    const u64 mask = __ballot(keep);
-    const int before = __popcll(mask & ((1ull << lane) - 1ull));
-    if (keep) kept_index[(size_t)b * kMaxCand + kept + before] = c;
-    kept += __popcll(mask);
-    i64 d = part ? fc : 0;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) d += __shfl_xor(d, off);
-    den += d;
+  } else {
+    fc = in ? f[c] : 0;
   }
-  for (int i = kept + lane; i < kMaxCand; i += 64) kept_index[(size_t)b * kMaxCand + i] = -1;
-  const bool warn_head = __ballot(warn_any) != 0;
+  const bool is_norm = c < n_norm;
+  const bool keep = is_norm && fc >= 32768;
+  const bool part = (is_norm && !keep) || (pkg && c == C - 1);
+  const u64 mask = __ballot(keep);
+  i64 d = part ? fc : 0;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) d += __shfl_xor(d, off);
+  const bool warn_wave = __ballot(warn) != 0;
   if (lane == 0) {
+    w_kept[wave] = __popcll(mask);
+    w_den[wave] = d;
+    w_warn[wave] = warn_wave;
+  }
+  __syncthreads();
+  int before = __popcll(mask & ((1ull << lane) - 1ull)), kept = 0;
+  i64 den = 0;
+  bool warn_head = false;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    before += w < wave ? w_kept[w] : 0;
+    kept += w_kept[w];
+    den += w_den[w];
+    warn_head = warn_head || w_warn[w];
+  }
+  int32_t *ki = kept_index + (size_t)b * kMaxCand;
+  if (keep) ki[before] = c;
+  if (c >= kept && c < kMaxCand) ki[c] = -1;
+  if (tid == 0) {
     const int n_part = C - kept;  // pruned normals + the incoming package
     const int exists = n_part > 0;
     st[0] = 1 + kept + exists;
     st[1] = exists;
     st[2] = kept;
     st[3] = n_part - pkg;
-    const int warn = (warn_head ? HV_WARN_HEAD_DEN_ZERO : 0) |
-                     ((exists && den == 0) ? HV_WARN_PACKAGE_DEN_ZERO : 0);
-    st[4] = warn;
-    if (img_warn) img_warn[b] |= warn;
+    const int warn_bits = (warn_head ? HV_WARN_HEAD_DEN_ZERO : 0) |
+                          ((exists && den == 0) ? HV_WARN_PACKAGE_DEN_ZERO : 0);
+    st[4] = warn_bits;
+    if (img_warn) img_warn[b] |= warn_bits;
   }
 }
 
@@ -357,22 +367,28 @@ __global__ __launch_bounds__(256) void k_selector_compact(
     const int8_t *tokens, const int32_t *offsets, const uint8_t *pkg_in, int batch,
     const int32_t *fused, const int32_t *kept_index, const int32_t *state, int8_t *out,
     int32_t *out_offsets, uint8_t *pkg_out, int32_t *token_counts, int stage) {
-  __shared__ int red[256];
-  __shared__ long long den_s;
-  const int b = blockIdx.x, tid = threadIdx.x;
-  int s = 0;
-  for (int i = tid; i < b; i += 256) s += max(state[(size_t)i * 5], 0);
-  red[tid] = s;
-  __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if (tid < w) red[tid] += red[tid + w];
-    __syncthreads();
-  }
-  const int out0 = red[0];
+  __shared__ int red[4];
+  __shared__ i64 den_part[4];
+  __shared__ int wgt[kMaxCand];
+  __shared__ int part_sum[21 * 192];
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int32_t *st = state + (size_t)b * 5;
   const int count = st[0], exists = st[1], kept = st[2];
   const int row0 = offsets[b], C = offsets[b + 1] - row0 - 1;
   const int pkg = pkg_in ? (pkg_in[b] ? 1 : 0) : 0;
+  // Source row of output row r is row0 + 1 + src_k[r]: -1 for the CLS row,
+  // then the kept candidates.
+  __shared__ int src_k[kMaxCand + 1];
+  const int *ki = kept_index + (size_t)b * kMaxCand;
+  if (tid <= kMaxCand) src_k[tid] = tid == 0 ? -1 : ki[tid - 1];
+  // Output row of this image: the token counts of the images before it.
+  int s = 0;
+  for (int i = tid; i < b; i += 256) s += max(state[(size_t)i * 5], 0);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  const int out0 = red[0] + red[1] + red[2] + red[3];
   if (tid == 0) {
     out_offsets[b] = out0;
     if (b == batch - 1) out_offsets[batch] = out0 + (count > 0 ? count : 0);
@@ -380,51 +396,62 @@ __global__ __launch_bounds__(256) void k_selector_compact(
     if (token_counts) token_counts[(size_t)b * 4 + stage] = count;
   }
   if (count <= 0) return;
-  // CLS and kept rows, 16 bytes per thread step.
-  const int *ki = kept_index + (size_t)b * kMaxCand;
-  for (int i = tid; i < (1 + kept) * 12; i += 256) {
-    const int r = i / 12, chunk = i - r * 12;
-    const int src = r == 0 ? row0 : row0 + 1 + ki[r - 1];
-    reinterpret_cast<v4i *>(out + (size_t)(out0 + r) * 192)[chunk] =
-        reinterpret_cast<const v4i *>(tokens + (size_t)src * 192)[chunk];
+  // CLS and kept rows, 16 bytes per item; four items per thread in flight
+  // (items past the end repeat the last one, so no copy is predicated).
+  const int n_items = (1 + kept) * 12;
+  for (int base = tid; base < n_items; base += 1024) {
+    v4i v[4];
+    int dst[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = min(base + j * 256, n_items - 1), r = i / 12, chunk = i - r * 12;
+      v[j] = reinterpret_cast<const v4i *>(tokens + (size_t)(row0 + 1 + src_k[r]) * 192)[chunk];
+      dst[j] = (out0 + r) * 12 + chunk;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) reinterpret_cast<v4i *>(out)[dst[j]] = v[j];
   }
   if (!exists) return;
   // Package row: num[ch] = sum over partitioned candidates of w_c * x_c[ch]
   // with w_c = fused score (or 1 when the scores sum to zero).  |num| <=
   // 196 * 65536 * 128 < 2^31.  Thread (channel group of 16, candidate
-  // group g) accumulates candidates g, g + 21, ...; LDS sums the groups.
+  // group g) accumulates candidates g, g + 21, ... (all of its candidate
+  // rows loaded at once, weight 0 for kept ones); LDS sums the groups.
+  constexpr int kSteps = (kMaxCand + 20) / 21;
+  const int cg = tid / 12, chg = tid - cg * 12;
+  v4i xv[kSteps];
+  if (tid < 12 * 21) {
+    const int8_t *cand = tokens + (size_t)(row0 + 1) * 192 + chg * 16;
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j)
+      xv[j] = *reinterpret_cast<const v4i *>(cand + (size_t)min(cg + 21 * j, C - 1) * 192);
+  }
   const int32_t *f = fused + (size_t)b * kMaxCand;
   const int n_norm = C - pkg;
-  __shared__ int wgt[kMaxCand];
-  __shared__ int part_sum[21 * 192];
-  if (tid < 64) {
-    long long d = 0;
-    for (int c = tid; c < C; c += 64) {
-      const bool part = (c < n_norm && f[c] < 32768) || (pkg && c == C - 1);
-      d += part ? f[c] : 0;
-    }
-    for (int off = 32; off > 0; off >>= 1) d += __shfl_xor(d, off);
-    if (tid == 0) den_s = d;
+  int fv = 0;
+  bool part = false;
+  if (tid < C) {
+    fv = f[tid];
+    part = (tid < n_norm && fv < 32768) || (pkg && tid == C - 1);
   }
+  i64 d = part ? fv : 0;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) d += __shfl_xor(d, off);
+  if (lane == 0) den_part[wave] = d;
   __syncthreads();
-  const long long den = den_s;
-  for (int c = tid; c < C; c += 256) {
-    const bool part = (c < n_norm && f[c] < 32768) || (pkg && c == C - 1);
-    wgt[c] = part ? (den == 0 ? 1 : f[c]) : 0;
-  }
+  const i64 den = den_part[0] + den_part[1] + den_part[2] + den_part[3];
+  if (tid < C) wgt[tid] = part ? (den == 0 ? 1 : fv) : 0;
   __syncthreads();
   if (tid < 12 * 21) {
-    const int cg = tid / 12, chg = tid - cg * 12;
     int acc[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc[j] = 0;
-    const int8_t *cand = tokens + (size_t)(row0 + 1) * 192 + chg * 16;
-    for (int c = cg; c < C; c += 21) {
-      const int w = wgt[c];
-      if (w == 0) continue;
-      const v4i v = *reinterpret_cast<const v4i *>(cand + (size_t)c * 192);
 #pragma unroll
-      for (int j = 0; j < 16; ++j) acc[j] += w * (int)(int8_t)(v[j >> 2] >> (8 * (j & 3)));
+    for (int j = 0; j < kSteps; ++j) {
+      const int c = cg + 21 * j;
+      const int w = c < C ? wgt[c] : 0;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) acc[k] += w * (int)(int8_t)(xv[j][k >> 2] >> (8 * (k & 3)));
     }
 #pragma unroll
     for (int j = 0; j < 16; ++j) part_sum[cg * 192 + chg * 16 + j] = acc[j];
@@ -455,7 +482,7 @@ int launch_selector(const SelectorArgs &a, hipStream_t s) {
                        a.offsets, a.pkg_in, a.hs, a.stats, fast, a.ck);
     if ((rc = check_hip(hipGetLastError(), "k_selector_head launch"))) return rc;
   }
-  hv_launch(k_selector_keep, dim3(a.batch), dim3(64), 0, s, a.offsets, a.pkg_in,
+  hv_launch(k_selector_keep, dim3(a.batch), dim3(256), 0, s, a.offsets, a.pkg_in,
                      a.fused, a.kept_index, a.state, p, a.p ? a.hs : nullptr,
                      a.p ? a.stats : nullptr, a.p ? a.ck.head_weights : nullptr, a.img_warn);
   if ((rc = check_hip(hipGetLastError(), "k_selector_keep launch"))) return rc;
