@@ -93,6 +93,70 @@ class Engine:
         return self.logits[:b], self.token_counts[:b], state, self.warnings[:b]
 
 
+@dataclass(frozen=True)
+class Ticket:
+    """One submitted batch: device views of its outputs (logits,
+    token_counts, selector state, warnings), the event recorded after its
+    forward and the stream it runs on."""
+    outputs: tuple
+    done: torch.cuda.Event
+    stream: torch.cuda.Stream
+
+    def wait(self):
+        """Orders the caller's current stream after this batch's forward."""
+        torch.cuda.current_stream(self.stream.device).wait_event(self.done)
+        return self.outputs
+
+    def synchronize(self):
+        """Blocks the host until this batch's forward has finished."""
+        self.done.synchronize()
+        return self.outputs
+
+
+class Pipeline:
+    """Up to `depth` batches in flight at once, each slot with its own
+    workspace and outputs on its own HIP stream (default priority), over one
+    shared device model.  Forwards of different batches are independent, so
+    the GPU overlaps one batch's latency-bound stages (the small pruned
+    blocks, the selectors) with another batch's wide GEMMs.
+
+    submit(images) enqueues a forward after the work already queued on the
+    caller's current stream (so the images and any reads of the slot's
+    previous outputs queued there come first) and returns a Ticket.  A
+    ticket's outputs stay valid until `depth` later submissions reuse its
+    slot; readers on other streams must order themselves after
+    `ticket.done`.  Every slot computes exactly what Engine.forward does."""
+
+    def __init__(self, params, max_batch, depth=3, device="cuda"):
+        if depth < 1:
+            raise ValueError("pipeline depth must be at least 1")
+        model = params if hasattr(params, "struct") else DeviceModel(params, device)
+        self.model = model
+        self.engines = [Engine(model, max_batch, device) for _ in range(depth)]
+        self.streams = [torch.cuda.Stream(device=model.device) for _ in range(depth)]
+        self._next = 0
+
+    @property
+    def depth(self):
+        return len(self.engines)
+
+    def submit(self, images, ckpt=None, ckpt_rows=None):
+        i = self._next
+        self._next = (i + 1) % len(self.engines)
+        s = self.streams[i]
+        s.wait_stream(torch.cuda.current_stream(images.device))
+        with torch.cuda.stream(s):
+            outputs = self.engines[i].forward(images, ckpt, ckpt_rows)
+        images.record_stream(s)
+        done = torch.cuda.Event()
+        done.record(s)
+        return Ticket(outputs, done, s)
+
+    def synchronize(self):
+        for s in self.streams:
+            s.synchronize()
+
+
 def _images(images):
     a = np.asarray(images.cpu().numpy() if isinstance(images, torch.Tensor) else images)
     if a.dtype.kind == "f":

@@ -164,3 +164,27 @@ def test_unpruned_control_vs_oracle(oracle):
     assert np.array_equal(r.warnings, warnings)
     assert np.array_equal(r.logits, logits)
     assert (r.token_counts == 197).all()
+
+
+def test_pipeline_slots_match_engine():
+    """Batches in flight on several streams (heatvit_amd.model.Pipeline)
+    give exactly Engine.forward's outputs, including after slots are reused
+    and for inputs produced on the caller's stream just before submit."""
+    import torch
+    from heatvit_amd.model import Engine, Pipeline
+    imgs, params = synth.throughput_workload(40)
+    src = torch.from_numpy(np.ascontiguousarray(imgs.reshape(40, -1))).cuda()
+    eng = Engine(params, 16)
+    cuts = [(0, 16), (16, 23), (23, 39), (5, 14), (24, 40), (0, 1)]
+    want = []
+    for a, b in cuts:
+        lg, tc, st, wn = eng.forward(src[a:b].clone())
+        want.append((lg.cpu().numpy(), tc.cpu().numpy(), st.cpu().numpy(), wn.cpu().numpy()))
+    pipe = Pipeline(eng.model, 16, depth=3)
+    for start in (0, 3):
+        tickets = [pipe.submit(src[a:b].clone()) for a, b in cuts[start:start + 3]]
+        for k, t in enumerate(tickets):
+            got = [x.cpu().numpy() for x in t.synchronize()]
+            for g, w in zip(got, want[start + k]):
+                assert np.array_equal(g, w)
+    pipe.synchronize()
