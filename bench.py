@@ -102,8 +102,10 @@ def main():
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--streams", type=int, default=3,
                     help="batches in flight, each on its own HIP stream (1: one at a time)")
-    ap.add_argument("--cpu-passes", type=int, default=2,
-                    help="passes of the CPU oracle over the whole batch (0 skips it)")
+    ap.add_argument("--cpu-passes", type=int, default=30,
+                    help="most passes of the CPU oracle over the whole batch (0 skips it)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="the CPU oracle stops after the first pass that ends past this time")
     ap.add_argument("--no-control", action="store_true", help="skip the unpruned control")
     ap.add_argument("--no-float", action="store_true",
                     help="skip the float-image front-end measurement")
@@ -273,14 +275,15 @@ def main():
     cpu = None
     if args.cpu_passes > 0:
         threads = min(16, os.cpu_count() or 1)
-        secs = 0.0
-        for _ in range(args.cpu_passes):
+        secs, passes = 0.0, 0
+        while passes < args.cpu_passes and (passes == 0 or secs < args.cpu_seconds):
             _, dt = cpu_baseline(images, params, threads)
             secs += dt
-        n = args.cpu_passes * args.batch
+            passes += 1
+        n = passes * args.batch
         cpu = {"value": round(n / secs, 2), "unit": "images/s", "cores": threads, "kind": "port",
                "sample": f"CPU oracle (oracle/hv_oracle.c, OpenMP, {threads} threads) over the "
-                         f"same {args.batch}-image workload, {args.cpu_passes} passes, "
+                         f"same {args.batch}-image workload, {passes} passes, "
                          f"{secs:.1f} s wall"}
 
     mean_tokens = counts.mean(axis=0).round(2).tolist()

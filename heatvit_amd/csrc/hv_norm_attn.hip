@@ -254,7 +254,13 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
   __shared__ __attribute__((aligned(16))) int8_t Ks[kMaxKeys * kKStride];
   __shared__ __attribute__((aligned(16))) int8_t Vt[64 * kVStride];
 
-  const int b = blockIdx.x / 3, h = blockIdx.x - 3 * (blockIdx.x / 3);
+  // The grid is a multiple of 8 and workgroups go round-robin over the 8
+  // XCDs, so XCD x runs logical items [x*T8, (x+1)*T8): the three heads of
+  // an image share one XCD's L2 and each row of QKV is fetched once.
+  const int T = 3 * g.batch, T8 = (T + 7) >> 3;
+  const int L = (blockIdx.x & 7) * T8 + (blockIdx.x >> 3);
+  if (L >= T) return;
+  const int b = L / 3, h = L - 3 * b;
   const int row0 = g.offsets[b];
   const int N = g.offsets[b + 1] - row0;
   // Images with a token count outside [1, 197] or rows outside the
@@ -414,7 +420,7 @@ int launch_attention(const AttnArgs &a_in, hipStream_t s) {
   a.ctx_fast = a.ctx_shift >= 1 && a.ctx_shift <= 30;
   a.ctx_rnd = a.ctx_fast ? 1 << (a.ctx_shift - 1) : 0;
   const bool ck = a.score || a.prob;
-  const dim3 grid(a.batch * 3), block(256);
+  const dim3 grid((a.batch * 3 + 7) / 8 * 8), block(256);
   if (a.q16_mode == 0 && !ck) hv_launch((k_attention<0, false>), grid, block, 0, s, a);
   else if (a.q16_mode == 0) hv_launch((k_attention<0, true>), grid, block, 0, s, a);
   else if (a.q16_mode == 1 && !ck) hv_launch((k_attention<1, false>), grid, block, 0, s, a);

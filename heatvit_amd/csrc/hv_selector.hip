@@ -48,7 +48,7 @@ __device__ __forceinline__ int sel_gelu(int acc, int bias, bool fast, const Rq &
 constexpr int kHeadThreads = 512;  // two lanes per candidate, kMaxCand <= 256
 
 __global__ __launch_bounds__(kHeadThreads) void k_selector_head(hv_selector_dev p, const int8_t *tokens,
-                                                       const int32_t *offsets,
+                                                       const int32_t *offsets, int batch,
                                                        const uint8_t *pkg_in, int32_t *hs_out,
                                                        int8_t *stats_out, int fast_shifts,
                                                        hv_selector_ckpt ck) {
@@ -61,7 +61,13 @@ __global__ __launch_bounds__(kHeadThreads) void k_selector_head(hv_selector_dev 
   __shared__ int glob[8];                 // [32] int8 as words
   __shared__ int hbuf[kHeadThreads];      // partial channel sums of the candidate mean
 
-  const int b = blockIdx.x / 3, h = blockIdx.x - 3 * (blockIdx.x / 3), tid = threadIdx.x;
+  // The grid is a multiple of 8 and workgroups go round-robin over the 8
+  // XCDs, so XCD x runs logical items [x*T8, (x+1)*T8): the three heads of
+  // an image share one XCD's L2.
+  const int T = 3 * batch, T8 = (T + 7) >> 3;
+  const int L = (blockIdx.x & 7) * T8 + (blockIdx.x >> 3);
+  if (L >= T) return;
+  const int b = L / 3, h = L - 3 * b, tid = threadIdx.x;
   const int row0 = offsets[b], N = offsets[b + 1] - row0, C = N - 1;
   const int pkg = pkg_in ? (pkg_in[b] ? 1 : 0) : 0;
   if (C < 1 || C > kMaxCand || C - pkg < 1 || row0 < 0) return;  // k_selector_keep reports
@@ -478,8 +484,8 @@ int launch_selector(const SelectorArgs &a, hipStream_t s) {
     const int fast = in(-16 - (p.in_exp + p.local_w_exp)) && in(p.local_out_exp + 16) &&
                      in(-16 - (p.concat_out_exp + p.score_w1_exp)) && in(p.h1_out_exp + 16) &&
                      in(-16 - (p.h1_out_exp + p.score_w2_exp)) && in(p.h2_out_exp + 16);
-    hv_launch(k_selector_head, dim3(a.batch * 3), dim3(kHeadThreads), 0, s, p, a.tokens,
-                       a.offsets, a.pkg_in, a.hs, a.stats, fast, a.ck);
+    hv_launch(k_selector_head, dim3((a.batch * 3 + 7) / 8 * 8), dim3(kHeadThreads), 0, s, p,
+              a.tokens, a.offsets, a.batch, a.pkg_in, a.hs, a.stats, fast, a.ck);
     if ((rc = check_hip(hipGetLastError(), "k_selector_head launch"))) return rc;
   }
   hv_launch(k_selector_keep, dim3(a.batch), dim3(256), 0, s, a.offsets, a.pkg_in,
