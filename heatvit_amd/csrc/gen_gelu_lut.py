@@ -7,8 +7,11 @@ fixed.py:15-45 / transformer.py:349-358), one table per so in [3, 12].
 
 G_so is a step function of q with a few hundred changes.  Table layout
 (32-bit words):
-  L1[b], b = u >> 9 with u = clamp(q, qlo, qhi) - qlo: bits 0..23 the index
-      of the coarse bucket's first L2 entry, bits 24..27 s2;
+  L1[b], b = u >> 9 with u = clamp(q, qlo, qhi) - qlo: bits 0..23 a signed
+      byte offset, from the table's start, chosen so that the entry of u is
+      at offset + E * (u >> s2) (E = 4 or 8 bytes per entry; so the bucket's
+      first entry sits at offset + E * (b * 2^(9 - s2))), bits 24..27 s2;
+  (L1 holds n1e words, its length rounded up to even; L2 follows it)
   L2, one entry per 2^s2 values of u: G at the entry's first u and up to K
       changes inside the entry, each an offset (9 bits, 511 = none) and the
       signed 7-bit step taken from that offset on.  K = 1: one word per entry,
@@ -77,6 +80,8 @@ def build_table(so, q, o, K):
     uo = o[base:base + span + 1]                # G at u = 0 .. span
     cu = ch - base                              # change positions in u
     n1 = span // (1 << S1) + 1
+    n1e = n1 + (n1 & 1)
+    esize = 8 if K == 3 else 4
     l1 = np.zeros(n1, np.uint32)
     l2 = []
     for b in range(n1):
@@ -92,7 +97,11 @@ def build_table(so, q, o, K):
             s2 -= 1
         if worst(s2) > K:
             raise RuntimeError(f"so={so}: more than {K} changes at one offset")
-        l1[b] = (len(l2) // (2 if K == 3 else 1)) | (s2 << 24)
+        first = len(l2) // (2 if K == 3 else 1)
+        base = 4 * n1e + esize * (first - b * (1 << (S1 - s2)))
+        if not -(1 << 23) <= base < (1 << 23):
+            raise RuntimeError(f"so={so}: coarse offset {base} exceeds 24 bits")
+        l1[b] = (base & 0xFFFFFF) | (s2 << 24)
         for fb in range(1 << (S1 - s2)):
             u0 = lo + (fb << s2)
             fields = []
@@ -124,13 +133,16 @@ def lookup(qlo, qhi, l1, l2, q, K):
     u = np.clip(q, qlo, qhi) - qlo
     w1 = l1[u >> S1].astype(np.int64)
     s2 = w1 >> 24
-    f = (w1 & 0xFFFFFF) + ((u & ((1 << S1) - 1)) >> s2)
+    n1e = len(l1) + (len(l1) & 1)
+    # byte address in the whole table (L1, padding, L2) -> L2 word index
+    addr = sx(w1 & 0xFFFFFF, 24) + (8 if K == 3 else 4) * (u >> s2)
+    f2 = addr // 4 - n1e
     off = u & ((1 << s2) - 1)
-    a = l2[(2 if K == 3 else 1) * f].astype(np.int64)
+    a = l2[f2].astype(np.int64)
     o = sx(a & 255, 8)
     o = o + np.where(off >= ((a >> 8) & 511), sx((a >> 17) & 127, 7), 0)
     if K == 3:
-        b = l2[2 * f + 1].astype(np.int64)
+        b = l2[f2 + 1].astype(np.int64)
         o = o + np.where(off >= (b & 511), sx((b >> 9) & 127, 7), 0)
         o = o + np.where(off >= ((b >> 16) & 511), sx((b >> 25) & 127, 7), 0)
     return o

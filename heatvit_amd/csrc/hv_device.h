@@ -241,25 +241,27 @@ __device__ __forceinline__ int gelu_post(i64 v, int shift_in, int shift_out) {
 }
 
 // requant(gelu(q), -16, so - 16, 8) from a GELU step table (layout in
-// gen_gelu_lut.py) staged in LDS: l1 the coarse words, l2 the fine entries
-// (K = 1: one word each, K = 3: two), [qlo, qhi] the table's clamp.  The
-// coarse word of u = clamp(q) - qlo names the first fine entry and its
-// width 2^s2; the fine entry holds the value at its start and up to K
-// (offset, step) changes inside it.
+// gen_gelu_lut.py) staged in LDS at `lut`: [qlo, qhi] the table's clamp.
+// The coarse word of u = clamp(q) - qlo gives the width 2^s2 of its fine
+// entries and a byte offset such that u's entry (K = 1: one word, K = 3:
+// two) sits at offset + entry size * (u >> s2); the entry holds the value
+// at its start and up to K (offset, step) changes inside it.
 template <int K>
-__device__ __forceinline__ int gelu_table(int q, const unsigned *l1, const unsigned *l2, int qlo,
-                                          int qhi) {
-  const int u = min(max(q, qlo), qhi) - qlo;
-  const unsigned w1 = l1[u >> 9];
+__device__ __forceinline__ int gelu_table(int q, const unsigned *lut, int qlo, int qhi) {
+  int c;
+  asm("v_med3_i32 %0, %1, %2, %3" : "=v"(c) : "v"(q), "v"(qlo), "v"(qhi));
+  const unsigned u = (unsigned)(c - qlo);
+  const unsigned w1 = lut[(int)u >> 9];  // u >= 0; the signed shift folds into the address
   const unsigned s2 = w1 >> 24;
-  const unsigned f = (w1 & 0xFFFFFFu) + (((unsigned)u & 511u) >> s2);
-  const unsigned off = (unsigned)u & ((1u << s2) - 1u);
+  const unsigned off = __builtin_amdgcn_ubfe(u, 0, s2);  // u mod 2^s2
+  const int at = __builtin_amdgcn_sbfe((int)w1, 0, 24) + (int)((u >> s2) * (K == 1 ? 4u : 8u));
+  const char *e = reinterpret_cast<const char *>(lut) + at;
   if constexpr (K == 1) {
-    const unsigned w = l2[f];
+    const unsigned w = *reinterpret_cast<const unsigned *>(e);
     const int o = __builtin_amdgcn_sbfe((int)w, 0, 8);
     return o + (off >= __builtin_amdgcn_ubfe(w, 8, 9) ? __builtin_amdgcn_sbfe((int)w, 17, 7) : 0);
   } else {
-    const uint2 w2 = reinterpret_cast<const uint2 *>(l2)[f];
+    const uint2 w2 = *reinterpret_cast<const uint2 *>(e);
     int o = __builtin_amdgcn_sbfe((int)w2.x, 0, 8);
     o += off >= __builtin_amdgcn_ubfe(w2.x, 8, 9) ? __builtin_amdgcn_sbfe((int)w2.x, 17, 7) : 0;
     o += off >= __builtin_amdgcn_ubfe(w2.y, 0, 9) ? __builtin_amdgcn_sbfe((int)w2.y, 9, 7) : 0;

@@ -99,7 +99,7 @@ __device__ __noinline__ v2i epi_exact(int epi, int acc, int bias, int res, int s
 // The launch's GELU step table in LDS (gelu_table in hv_device.h).
 template <int K>
 __device__ __forceinline__ int gelu_lut(int q, const unsigned *lut, int qhi, const GemmArgs &g) {
-  return gelu_table<K>(q, lut, lut + g.lut_n1e, g.lut_qlo, qhi);
+  return gelu_table<K>(q, lut, g.lut_qlo, qhi);
 }
 
 // Stages the launch's GELU step table in LDS (all threads, then a barrier).

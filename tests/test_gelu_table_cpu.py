@@ -50,5 +50,9 @@ def test_table_lookup_is_exact_and_checked(gen, domain, so, k):
     # G is constant outside [qlo, qhi]
     assert (o[q <= qlo] == o[q == qlo][0]).all() and (o[q >= qhi] == o[q == qhi][0]).all()
     bad = l2.copy()
-    bad[(2 if k == 3 else 1) * (int(l1[0]) & 0xFFFFFF)] ^= 1   # value at qlo, off by one
+    # the entry of u = 0 (q = qlo) sits at the first coarse word's byte offset
+    # into the whole table (coarse words, padded to even, then entries)
+    at = int(l1[0]) & 0xFFFFFF
+    at = at - (1 << 24) if at >= 1 << 23 else at
+    bad[at // 4 - (len(l1) + (len(l1) & 1))] ^= 1   # value at qlo, off by one
     assert not np.array_equal(gen.lookup(qlo, qhi, l1, bad, q, k), o)
