@@ -421,36 +421,39 @@ __host__ __device__ __forceinline__ int ln_norm(int x, const LnRow &r) {
   return v < -(1 << 23) ? -(1 << 23) : (v > (1 << 23) - 1 ? (1 << 23) - 1 : v);
 }
 
-// One row of the int32 LayerNorm by a group of 8 lanes (sub = lane & 7 owns
-// channels 24*sub .. +23): w, gm, bt hold the lane's input, gamma and beta
-// bytes packed four per word; out receives the packed int8 outputs.  All 8
-// lanes of the group call it together (8-lane shuffles).  Returns the
-// row's negative-variance flag.
+// One row of the int32 LayerNorm by a group of LPR lanes (4 or 8; sub =
+// lane % LPR owns channels (192 / LPR) * sub onwards): w, gm, bt hold the
+// lane's input, gamma and beta bytes packed four per word; out receives the
+// packed int8 outputs.  All LPR lanes of the group call it together
+// (LPR-lane shuffles).  Returns the row's negative-variance flag.
 struct Ln32 {
   const int8_t *gamma, *beta;
   int8_t *out;
   int s, t, bs, os;  // x_scale + 32, 2*x_scale + 32, beta shift, output shift
 };
 
-__device__ __forceinline__ bool ln32_row(const int (&w)[6], const int (&gm)[6], const int (&bt)[6],
-                                         const Ln32 &ln, int (&out)[6]) {
+template <int LPR>
+__device__ __forceinline__ bool ln32_row(const int (&w)[48 / LPR], const int (&gm)[48 / LPR],
+                                         const int (&bt)[48 / LPR], const Ln32 &ln,
+                                         int (&out)[48 / LPR]) {
+  constexpr int NW = 48 / LPR;  // words (4 channels each) per lane
   int sx = 0, sxx = 0;
 #pragma unroll
-  for (int q = 0; q < 6; ++q) {
+  for (int q = 0; q < NW; ++q) {
     sx = __builtin_amdgcn_sdot4(w[q], 0x01010101, sx, false);
     sxx = __builtin_amdgcn_sdot4(w[q], w[q], sxx, false);
   }
 #pragma unroll
-  for (int off = 1; off < 8; off <<= 1) {
+  for (int off = 1; off < LPR; off <<= 1) {
     sx += __shfl_xor(sx, off);
     sxx += __shfl_xor(sxx, off);
   }
   const LnRow r = ln_row_consts(sx, sxx, ln.s, ln.t);
   const int rnd = 1 << (ln.os - 1);
 #pragma unroll
-  for (int q = 0; q < 6; ++q) out[q] = 0;
+  for (int q = 0; q < NW; ++q) out[q] = 0;
 #pragma unroll
-  for (int j = 0; j < 24; ++j) {
+  for (int j = 0; j < 4 * NW; ++j) {
     const int sh = 8 * (j & 3);
     const int xv = (int)(int8_t)(w[j >> 2] >> sh);
     const int g = (int)(int8_t)(gm[j >> 2] >> sh);
@@ -463,12 +466,14 @@ __device__ __forceinline__ bool ln32_row(const int (&w)[6], const int (&gm)[6], 
   return r.neg_var;
 }
 
-// gamma/beta bytes of lane sub (24 channels) as packed words.
-__device__ __forceinline__ void ln32_params(const Ln32 &ln, int sub, int (&gm)[6], int (&bt)[6]) {
-  const int2 *gp = reinterpret_cast<const int2 *>(ln.gamma + sub * 24);
-  const int2 *bp = reinterpret_cast<const int2 *>(ln.beta + sub * 24);
+// gamma/beta bytes of lane sub (192 / LPR channels) as packed words.
+template <int LPR>
+__device__ __forceinline__ void ln32_params(const Ln32 &ln, int sub, int (&gm)[48 / LPR],
+                                            int (&bt)[48 / LPR]) {
+  const int2 *gp = reinterpret_cast<const int2 *>(ln.gamma + sub * (192 / LPR));
+  const int2 *bp = reinterpret_cast<const int2 *>(ln.beta + sub * (192 / LPR));
 #pragma unroll
-  for (int q = 0; q < 3; ++q) {
+  for (int q = 0; q < 24 / LPR; ++q) {
     const int2 a = gp[q], c = bp[q];
     gm[2 * q] = a.x; gm[2 * q + 1] = a.y;
     bt[2 * q] = c.x; bt[2 * q + 1] = c.y;

@@ -112,14 +112,16 @@ __global__ __launch_bounds__(256) void k_layernorm(const int8_t *__restrict__ x,
 // [1, 29] (LnRow in hv_device.h): eight lanes per row, 24 channels each.
 // Row sums come from packed int8 dot products; each element costs three
 // 24-bit multiply-adds for norm_q16, one for gamma/beta and the requant.
+template <int LPR>
 __global__ __launch_bounds__(256) void k_layernorm32(const int8_t *__restrict__ x, Ln32 ln,
                                                      int rows, const int32_t *rows_dev,
                                                      uint8_t *neg_var, LnWarn lw) {
-  const int sub = threadIdx.x & 7;
-  auto load_row = [&](int row, int (&w)[6]) {
-    const int2 *xr = reinterpret_cast<const int2 *>(x + (size_t)row * 192 + sub * 24);
+  constexpr int NW = 48 / LPR, RPB = 256 / LPR;  // words per lane, rows per workgroup
+  const int sub = threadIdx.x & (LPR - 1);
+  auto load_row = [&](int row, int (&w)[NW]) {
+    const int2 *xr = reinterpret_cast<const int2 *>(x + (size_t)row * 192 + sub * (192 / LPR));
 #pragma unroll
-    for (int q = 0; q < 3; ++q) {
+    for (int q = 0; q < NW / 2; ++q) {
       const int2 v = xr[q];
       w[2 * q] = v.x;
       w[2 * q + 1] = v.y;
@@ -127,19 +129,22 @@ __global__ __launch_bounds__(256) void k_layernorm32(const int8_t *__restrict__ 
   };
   // The first row, gamma and beta are loaded before the device row count
   // arrives (the buffers hold `rows` rows), so the loads overlap.
-  int row = blockIdx.x * 32 + (threadIdx.x >> 3);
-  int w[6] = {0, 0, 0, 0, 0, 0};
-  if (row < rows) load_row(row, w);
-  int gm[6], bt[6];
-  ln32_params(ln, sub, gm, bt);
-  const int R = rows_dev ? min(*rows_dev, rows) : rows;
-  for (; row < R; row += gridDim.x * 32) {
-    int out[6];
-    if (row != blockIdx.x * 32 + (int)(threadIdx.x >> 3)) load_row(row, w);
-    const bool neg = ln32_row(w, gm, bt, ln, out);
-    int2 *yr = reinterpret_cast<int2 *>(ln.out + (size_t)row * 192 + sub * 24);
+  const int row_first = blockIdx.x * RPB + (int)(threadIdx.x / LPR);
+  int row = row_first;
+  int w[NW];
 #pragma unroll
-    for (int q = 0; q < 3; ++q) yr[q] = int2{out[2 * q], out[2 * q + 1]};
+  for (int q = 0; q < NW; ++q) w[q] = 0;
+  if (row < rows) load_row(row, w);
+  int gm[NW], bt[NW];
+  ln32_params<LPR>(ln, sub, gm, bt);
+  const int R = rows_dev ? min(*rows_dev, rows) : rows;
+  for (; row < R; row += gridDim.x * RPB) {
+    int out[NW];
+    if (row != row_first) load_row(row, w);
+    const bool neg = ln32_row<LPR>(w, gm, bt, ln, out);
+    int2 *yr = reinterpret_cast<int2 *>(ln.out + (size_t)row * 192 + sub * (192 / LPR));
+#pragma unroll
+    for (int q = 0; q < NW / 2; ++q) yr[q] = int2{out[2 * q], out[2 * q + 1]};
     if (neg_var && sub == 0) neg_var[row] = neg ? 1 : 0;
     if (neg && lw.img_warn && sub == 0) ln_warn_row(lw.offsets, lw.batch, lw.img_warn, row);
   }
@@ -170,9 +175,12 @@ int launch_layernorm(const int8_t *x, const int8_t *g, const int8_t *b, int8_t *
   const int common = (g_exp - 16) < b_exp ? (g_exp - 16) : b_exp;
   Ln32 ln;
   if (((uintptr_t)x & 7) == 0 && ln32_setup(g, b, y, x_exp, g_exp, b_exp, out_exp, &ln)) {
-    const int blocks = (rows + 31) / 32;
-    hv_launch(k_layernorm32, dim3(blocks < 256 * 8 ? blocks : 256 * 8), dim3(256), 0, s, x, ln,
-              rows, rows_dev, neg_var, lw);
+    // eight lanes per row: four lanes (half the repeated per-row constants,
+    // 150 VGPRs) measured slower one batch at a time and even pipelined
+    constexpr int kLpr = 8;
+    const int blocks = (rows + 256 / kLpr - 1) / (256 / kLpr);
+    hv_launch(k_layernorm32<kLpr>, dim3(blocks < 256 * 8 ? blocks : 256 * 8), dim3(256), 0, s, x,
+              ln, rows, rows_dev, neg_var, lw);
     return check_hip(hipGetLastError(), "k_layernorm32 launch");
   }
   const bool fast_norm = x_exp <= -1;
