@@ -60,9 +60,11 @@ static constexpr int kImageBytes = 224 * 224 * 3;
 // grid with static tile striding left a partial last round per workgroup.
 static constexpr int kGridCap = 1 << 20;
 static constexpr int kLdsGridCap = 256 * 2;  // LDS-staged kernel: 2 per CU, persistent
-// GELU step-table launches: persistent, four workgroups per CU (each stages
-// the table once; two or eight per CU, or one workgroup per tile, were slower)
-static constexpr int kLutGridCap = 256 * 4;
+// GELU step-table launches: persistent, five workgroups per CU, which the
+// 92 VGPRs and the largest table (31 KB of LDS) both allow; each stages the
+// table once (two, three, four or eight per CU, or one workgroup per tile,
+// were slower)
+static constexpr int kLutGridCap = 256 * 5;
 
 template <int AMODE>
 __device__ __forceinline__ const int8_t *a_row(const GemmArgs &g, int r) {
