@@ -18,9 +18,16 @@ that every pipeline slot's logits equal the single-stream forward's.
 
 Prints one JSON line (rank 0) with the images/s figure, the roofline of the
 dominant kernel class (HIP start/stop events recorded by each kernel's own
-dispatch on the launch stream, over a second pass of the same steps), the GEMM-phase int8 MFMA utilisation, the unpruned
-control's images/s and the CPU oracle's throughput on a bounded sample of
-the same workload.
+dispatch on the launch stream, over a second pass of the same steps), the
+GEMM-phase int8 MFMA utilisation, the unpruned control's images/s, the CPU
+oracle's throughput on a bounded sample of the same workload, and
+`bit_exact`: the 256-image logits and token counts of the pruned batch and
+of the unpruned control, compared with the CPU oracle on the same inputs
+(the process exits with status 1 when they differ).  `configs` times the
+smaller workloads (one block, the unpruned model on one image, the selector
+over 64 token sets, the pruned model over 32 images), each checked against
+the oracle, and `softmax_standalone` the integer softmax over the attention's
+3*197 rows per image of the batch.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5]
 """
@@ -85,13 +92,208 @@ def class_work(counts, params, batch):
     return ops, hbm
 
 
-def cpu_baseline(images, params, threads):
+def oracle_model(images, params, threads):
+    """The CPU oracle over a batch: (logits, token counts, status, seconds)."""
     from oracle import oracle
     t0 = time.perf_counter()
-    _, _, status, _ = oracle.model_infer_batch(images, params, threads=threads)
-    dt = time.perf_counter() - t0
-    assert not status.any()
-    return len(images) / dt, dt
+    logits, counts, status, _ = oracle.model_infer_batch(images, params, threads=threads)
+    return logits, counts, status, time.perf_counter() - t0
+
+
+def roof(ops, nbytes, ms):
+    """Roofline entry of one kernel class: the binding roof is the one its
+    arithmetic intensity (int8 ops per algorithmic HBM byte) selects against
+    the ridge point peak_ops / peak_bytes = 625 ops/B; the other roof's
+    fraction is reported beside it."""
+    t = ms * 1e-3
+    tops = ops / t / 1e12 if ops else 0.0
+    gbs = nbytes / t / 1e9 if nbytes else 0.0
+    ridge = MI355X_INT8_TOPS * 1e12 / (MI355X_HBM_GBS * 1e9)
+    intensity = ops / nbytes if nbytes else float("inf")
+    if intensity >= ridge:
+        r = {"bound": "mfma", "achieved": round(tops, 2), "peak": MI355X_INT8_TOPS,
+             "unit": "TFLOP/s", "frac": round(tops / MI355X_INT8_TOPS, 4),
+             "hbm_frac": round(gbs / MI355X_HBM_GBS, 4)}
+    else:
+        r = {"bound": "hbm", "achieved": round(gbs, 1), "peak": MI355X_HBM_GBS, "unit": "GB/s",
+             "frac": round(gbs / MI355X_HBM_GBS, 4),
+             "mfma_frac": round(tops / MI355X_INT8_TOPS, 4)}
+    r["ops_per_byte"] = round(intensity, 1) if nbytes else None
+    return r
+
+
+def _sync_time(fn, warmup, steps):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def _class_ms(L, fn, steps):
+    """Per-class kernel milliseconds per call of fn (dispatch-recorded events)."""
+    from heatvit_amd import _lib
+    L.hv_profile_enable(1)
+    for _ in range(steps):
+        fn()
+    ms = np.zeros(len(_lib.PROF_CLASSES), np.float32)
+    launches = np.zeros(len(_lib.PROF_CLASSES), np.int32)
+    _lib.check(L.hv_profile_read(ms.ctypes.data, launches.ctypes.data, len(ms)), "profile")
+    L.hv_profile_enable(0)
+    return {n: float(ms[i]) / steps for i, n in enumerate(_lib.PROF_CLASSES) if launches[i]}
+
+
+GEMM_CLASSES = ("patch", "gemm_qkv", "attention", "gemm_proj", "gemm_ffn1", "gemm_ffn2", "head")
+
+
+def _summary(cls_ms, ops, hbm, batch, ms, exact, cpu_s):
+    gemm_ms = sum(cls_ms.get(n, 0.0) for n in GEMM_CLASSES)
+    gemm_ops = sum(ops.get(n, 0) for n in GEMM_CLASSES)
+    line = {"images_per_s": round(batch / (ms * 1e-3), 1), "ms_per_forward": round(ms, 4),
+            "bit_exact": exact,
+            "cpu_oracle_images_per_s": round(batch / cpu_s, 2) if cpu_s else None}
+    if gemm_ms:
+        line["gemm_phase_frac_int8_peak"] = round(
+            gemm_ops / (gemm_ms * 1e-3) / 1e12 / MI355X_INT8_TOPS, 4)
+    for name in ("layernorm", "selector"):
+        if cls_ms.get(name) and hbm.get(name):
+            gbs = hbm[name] / (cls_ms[name] * 1e-3) / 1e9
+            line[f"{name}_gbs"] = round(gbs, 1)
+            line[f"{name}_hbm_frac"] = round(gbs / MI355X_HBM_GBS, 4)
+    return line
+
+
+def config_lines(args, L):
+    """The smaller workloads, one forward at a time on the current stream,
+    each compared with the CPU oracle: one block over 197 tokens, the
+    unpruned model on one image, the selector over 64 token sets of 197, the
+    pruned model over 32 images."""
+    import torch
+
+    from heatvit_amd import _lib, synth
+    from heatvit_amd.device import DeviceBlock, DeviceSelector
+    from heatvit_amd.model import Engine
+    from oracle import oracle
+
+    def stream():
+        return torch.cuda.current_stream().cuda_stream
+
+    def dev(a):
+        return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+    threads = min(16, os.cpu_count() or 1)
+    out = {}
+
+    x, bp = synth.block_workload()
+    db = DeviceBlock(bp)
+    xd, off = dev(x), dev(np.array([0, 197], np.int32))
+    z = torch.empty((197, 192), dtype=torch.int8, device="cuda")
+    ws = torch.empty(L.hv_block_workspace_bytes(1, 197), dtype=torch.uint8, device="cuda")
+
+    def block():
+        _lib.check(L.hv_block_forward(db.struct, xd.data_ptr(), off.data_ptr(), 1, 197,
+                                      z.data_ptr(), None, None, None, ws.data_ptr(), ws.numel(),
+                                      stream()), "block")
+    ms = _sync_time(block, args.warmup, args.steps)
+    t0 = time.perf_counter()
+    want, _ = oracle.transformer_block(x, bp, checkpoints=False)
+    cpu_s = time.perf_counter() - t0
+    n = 197
+    ops = {"gemm_qkv": 2 * 192 * 576 * n, "gemm_proj": 2 * 192 * 192 * n,
+           "gemm_ffn1": 2 * 192 * 768 * n, "gemm_ffn2": 2 * 768 * 192 * n,
+           "attention": 2 * 384 * n * n}
+    hbm = {"layernorm": 2 * 2 * 192 * n}
+    out["c0_block_b1"] = _summary(_class_ms(L, block, args.steps), ops, hbm, 1, ms,
+                                  bool(np.array_equal(z.cpu().numpy(), want)), cpu_s)
+
+    for key, (imgs, params) in (("c1_full_unpruned_b1", synth.full_workload()),
+                                ("c3_pruned_b32", synth.pruned_workload())):
+        b = len(imgs)
+        eng = Engine(params, b)
+        idev = dev(imgs.reshape(b, -1))
+        ms = _sync_time(lambda: eng.forward(idev), args.warmup, args.steps)
+        logits = eng.logits[:b].cpu().numpy()
+        counts = eng.token_counts[:b].cpu().numpy()
+        o_logits, o_counts, o_status, cpu_s = oracle_model(imgs, params, threads)
+        exact = bool(not o_status.any() and np.array_equal(logits, o_logits) and
+                     np.array_equal(counts, o_counts))
+        ops, hbm = class_work(counts, params, b)
+        out[key] = _summary(_class_ms(L, lambda: eng.forward(idev), args.steps), ops, hbm, b,
+                            ms, exact, cpu_s)
+        if params.selectors:
+            out[key]["mean_tokens_per_stage"] = counts.mean(axis=0).round(2).tolist()
+        del eng
+
+    tokens, sp = synth.selector_workload()
+    b = len(tokens)
+    ds = DeviceSelector(sp)
+    tin = dev(tokens.reshape(-1, 192))
+    offs = dev(np.arange(b + 1, dtype=np.int32) * 197)
+    pkg = torch.zeros(b, dtype=torch.uint8, device="cuda")
+    o_tok = torch.empty((b * 198, 192), dtype=torch.int8, device="cuda")
+    o_off = torch.empty(b + 1, dtype=torch.int32, device="cuda")
+    o_pkg = torch.empty(b, dtype=torch.uint8, device="cuda")
+    fused = torch.empty((b, 196), dtype=torch.int32, device="cuda")
+    kept = torch.empty((b, 196), dtype=torch.int32, device="cuda")
+    state = torch.empty((b, 5), dtype=torch.int32, device="cuda")
+    sws = torch.empty(L.hv_selector_workspace_bytes(b), dtype=torch.uint8, device="cuda")
+
+    def selector():
+        _lib.check(L.hv_selector_forward(ds.struct, tin.data_ptr(), offs.data_ptr(),
+                                         pkg.data_ptr(), b, o_tok.data_ptr(), o_off.data_ptr(),
+                                         o_pkg.data_ptr(), fused.data_ptr(), kept.data_ptr(),
+                                         state.data_ptr(), None, sws.data_ptr(), sws.numel(),
+                                         stream()), "selector")
+    ms = _sync_time(selector, args.warmup, args.steps)
+    got_tok, got_off, st = o_tok.cpu().numpy(), o_off.cpu().numpy(), state.cpu().numpy()
+    exact, cpu_s = True, 0.0
+    for i in range(b):
+        t0 = time.perf_counter()
+        w = oracle.token_selector(tokens[i], False, sp, checkpoints=False)
+        cpu_s += time.perf_counter() - t0
+        exact = exact and st[i, 0] == w["token_count"] and \
+            np.array_equal(got_tok[got_off[i]:got_off[i + 1]], w["tokens"])
+    n_out = int(st[:, 0].sum())
+    ops = {"selector": 2 * 13938 * 196 * b}
+    hbm = {"selector": 192 * 197 * b + 192 * n_out}
+    out["c2_selector_b64"] = _summary(_class_ms(L, selector, args.steps), ops, hbm, b, ms,
+                                      bool(exact), cpu_s)
+    out["c2_selector_b64"]["mean_tokens_out"] = round(n_out / b, 2)
+    return out
+
+
+def softmax_standalone(args, L):
+    """hv_softmax_rows over the attention's rows of one batch at stage 0:
+    3 heads x 197 query rows of 197 q16 scores per image (int32 in, UQ0.8
+    out: 5 bytes per element), checked against the oracle on 256 rows."""
+    import torch
+
+    from heatvit_amd import _lib
+    from oracle import oracle
+    rows = 3 * 197 * args.batch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(20260815)
+    x = torch.randint(-(1 << 18), 1 << 18, (rows * 197,), dtype=torch.int32, device="cuda",
+                      generator=g)
+    off = torch.arange(rows + 1, dtype=torch.int32, device="cuda") * 197
+    att = torch.empty(rows * 197, dtype=torch.uint8, device="cuda")
+
+    def run():
+        _lib.check(L.hv_softmax_rows(x.data_ptr(), off.data_ptr(), rows, att.data_ptr(), None,
+                                     torch.cuda.current_stream().cuda_stream), "softmax")
+    ms = _sync_time(run, args.warmup, args.steps)
+    xs, got = x.view(rows, 197).cpu().numpy(), att.view(rows, 197).cpu().numpy()
+    pick = np.random.default_rng(7).choice(rows, 256, replace=False)
+    exact = all(np.array_equal(got[r], oracle.softmax_attention(xs[r])) for r in pick)
+    nbytes = rows * 197 * 5
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"workload": f"{rows} rows of 197 int32 scores (3 x 197 per image, batch "
+                        f"{args.batch}) -> UQ0.8", "ms": round(ms, 4), "gbs": round(gbs, 1),
+            "hbm_frac": round(gbs / MI355X_HBM_GBS, 4), "bit_exact_sample": bool(exact)}
 
 
 def main():
@@ -109,6 +311,8 @@ def main():
     ap.add_argument("--no-control", action="store_true", help="skip the unpruned control")
     ap.add_argument("--no-float", action="store_true",
                     help="skip the float-image front-end measurement")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the per-config lines and the standalone softmax")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run three 64 MiB device-to-device copies (the reference "
                          "kernel for scaling HBM counters in a profiler run)")
@@ -195,14 +399,11 @@ def main():
     gemm_tops = gemm_ops / (gemm_ms * 1e-3) / 1e12
     dom = max(per_class, key=lambda n: per_class[n]["ms_per_step"])
     d = per_class[dom]
-    if dom in gemm_names:
-        achieved = ops[dom] / (d["ms_per_step"] * 1e-3) / 1e12
-        roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MI355X_INT8_TOPS,
-                    "unit": "TFLOP/s", "frac": round(achieved / MI355X_INT8_TOPS, 4)}
-    else:
-        achieved = hbm[dom] / (d["ms_per_step"] * 1e-3) / 1e9
-        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": MI355X_HBM_GBS,
-                    "unit": "GB/s", "frac": round(achieved / MI355X_HBM_GBS, 4)}
+    roofline = roof(ops.get(dom, 0), hbm.get(dom, 0), d["ms_per_step"])
+    for name, entry in per_class.items():
+        if ops.get(name) or hbm.get(name):
+            r = roof(ops.get(name, 0), hbm.get(name, 0), entry["ms_per_step"])
+            entry["bound"], entry["frac"] = r["bound"], r["frac"]
     roofline["kernel"] = dom
     roofline["avg_launch_us"] = d["avg_launch_us"]
     traffic_file = ROOT / "profiles" / f"traffic_{dom}.json"
@@ -221,10 +422,12 @@ def main():
                             "frac": round(rate / MI355X_VALU_GINST, 4)}
 
     control = None
+    ctrl_logits = None
     if not args.no_control:
         ctrl = Engine(synth.unpruned_control(params), args.batch)
         for _ in range(max(1, args.warmup // 2)):
             ctrl.forward(dev)
+        ctrl_logits = ctrl.logits[:args.batch].cpu().numpy()
         c_lat = timed(ctrl.forward, args.steps)
         c_wall = c_lat
         if args.streams > 1:
@@ -272,12 +475,27 @@ def main():
                     "front_end_gbs": round(fe_bytes / (fe_ms * 1e-3) / 1e9, 1)}
         del fdev
 
+    configs = None if args.no_configs else config_lines(args, L)
+    softmax = None if args.no_configs else softmax_standalone(args, L)
+
+    # Bit-exactness of the timed outputs against the CPU oracle on the same
+    # images: the pruned batch (its first pass is also the CPU baseline's
+    # first pass) and the unpruned control.
+    threads = min(16, os.cpu_count() or 1)
+    gpu_logits = ref_logits.cpu().numpy()
+    o_logits, o_counts, o_status, dt = oracle_model(images, params, threads)
+    bit_exact = {"pruned": bool(not o_status.any() and np.array_equal(o_logits, gpu_logits)
+                                and np.array_equal(o_counts, counts))}
+    if ctrl_logits is not None:
+        c_logits, c_counts, c_status, _ = oracle_model(images, synth.unpruned_control(params),
+                                                       threads)
+        bit_exact["unpruned_control"] = bool(not c_status.any() and
+                                             np.array_equal(c_logits, ctrl_logits))
     cpu = None
     if args.cpu_passes > 0:
-        threads = min(16, os.cpu_count() or 1)
-        secs, passes = 0.0, 0
-        while passes < args.cpu_passes and (passes == 0 or secs < args.cpu_seconds):
-            _, dt = cpu_baseline(images, params, threads)
+        secs, passes = dt, 1
+        while passes < args.cpu_passes and secs < args.cpu_seconds:
+            dt = oracle_model(images, params, threads)[3]
             secs += dt
             passes += 1
         n = passes * args.batch
@@ -300,15 +518,22 @@ def main():
         "one_batch_at_a_time": {"value": round(args.batch / (latency_ms / 1e3), 1),
                                 "ms_per_batch": round(latency_ms, 4)},
         "pipelined_logits_equal": pipe_equal,
+        "bit_exact": all(bit_exact.values()) and pipe_equal is not False,
+        "bit_exact_checks": bit_exact,
         "roofline": roofline,
         "gemm_phase": {"tops": round(gemm_tops, 1), "frac_int8_peak": round(gemm_tops / MI355X_INT8_TOPS, 4),
                        "ms_per_step": round(gemm_ms, 4)},
         "kernels": per_class,
         "control": control,
         "float_images": float_fe,
+        "configs": configs,
+        "softmax_standalone": softmax,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
+    if not line["bit_exact"] or (configs and not all(c["bit_exact"] for c in configs.values())):
+        print("bench.py: GPU outputs differ from the CPU oracle", file=sys.stderr)
+        sys.exit(1)
 
 
 if __name__ == "__main__":

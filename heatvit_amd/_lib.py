@@ -21,7 +21,7 @@ HV_PRIM_GELU_POST, HV_PRIM_GELU_TABLE = 4, 5
 GELU_TABLE_SO = range(3, 13)
 HV_EPI_I8, HV_EPI_I32, HV_EPI_GELU, HV_EPI_RESIDUAL = 0, 1, 2, 3
 HV_A_ROWS, HV_A_GATHER = 0, 1
-ABI_VERSION = 4
+ABI_VERSION = 5
 PROF_CLASSES = ("patch", "layernorm", "gemm_qkv", "attention", "gemm_proj", "gemm_ffn1",
                 "gemm_ffn2", "selector", "head", "other")
 
@@ -96,7 +96,7 @@ class Schedule(C.Structure):
 
 class SelectorCkpt(C.Structure):
     _fields_ = [(n, _vp) for n in ("local", "global_", "head_scores", "head_stats",
-                                   "head_weights")]
+                                   "head_weights", "h2")]
 
 
 class BlockCkpt(C.Structure):

@@ -271,7 +271,7 @@ const char *hv_last_error(void) { return g_err; }
 
 int hv_last_error_class(void) { return g_err_class; }
 
-int hv_abi_version(void) { return 4; }
+int hv_abi_version(void) { return 5; }
 
 int hv_eval_primitive(int op, const int64_t *in, int64_t *out, int64_t n, int a, int b, int c,
                       hv_stream_t stream) {

@@ -440,11 +440,15 @@ int launch_attention(const AttnArgs &a_in, hipStream_t s) {
 
 // ---------------------------------------------------------------------------
 // Softmax over ragged rows (nonlinear.softmax_scaled / _attention /
-// _selector, nonlinear.py:109-133): one wavefront per row, <= 256 entries.
+// _selector, nonlinear.py:109-133): one wavefront per row (<= 256 entries),
+// four rows per workgroup.  Rows of at most 255 entries sum to below 2^24
+// (each exponential <= exp(0) = 65554), so their reciprocal takes the
+// 32-bit form; longer rows the 64-bit one.  att / sel may be NULL.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void k_softmax_rows(const int32_t *x, const int32_t *offsets,
-                                                     uint8_t *att, int32_t *sel) {
-  const int row = blockIdx.x, lane = threadIdx.x;
+__global__ __launch_bounds__(256) void k_softmax_rows(const int32_t *x, const int32_t *offsets,
+                                                      int rows, uint8_t *att, int32_t *sel) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= rows) return;
   const int o = offsets[row], n = offsets[row + 1] - o;
   if (n <= 0 || n > 256) return;
   int v[4];
@@ -469,14 +473,14 @@ __global__ __launch_bounds__(64) void k_softmax_rows(const int32_t *x, const int
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-  const unsigned recip = softmax_recip(sum);
+  const unsigned recip = n <= 255 ? softmax_recip24(sum) : softmax_recip(sum);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int c = lane + 64 * j;
     if (c < n) {
       const unsigned ratio = softmax_ratio(e[j], recip);
-      att[o + c] = (uint8_t)prob_u8(ratio);
-      sel[o + c] = (int32_t)(ratio > 65536u ? 65536u : ratio);
+      if (att) att[o + c] = (uint8_t)prob_u8(ratio);
+      if (sel) sel[o + c] = (int32_t)(ratio > 65536u ? 65536u : ratio);
     }
   }
 }
@@ -484,7 +488,7 @@ __global__ __launch_bounds__(64) void k_softmax_rows(const int32_t *x, const int
 int launch_softmax_rows(const int32_t *x, const int32_t *offsets, int rows, uint8_t *att,
                         int32_t *sel, hipStream_t s) {
   if (rows <= 0) return HV_OK;
-  hv_launch(k_softmax_rows, dim3(rows), dim3(64), 0, s, x, offsets, att, sel);
+  hv_launch(k_softmax_rows, dim3((rows + 3) / 4), dim3(256), 0, s, x, offsets, rows, att, sel);
   return check_hip(hipGetLastError(), "k_softmax_rows launch");
 }
 

@@ -151,10 +151,18 @@ struct Reader {
     if (off + (uint64_t)bytes > weight_end) weight_end = off + bytes;
     return off;
   }
-  // GEMM weights: src1 and bias from the weight region, bias enabled.
-  void gemm_weights(const Desc *g, uint32_t wbytes, uint32_t bbytes, uint32_t *w, uint32_t *b) {
+  // GEMM weights: src1 and bias from the weight region, bias enabled, the
+  // weights read as [K][N] against a signed activation with the operands in
+  // place (RHS_TRANSPOSE, SWAP_ACTIVATION and SRC0_UNSIGNED clear), and an
+  // int8 output unless out_i32 (the classifier).
+  void gemm_weights(const Desc *g, uint32_t wbytes, uint32_t bbytes, uint32_t *w, uint32_t *b,
+                    bool out_i32 = false) {
     if (ok() && !g->has(F_BIAS))
       rc = fail(HV_EVALUE, HV_ERR_DIMENSION, "descriptor %d: GEMM without bias", pos - 1);
+    if (ok() && (g->has(F_RHS_TRANSPOSE) || g->has(F_SWAP) || g->has(F_SRC0_UNSIGNED) ||
+                 g->has(F_OUT_I32) != out_i32))
+      rc = fail(HV_EVALUE, HV_ERR_DIMENSION, "descriptor %d: weight GEMM flags 0x%x", pos - 1,
+                g->flags);
     *w = weight(g->src1, wbytes, !g->has(F_SRC1_SCRATCH));
     *b = weight(g->bias, bbytes, !g->has(F_BIAS_SCRATCH));
   }
@@ -490,7 +498,7 @@ int hv_schedule_compile(const uint8_t *words, int n_desc, hv_schedule *out) {
     r.same(head->s0, m.final_ln_out_exp, "final LayerNorm -> classifier");
     m.head_w_exp = head->s1;
     r.same(head->sdst, kLogit, "logits");
-    r.gemm_weights(head, 192 * 1000, 1000 * 4, &sc.head_w, &sc.head_b);
+    r.gemm_weights(head, 192 * 1000, 1000 * 4, &sc.head_w, &sc.head_b, true);
   }
   if (r.ok() && r.pos != n_desc)
     r.rc = fail(HV_EVALUE, HV_ERR_DIMENSION, "descriptors after FINISH (%d)", r.pos);

@@ -228,6 +228,9 @@ __global__ __launch_bounds__(kHeadThreads) void k_selector_head(hv_selector_dev 
         for (int o = 0; o < LPC; ++o)
 #pragma unroll
           for (int q = 0; q < W2; ++q) h2[o * W2 + q] = __shfl(mine2[q], base + o);
+        if (ck.h2 && sub == 0)
+          *reinterpret_cast<v4i *>(ck.h2 + (((size_t)b * 3 + h) * kMaxCand + c) * 16) =
+              v4i{h2[0], h2[1], h2[2], h2[3]};
         // layer 3: logit (sub & 1) here; the group's first two lanes hold both
         const int lj = sub & 1;
         int acc = 0;
@@ -264,17 +267,25 @@ __device__ int fuse_candidate(const hv_selector_dev &p, const int8_t *stats, con
   int hid[3];
 #pragma unroll
   for (int j = 0; j < 3; ++j) {
-    int acc = p.hw_b1[j];
+    // The bias is any int32 and the reference adds it in int64
+    // (gemm.py:118-119): the three products (|sum| < 2^16) are summed in
+    // 32 bits and the bias added in 64.  The empty asm keeps the compiler
+    // from folding bias and products into one 32-bit dot-product
+    // accumulation, which wraps for biases near the int32 limits.
+    int dot = 0;
 #pragma unroll
-    for (int k = 0; k < 3; ++k) acc += (int)stats[k] * (int)p.hw_w1t[j * 3 + k];
-    hid[j] = gelu_post(acc, a_in, a_out);
+    for (int k = 0; k < 3; ++k) dot += (int)stats[k] * (int)p.hw_w1t[j * 3 + k];
+    asm volatile("" : "+v"(dot));
+    hid[j] = gelu_post((i64)p.hw_b1[j] + dot, a_in, a_out);
   }
   i64 num = 0, den = 0;
 #pragma unroll
   for (int j = 0; j < 3; ++j) {
-    i64 acc = p.hw_b2[j];
+    int dot = 0;
 #pragma unroll
-    for (int k = 0; k < 3; ++k) acc += (i64)hid[k] * p.hw_w2t[j * 3 + k];
+    for (int k = 0; k < 3; ++k) dot += hid[k] * (int)p.hw_w2t[j * 3 + k];
+    asm volatile("" : "+v"(dot));
+    const i64 acc = (i64)p.hw_b2[j] + dot;
     const int w = sat_q016(plan_sigmoid((int)requant_shift(acc, b_sh, 24)));
     if (weights_out) weights_out[j] = w;
     num += (i64)hs[j * kMaxCand] * w;
@@ -298,7 +309,7 @@ __global__ __launch_bounds__(256) void k_selector_keep(const int32_t *offsets,
                                                        hv_selector_dev p, const int32_t *hs,
                                                        const int8_t *stats, int32_t *weights_ck,
                                                        int32_t *img_warn) {
-  __shared__ int w_kept[4], w_warn[4];
+  __shared__ int w_kept[4], w_warn[4], w_bad[4];
   __shared__ i64 w_den[4];
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int C = offsets[b + 1] - offsets[b] - 1;
@@ -316,7 +327,7 @@ __global__ __launch_bounds__(256) void k_selector_keep(const int32_t *offsets,
   const int c = tid;
   const bool in = c < C;
   int fc = 0;
-  bool warn = false;
+  bool warn = false, bad = false;
   if (hs) {
     if (in) {
       fc = fuse_candidate(p, stats + ((size_t)b * kMaxCand + c) * 3,
@@ -326,7 +337,10 @@ __global__ __launch_bounds__(256) void k_selector_keep(const int32_t *offsets,
       f[c] = fc;
     }
   } else {
+    // Given scores must be Q0.16 values in [0, 65536] (selector._q016): an
+    // image holding any other value is rejected like a bad token count.
     fc = in ? f[c] : 0;
+    bad = in && (unsigned)fc > 65536u;
   }
   const bool is_norm = c < n_norm;
   const bool keep = is_norm && fc >= 32768;
@@ -341,7 +355,13 @@ __global__ __launch_bounds__(256) void k_selector_keep(const int32_t *offsets,
     w_den[wave] = d;
     w_warn[wave] = warn_wave;
   }
+  const bool bad_wave = __ballot(bad) != 0;
+  if (lane == 0) w_bad[wave] = bad_wave;
   __syncthreads();
+  if (w_bad[0] | w_bad[1] | w_bad[2] | w_bad[3]) {
+    if (tid == 0) { st[0] = -1; st[1] = 0; st[2] = 0; st[3] = 0; st[4] = 0; }
+    return;
+  }
   int before = __popcll(mask & ((1ull << lane) - 1ull)), kept = 0;
   i64 den = 0;
   bool warn_head = false;

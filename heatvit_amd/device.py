@@ -11,7 +11,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from .params import BlockParams, HeatViTParams, PatchParams, SelectorParams, check_scale_exps
+from .params import BlockParams, HeatViTParams, SelectorParams, check_scale_exps, coerce
 
 
 # Position of output channel c (0..31) of a weight tile among the MFMA
@@ -125,8 +125,7 @@ def _patch_struct(pp, h):
 
 class DeviceBlock:
     def __init__(self, params, device="cuda"):
-        if not isinstance(params, BlockParams):
-            raise TypeError("params must be BlockParams")
+        params = coerce(params, BlockParams)
         check_scale_exps(params)
         self.params = params
         self.holder = _Holder(device)
@@ -135,8 +134,7 @@ class DeviceBlock:
 
 class DeviceSelector:
     def __init__(self, params, device="cuda"):
-        if not isinstance(params, SelectorParams):
-            raise TypeError("params must be SelectorParams")
+        params = coerce(params, SelectorParams)
         check_scale_exps(params)
         self.params = params
         self.holder = _Holder(device)
@@ -147,10 +145,7 @@ class DeviceModel:
     """HeatViTParams uploaded once (about 6 MB of packed weights)."""
 
     def __init__(self, params, device="cuda"):
-        if not isinstance(params, HeatViTParams):
-            raise TypeError("params must be HeatViTParams")
-        if not isinstance(params.patch, PatchParams):
-            raise TypeError("patch must be PatchParams")
+        params = coerce(params, HeatViTParams)
         if (params.patch.width, params.patch.height, params.patch.patch) != (224, 224, 16):
             raise ValueError("the HIP patch embedding handles 224x224x3 images with 16x16 patches")
         check_scale_exps(params)

@@ -19,7 +19,7 @@ import torch
 from . import _lib
 from .device import DeviceModel
 from .image import float_images
-from .params import HeatViTParams
+from .params import HeatViTParams, coerce
 
 LOGIT_SCALE_EXP = -14
 WARN_HEAD_DEN_ZERO, WARN_PACKAGE_DEN_ZERO, WARN_LN_NEGATIVE_VARIANCE = 1, 2, 4
@@ -174,11 +174,11 @@ class HeatViTModel:
         self._cache = None
 
     def _engine(self, params, batch):
-        if not isinstance(params, HeatViTParams):
-            raise TypeError("params must be HeatViTParams")
+        # params: HeatViTParams, or the reference's own HeatViTParams (or any
+        # object with its field names), converted once per params object
         if (self._cache is None or self._cache[0] is not params or
                 self._cache[1].max_batch < batch):
-            self._cache = (params, Engine(params, batch))
+            self._cache = (params, Engine(coerce(params, HeatViTParams), batch))
         return self._cache[1]
 
     def infer_batch(self, images, params, checkpoints=False):
@@ -225,7 +225,8 @@ class HeatViTModel:
         images: returns (logits [B][1000] int32, token_counts [B][4],
         LOGIT_SCALE_EXP).  prune=False skips the selectors."""
         if not prune:
-            params = dataclasses.replace(params, selectors=(), selector_blocks=())
+            params = dataclasses.replace(coerce(params, HeatViTParams), selectors=(),
+                                         selector_blocks=())
         r = self.infer_float_batch(images, params)
         return r.logits, r.token_counts, LOGIT_SCALE_EXP
 

@@ -15,7 +15,7 @@ arrays are both accepted.  Floats raise TypeError, out-of-range values and
 wrong shapes raise ValueError, as in the reference.
 """
 
-from dataclasses import dataclass, field, fields
+from dataclasses import MISSING, dataclass, field, fields
 
 import numpy as np
 
@@ -293,6 +293,42 @@ class HeatViTParams:
         _check_exps(self)
 
 
+# Container-valued fields, per container class.
+_NESTED = {
+    (HeatViTParams, "patch"): lambda v: coerce(v, PatchParams),
+    (HeatViTParams, "blocks"): lambda v: tuple(coerce(b, BlockParams) for b in v),
+    (HeatViTParams, "selectors"): lambda v: tuple(coerce(s, SelectorParams) for s in v),
+    (BlockParams, "mhsa"): lambda v: coerce(v, MhsaParams),
+    (BlockParams, "ffn"): lambda v: coerce(v, FfnParams),
+    (SelectorParams, "local"): lambda v: coerce(v, SelectorLocalParams),
+    (SelectorParams, "score"): lambda v: coerce(v, SelectorScoreParams),
+    (SelectorParams, "head_weight"): lambda v: coerce(v, SelectorHeadWeightParams),
+}
+
+
+def coerce(obj, cls):
+    """`obj` as an instance of `cls` (one of the containers above).
+
+    An instance is returned unchanged.  Any other object is rebuilt from its
+    attributes of the same names -- the reference's own frozen dataclasses
+    (model.py:24-47, transformer.py:51-398, selector.py:111-222) or any
+    stand-in with those fields -- with nested containers converted alike and
+    every value validated as for a direct construction.  A missing field
+    that has no default raises TypeError."""
+    if isinstance(obj, cls):
+        return obj
+    kwargs = {}
+    for f in fields(cls):
+        if not hasattr(obj, f.name):
+            if f.default is MISSING and f.default_factory is MISSING:
+                raise TypeError(f"{type(obj).__name__} lacks field {f.name!r} of {cls.__name__}")
+            continue
+        v = getattr(obj, f.name)
+        conv = _NESTED.get((cls, f.name))
+        kwargs[f.name] = conv(v) if conv else v
+    return cls(**kwargs)
+
+
 SCALE_EXP_RANGE = (-32, 31)
 
 
@@ -319,5 +355,5 @@ def check_scale_exps(obj):
 __all__ = [
     "PatchParams", "MhsaParams", "FfnParams", "BlockParams", "SelectorLocalParams",
     "SelectorScoreParams", "SelectorHeadWeightParams", "SelectorParams", "HeatViTParams",
-    "check_scale_exps", "field",
+    "check_scale_exps", "coerce", "field",
 ]

@@ -14,7 +14,6 @@ import torch
 
 from . import _lib
 from .device import DeviceSelector
-from .params import SelectorParams
 
 WARN_HEAD_DEN_ZERO = 1 << 0
 WARN_PACKAGE_DEN_ZERO = 1 << 1
@@ -47,10 +46,8 @@ def _stream():
 def token_selector_batch(token_sets, package_flags, params):
     if isinstance(params, DeviceSelector):
         dev = params
-    elif isinstance(params, SelectorParams):
-        dev = DeviceSelector(params)
     else:
-        raise TypeError("params must be SelectorParams")
+        dev = DeviceSelector(params)
     sets = []
     for t in token_sets:
         a = np.asarray(t.cpu().numpy() if isinstance(t, torch.Tensor) else t)

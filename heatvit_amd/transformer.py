@@ -14,7 +14,7 @@ import torch
 
 from . import _lib
 from .device import DeviceBlock, _Holder, _patch_struct
-from .params import BlockParams, PatchParams, check_scale_exps
+from .params import PatchParams, check_scale_exps, coerce
 
 
 def _stream():
@@ -38,8 +38,7 @@ def patch_embedding(image, params, *, batch=False):
     """NHWC image(s) -> [197][192] int8 at tokens_scale_exp.  With
     batch=True, `image` is [B][224*224*3] (or [B][224][224][3]) and the
     result is [B][197][192]."""
-    if not isinstance(params, PatchParams):
-        raise TypeError("params must be PatchParams")
+    params = coerce(params, PatchParams)
     check_scale_exps(params)
     if (params.width, params.height, params.patch) != (224, 224, 16):
         raise ValueError("the HIP patch embedding handles 224x224x3 images with 16x16 patches")
@@ -70,10 +69,8 @@ def transformer_block_batch(xs, params, checkpoints=False, warnings=False):
     (WARN_LN_NEGATIVE_VARIANCE when LN1 or LN2 clamped a row's variance)."""
     if isinstance(params, DeviceBlock):
         dev = params
-    elif isinstance(params, BlockParams):
-        dev = DeviceBlock(params)
     else:
-        raise TypeError("params must be BlockParams")
+        dev = DeviceBlock(params)
     xs = [_rows_i8("x", x) for x in xs]
     lens = [len(x) for x in xs]
     if not xs or any(n < 1 or n > 197 for n in lens):

@@ -95,7 +95,7 @@ int hv_eval_primitive(int op, const int64_t *in, int64_t *out, int64_t n, int a,
 
 /* Softmax over ragged rows (nonlinear.py:109-133): row r is
  * x[offsets[r] .. offsets[r+1]); writes the attention UQ0.8 bytes and the
- * selector Q0.16 values.  Row length <= 256. */
+ * selector Q0.16 values (either output may be NULL).  Row length <= 256. */
 int hv_softmax_rows(const int32_t *x, const int32_t *offsets, int rows, uint8_t *attention,
                     int32_t *selector, hv_stream_t stream);
 
@@ -286,6 +286,7 @@ typedef struct {
   int32_t *head_scores;  /* [B][3][196]     */
   int8_t *head_stats;    /* [B][196][3]     */
   int32_t *head_weights; /* [B][196][3]     */
+  int8_t *h2;            /* [B][3][196][16]: score MLP layer 2 (selector.py:307-335), 16-byte aligned */
 } hv_selector_ckpt;
 
 size_t hv_selector_workspace_bytes(int batch);
@@ -298,7 +299,8 @@ int hv_selector_forward(const hv_selector_dev *p, const int8_t *tokens, const in
 /* selector.finalize_tokens (selector.py:421-500) from given fused scores
  * fused [B][196] (Q0.16, candidate c of image b at b*196 + c; the last
  * candidate is the incoming package when pkg_in[b]); outputs as in
- * hv_selector_forward. */
+ * hv_selector_forward.  An image with a score outside [0, 65536] is
+ * rejected (state token count -1), as selector._q016 raises ValueError. */
 int hv_selector_finalize(const int8_t *tokens, const int32_t *offsets, const uint8_t *pkg_in,
                          const int32_t *fused, int batch, int8_t *out_tokens,
                          int32_t *out_offsets, uint8_t *pkg_out, int32_t *kept_index,

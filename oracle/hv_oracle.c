@@ -695,6 +695,7 @@ int hvo_token_selector(const int8_t *tokens, int n, int package_present,
               p->score_w1_exp, p->h1_out_exp, h1);
     gemm_gelu(h1, C, 32, p->w2 + (size_t)h * 32 * 16, p->b2 + h * 16, 16, p->h1_out_exp,
               p->score_w2_exp, p->h2_out_exp, h2);
+    if (ck && ck->h2) memcpy(ck->h2 + (size_t)h * C * 16, h2, (size_t)C * 16);
     hvo_gemm(h2, p->w3 + (size_t)h * 16 * 2, p->b3 + h * 2, C, 2, 16, 0, 0, acc);
     for (int c = 0; c < C; c++) {
       int32_t q[2], sm[2];

@@ -151,6 +151,7 @@ typedef struct {
   int8_t *head_stats;    /* [C][3] */
   int32_t *head_weights; /* [C][3] */
   int32_t *fused;        /* [C] */
+  int8_t *h2;            /* [3][C][16]: score MLP layer 2 (score_mlp_layers h2) */
 } hvo_selector_ckpt;
 
 typedef struct {

@@ -76,7 +76,7 @@ class BlockCkpt(C.Structure):
 
 class SelectorCkpt(C.Structure):
     _fields_ = [("local", _p8), ("global_", _p8), ("head_scores", _p32),
-                ("head_stats", _p8), ("head_weights", _p32), ("fused", _p32)]
+                ("head_stats", _p8), ("head_weights", _p32), ("fused", _p32), ("h2", _p8)]
 
 
 class SelectorState(C.Structure):
@@ -492,7 +492,7 @@ def finalize_tokens(cls, normal, incoming, scores):
 
 
 SELECTOR_KEYS = ("local", "global_features", "head_scores", "head_stats", "head_weights",
-                 "fused_scores")
+                 "fused_scores", "h2")
 
 
 def token_selector(tokens, package_present, sp, checkpoints=True):
@@ -506,10 +506,12 @@ def token_selector(tokens, package_present, sp, checkpoints=True):
     state = SelectorState()
     bufs = dict(local=np.zeros((3, c, 32), np.int8), global_features=np.zeros((3, 32), np.int8),
                 head_scores=np.zeros((3, c), np.int32), head_stats=np.zeros((c, 3), np.int8),
-                head_weights=np.zeros((c, 3), np.int32), fused_scores=np.zeros(c, np.int32))
+                head_weights=np.zeros((c, 3), np.int32), fused_scores=np.zeros(c, np.int32),
+                h2=np.zeros((3, c, 16), np.int8))
     ck = SelectorCkpt(_ptr(bufs["local"], _p8), _ptr(bufs["global_features"], _p8),
                       _ptr(bufs["head_scores"], _p32), _ptr(bufs["head_stats"], _p8),
-                      _ptr(bufs["head_weights"], _p32), _ptr(bufs["fused_scores"], _p32))
+                      _ptr(bufs["head_weights"], _p32), _ptr(bufs["fused_scores"], _p32),
+                      _ptr(bufs["h2"], _p8))
     _check(lib().hvo_token_selector(_ptr(tokens, _p8), n, int(bool(package_present)),
                                     C.byref(st), _ptr(out, _p8), _ptr(kept, _p32),
                                     C.byref(state), C.byref(ck) if checkpoints else None),

@@ -156,7 +156,7 @@ def test_throughput_batch_vs_oracle_and_deterministic(oracle):
 
 def test_unpruned_control_vs_oracle(oracle):
     from heatvit_amd.model import HeatViTModel
-    imgs, params = synth.throughput_workload(64)
+    imgs, params = synth.throughput_workload()  # all 256 images of the control
     ctrl = synth.unpruned_control(params)
     r = HeatViTModel().infer_batch(imgs, ctrl)
     logits, counts, status, warnings = oracle.model_infer_batch(imgs, ctrl)

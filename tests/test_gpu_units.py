@@ -95,23 +95,23 @@ def test_gemm_epilogues_vs_oracle(ops, oracle, m, n, k):
                               oracle.gemm_writeback(acc, src, dst, 8)), (src, dst)
     assert np.array_equal(ops.gemm_writeback(a, w, bias, -14, -14, 32),
                           oracle.gemm_writeback(acc, -14, -14, 32))
-    rows = slice(0, 96)  # the element-wise oracle checks below are scalar
-    # GELU post-op (transformer.py:349-358)
+    # GELU post-op (transformer.py:349-358), every element
     for src, dst in ((-14, -7), (-22, -5)):
-        q = oracle.requant_array(acc[rows], src, -16, 24)
+        q = oracle.requant_array(acc, src, -16, 24)
         want = oracle.requant_array(oracle.gelu_array(q).astype(np.int64), -16, dst, 8)
         got = ops.gemm_writeback(a, w, bias, src, dst, 8, epilogue="gelu")
-        assert np.array_equal(got[rows], want), (src, dst)
-    # residual align-add (transformer.py:96-101)
+        assert np.array_equal(got, want), (src, dst)
+    # residual align-add (transformer.py:96-101), every element: the aligned
+    # sum stays below 2^58 for these exponents, so int64 holds it exactly
     res = rng.integers(-128, 128, (m, n))
     for mid, rexp, out in ((-7, -6, -7), (-9, -4, -5), (-30, 20, -3)):
-        t = oracle.gemm_writeback(acc[rows], -14, mid, 8).astype(np.int64)
+        t = oracle.gemm_writeback(acc, -14, mid, 8).astype(np.int64)
         c = min(rexp, mid)
-        want = np.vectorize(lambda r, tt: oracle.requant(
-            (int(r) << (rexp - c)) + (int(tt) << (mid - c)), c, out, 8))(res[rows], t)
+        aligned = (res.astype(np.int64) << (rexp - c)) + (t << (mid - c))
+        want = oracle.requant_array(aligned, c, out, 8)
         got = ops.gemm_writeback(a, w, bias, -14, out, 8, epilogue="residual", mid_exp=mid,
                                  residual=res, res_exp=rexp)
-        assert np.array_equal(got[rows], want), (mid, rexp, out)
+        assert np.array_equal(got, want.reshape(got.shape)), (mid, rexp, out)
 
 
 def test_gemm_gather_rows(ops, oracle):

@@ -137,6 +137,13 @@ def test_mutated_roms(L):
     expect(lambda w: set_field(w[4], 204, 32, 0x1004), _lib.HV_ERR_ADDRESS)   # src0 offset
     expect(lambda w: set_field(w[4], 70, 6, 5), _lib.HV_ERR_DIMENSION)        # QKV s0 chain
     expect(lambda w: set_field(w[3], 256, 16, 64), _lib.HV_ERR_DIMENSION)     # LN over 64
+    # weight GEMMs (patch 1, QKV 4, proj 10, selector-1 local 42, its score
+    # layer 3 47, head-weight 50) with transposed or swapped operands, an
+    # unsigned activation or an int32 output; the classifier without int32
+    for idx in (1, 4, 10, 42, 47, 50):
+        for flag in (0, 4, 7, 18):
+            expect(lambda w: set_field(w[idx], 288 + flag, 1, 1), _lib.HV_ERR_DIMENSION)
+    expect(lambda w: set_field(w[len(w) - 2], 288 + 7, 1, 0), _lib.HV_ERR_DIMENSION)
     rc, cls, _ = compile_words(L, base[:150])                                  # truncated
     assert rc == _lib.HV_EVALUE and cls == _lib.HV_ERR_OPCODE
     rc, cls, _ = compile_words(L, np.concatenate([base, base[-1:]]))          # after FINISH
