@@ -21,6 +21,7 @@ HV_PRIM_GELU_POST, HV_PRIM_GELU_TABLE = 4, 5
 GELU_TABLE_SO = range(3, 13)
 HV_EPI_I8, HV_EPI_I32, HV_EPI_GELU, HV_EPI_RESIDUAL = 0, 1, 2, 3
 HV_A_ROWS, HV_A_GATHER = 0, 1
+HV_SELECTOR_NOALLOC_MAX_BATCH = 1024
 ABI_VERSION = 5
 PROF_CLASSES = ("patch", "layernorm", "gemm_qkv", "attention", "gemm_proj", "gemm_ffn1",
                 "gemm_ffn2", "selector", "head", "other")
@@ -146,6 +147,9 @@ def _declare(L):
     L.hv_selector_forward.argtypes = [C.POINTER(SelectorDev), _vp, _vp, _vp, C.c_int, _vp, _vp,
                                       _vp, _vp, _vp, _vp, C.POINTER(SelectorCkpt), _vp,
                                       C.c_size_t, _vp]
+    L.hv_selector_forward_noalloc.argtypes = [C.POINTER(SelectorDev), _vp, _vp, _vp, C.c_int,
+                                              _vp, _vp, _vp, _vp, _vp, _vp,
+                                              C.POINTER(SelectorCkpt), _vp]
     L.hv_selector_finalize.argtypes = [_vp, _vp, _vp, _vp, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp]
     L.hv_patch_embedding.argtypes = [C.POINTER(PatchDev), _vp, C.c_int, _vp, _vp]
     L.hv_model_workspace_bytes.restype = C.c_size_t
@@ -182,7 +186,8 @@ def exported_symbols():
     return ("hv_last_error", "hv_last_error_class", "hv_abi_version", "hv_eval_primitive",
             "hv_softmax_rows",
             "hv_layernorm_i8", "hv_attention_i8", "hv_gemm_i8", "hv_block_workspace_bytes", "hv_block_forward",
-            "hv_selector_workspace_bytes", "hv_selector_forward", "hv_selector_finalize",
+            "hv_selector_workspace_bytes", "hv_selector_forward", "hv_selector_forward_noalloc",
+            "hv_selector_finalize",
             "hv_patch_embedding", "hv_profile_enable", "hv_profile_read",
             "hv_model_workspace_bytes", "hv_model_forward", "hv_model_forward_f32",
             "hv_quantize_images", "hv_schedule_compile", "hv_schedule_packed_bytes",

@@ -4,6 +4,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <vector>
 
 #include "hv_device.h"
@@ -410,6 +411,66 @@ int hv_selector_forward(const hv_selector_dev *p, const int8_t *tokens, const in
   a.kept_index = kept_index; a.state = state;
   if (ck) a.ck = *ck;
   return launch_selector(a, (hipStream_t)stream);
+}
+
+}  // extern "C"
+
+namespace hv {
+// Scratch of hv_selector_forward_noalloc: the selector workspace carved for
+// HV_SELECTOR_NOALLOC_MAX_BATCH images.  Host code never uses the array's
+// name as an address: each device's copy is found once with
+// hipGetSymbolAddress (with that device current) and kept per device.
+static constexpr size_t kNoAllocScratchBytes = 3 * 1024 * 1024;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+static constexpr int kMaxDevices = 64;
+static void *g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+static int noalloc_scratch(void **out) {
+  int dev = -1;
+  int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (rc) return rc;
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(HV_EVALUE, HV_ERR_DIMENSION, "selector noalloc: device %d beyond %d", dev,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *ptr = nullptr;
+    rc = check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress");
+    if (rc) return rc;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return HV_OK;
+}
+}  // namespace hv
+
+extern "C" {
+
+int hv_selector_forward_noalloc(const hv_selector_dev *p, const int8_t *tokens,
+                                const int32_t *offsets, const uint8_t *pkg_in, int batch,
+                                int8_t *out_tokens, int32_t *out_offsets, uint8_t *pkg_out,
+                                int32_t *fused, int32_t *kept_index, int32_t *state,
+                                const hv_selector_ckpt *ck, hv_stream_t stream) {
+  clear_error();
+  if (batch > HV_SELECTOR_NOALLOC_MAX_BATCH)
+    return fail(HV_EVALUE, HV_ERR_DIMENSION,
+                "selector noalloc: batch %d exceeds the fixed scratch's %d images", batch,
+                HV_SELECTOR_NOALLOC_MAX_BATCH);
+  static_assert(kNoAllocScratchBytes >= (size_t)HV_SELECTOR_NOALLOC_MAX_BATCH * 196 * 3 * 5 + 512,
+                "scratch holds the selector workspace of the largest batch");
+  if (batch <= 0) return hv_selector_forward(p, tokens, offsets, pkg_in, batch, out_tokens,
+                                             out_offsets, pkg_out, fused, kept_index, state, ck,
+                                             nullptr, 0, stream);
+  void *ws = nullptr;
+  int rc = noalloc_scratch(&ws);
+  if (rc) return rc;
+  const size_t need = hv_selector_workspace_bytes(batch);
+  if (need > kNoAllocScratchBytes)
+    return fail(HV_EVALUE, HV_ERR_DIMENSION, "selector noalloc: workspace %zu > scratch %zu",
+                need, kNoAllocScratchBytes);
+  return hv_selector_forward(p, tokens, offsets, pkg_in, batch, out_tokens, out_offsets, pkg_out,
+                             fused, kept_index, state, ck, ws, kNoAllocScratchBytes, stream);
 }
 
 int hv_selector_finalize(const int8_t *tokens, const int32_t *offsets, const uint8_t *pkg_in,

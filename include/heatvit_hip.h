@@ -296,6 +296,22 @@ int hv_selector_forward(const hv_selector_dev *p, const int8_t *tokens, const in
                         int32_t *kept_index, int32_t *state, const hv_selector_ckpt *ck,
                         void *workspace, size_t workspace_bytes, hv_stream_t stream);
 
+/* hv_selector_forward with no workspace argument and no allocation: the
+ * head scores and statistics live in a fixed device array of the library
+ * (about 3 MB per GPU, held until the process ends), so callers that cannot
+ * call hipMalloc (code under HIP graph capture, serving loops, harnesses
+ * that forbid allocation) can run the selector.  No counterpart in the
+ * reference.  batch <= HV_SELECTOR_NOALLOC_MAX_BATCH (HV_EVALUE /
+ * HV_ERR_DIMENSION beyond).  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (different streams or threads) race.
+ * Nothing in the array needs clearing between calls. */
+#define HV_SELECTOR_NOALLOC_MAX_BATCH 1024
+int hv_selector_forward_noalloc(const hv_selector_dev *p, const int8_t *tokens,
+                                const int32_t *offsets, const uint8_t *pkg_in, int batch,
+                                int8_t *out_tokens, int32_t *out_offsets, uint8_t *pkg_out,
+                                int32_t *fused, int32_t *kept_index, int32_t *state,
+                                const hv_selector_ckpt *ck, hv_stream_t stream);
+
 /* selector.finalize_tokens (selector.py:421-500) from given fused scores
  * fused [B][196] (Q0.16, candidate c of image b at b*196 + c; the last
  * candidate is the incoming package when pkg_in[b]); outputs as in
