@@ -37,6 +37,7 @@ class SelectorResult:
     head_weights: np.ndarray = None
     fused_scores: np.ndarray = None
     kept_index: np.ndarray = None
+    h2: np.ndarray = None  # [3][C][16] second score-MLP layer (selector.py:307-335)
 
 
 def _stream():
@@ -86,9 +87,10 @@ def token_selector_batch(token_sets, package_flags, params):
                    head_stats=torch.zeros((b, MAX_CANDIDATES, 3), dtype=torch.int8,
                                           device="cuda"),
                    head_weights=torch.zeros((b, MAX_CANDIDATES, 3), dtype=torch.int32,
-                                            device="cuda"))
+                                            device="cuda"),
+                   h2=torch.zeros((b, 3, MAX_CANDIDATES, 16), dtype=torch.int8, device="cuda"))
     ck = _lib.SelectorCkpt(*[ck_bufs[k].data_ptr() for k in (
-        "local", "global_", "head_scores", "head_stats", "head_weights")])
+        "local", "global_", "head_scores", "head_stats", "head_weights", "h2")])
     L = _lib.lib()
     ws = torch.empty(max(1, L.hv_selector_workspace_bytes(b)), dtype=torch.uint8, device="cuda")
     _lib.check(L.hv_selector_forward(dev.struct, dev_in.data_ptr(), off.data_ptr(),
@@ -112,7 +114,8 @@ def token_selector_batch(token_sets, package_flags, params):
             head_scores=host["head_scores"][i, :, :c].copy(),
             head_stats=host["head_stats"][i, :c].copy(),
             head_weights=host["head_weights"][i, :c].copy(),
-            fused_scores=fused[i, :c].copy(), kept_index=kept[i, :state[i, 2]].copy()))
+            fused_scores=fused[i, :c].copy(), kept_index=kept[i, :state[i, 2]].copy(),
+            h2=host["h2"][i, :, :c].copy()))
     return results
 
 
