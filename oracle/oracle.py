@@ -86,7 +86,10 @@ class SelectorState(C.Structure):
 
 
 def build(force=False):
-    """Compile liboracle.so with the committed Makefile."""
+    """Compile liboracle.so with the committed Makefile (with
+    HEATVIT_ORACLE_LIB set, that library is used as built)."""
+    if os.environ.get("HEATVIT_ORACLE_LIB"):
+        return
     if force or not LIB_PATH.exists():
         subprocess.run(["make", "-s", "-B" if force else "liboracle.so"], cwd=HERE,
                        check=True)
@@ -98,9 +101,12 @@ _LIB = None
 def lib():
     global _LIB
     if _LIB is None:
-        if not LIB_PATH.exists():
-            build()
-        L = C.CDLL(str(LIB_PATH))
+        path = os.environ.get("HEATVIT_ORACLE_LIB")
+        if not path:
+            if not LIB_PATH.exists():
+                build()
+            path = str(LIB_PATH)
+        L = C.CDLL(path)
         L.hvo_round_shift_away.restype = C.c_int64
         L.hvo_round_shift_away.argtypes = [C.c_int64, C.c_int]
         L.hvo_sat_signed.restype = C.c_int64
