@@ -295,6 +295,19 @@ __host__ __device__ __forceinline__ unsigned softmax_exp(int xt) {
   return e >> (z < 31u ? z : 31u);
 }
 
+// The same exponential from nx = -x_tilde >= 0 (the row maximum minus the
+// element) in 24-bit multiply-adds: beyond 17 * 45426 the result is 0 (e <
+// 2^17 shifted by z >= 17), so nx is clamped there, z = nx / 45426 <= 17
+// needs no further clamp, s = 88670 - nx + 45426 z lies in (43244, 88670],
+// its square is one 32x32->64 multiply-add and 23495 * square < 2^32.
+__host__ __device__ __forceinline__ unsigned softmax_exp_nx(unsigned nx) {
+  const unsigned n = nx < 17u * 45426u ? nx : 17u * 45426u;
+  const unsigned z = n / 45426u;
+  const unsigned s = mul_u24(z, 45426u) + (88670u - n);
+  const unsigned square = (unsigned)(((u64)s * s + 32768u) >> 16);
+  return (((mul_u24(23495u, square) + 32768u) >> 16) + 22544u) >> z;
+}
+
 // round_div(2^32, sum) for a row sum that includes exp(0) = 65554, so
 // 65554 <= sum < 2^32 and the result is below 2^17 (nonlinear.py:119):
 // float estimate, exact correction on the remainder.

@@ -215,8 +215,8 @@ int launch_layernorm(const int8_t *x, const int8_t *g, const int8_t *b, int8_t *
 // four per dword they are exactly the B operand of ctx^T = V^T P^T once V^T
 // is stored in LDS with the matching key order (key 16t + 4g + i of a
 // 64-key chunk at byte 16g + 4t + i).  P is unsigned and the MFMA signed,
-// so P = 2*(P >> 1) + (P & 1) runs as two products with int8 operands;
-// |ctx| <= 197*128*255 < 2^23.  Lane l then holds four consecutive context
+// so the bytes enter as P - 128 and the product is corrected by 128 times
+// the per-channel key sum of V; |ctx| <= 197*128*255 < 2^23.  Lane l then holds four consecutive context
 // channels of query l%16 and stores them as one dword.  V^T is built with
 // 4x4 byte transposes in registers (dword LDS stores).
 // ---------------------------------------------------------------------------
@@ -240,7 +240,8 @@ template <int MODE>
 __device__ __forceinline__ int attn_q16(int acc, const AttnArgs &g) {
   int r;
   if (MODE == 0) {
-    r = (acc + g.q16_rnd + (acc >> 31)) >> g.q16_s;
+    // a right shift by s >= 1 of |acc| <= 2^20 stays inside 24 bits
+    return (acc + g.q16_rnd + (acc >> 31)) >> g.q16_s;
   } else if (MODE == 1) {
     r = acc * (1 << g.q16_s);
   } else {
@@ -257,10 +258,118 @@ __device__ __noinline__ int attn_ctx_general(int v, int ctx_shift) {
   return (int)requant_shift(v, ctx_shift, 8);
 }
 
+// The query tiles of one wavefront for an image of NT key tiles (N in
+// (16 (NT - 1), 16 NT]): straight-line code per tile count, so the score
+// MFMAs issue back to back and only the last tile masks padded keys.
+template <int MODE, bool CKPT, int NT>
+__device__ __forceinline__ void attn_tiles(const AttnArgs &g, const int8_t *Ks, const int8_t *Vt,
+                                           const int *vsum, const int8_t *qkv, int b, int h, int N,
+                                           int row0, int wave, int lane) {
+  constexpr int NC = (NT + 3) / 4;  // PV chunks of 64 keys
+  const int ql = lane & 15, grp = lane >> 4;
+  const int kvalid = N - 16 * (NT - 1) - 4 * grp;  // valid keys i < kvalid in the last tile
+  // Query tiles round-robin over the wavefronts, rotated by workgroup so
+  // the wavefront that gets the extra tile sits on a different SIMD in
+  // neighbouring workgroups.
+  for (int qt = (wave + blockIdx.x) & 3; qt < NT; qt += 4) {
+    const int q = qt * 16 + ql;  // this lane's query
+    v4i qb = v4i{0};
+    if (q < N) qb = *reinterpret_cast<const v4i *>(qkv + (size_t)q * 576 + h * 64 + grp * 16);
+    // S^T tiles: lane holds keys 16 kt + 4 grp + i of query ql.
+    v4i st[NT];
+#pragma unroll
+    for (int kt = 0; kt < NT; ++kt) {
+      const v4i ka = *reinterpret_cast<const v4i *>(&Ks[(kt * 16 + ql) * kKStride + grp * 16]);
+      st[kt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ka, qb, v4i{0}, 0, 0, 0);
+    }
+    // Q8.16 scores; padded keys (only in the last tile) get -2^30, below
+    // every score, so their exponential is exactly zero.
+    int mx = -(1 << 30);
+#pragma unroll
+    for (int kt = 0; kt < NT; ++kt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (CKPT && g.score && q < N && kt * 16 + 4 * grp + i < N)
+          g.score[(((size_t)b * 3 + h) * 197 + q) * 197 + kt * 16 + 4 * grp + i] =
+              attn_score_ckpt(st[kt][i], g.score_shift);
+        int v = attn_q16<MODE>(st[kt][i], g);
+        if (kt == NT - 1) v = i < kvalid ? v : -(1 << 30);
+        st[kt][i] = v;
+      }
+      mx = max(mx, max(max(st[kt][0], st[kt][1]), max(st[kt][2], st[kt][3])));
+    }
+    mx = max(mx, __shfl_xor(mx, 16));
+    mx = max(mx, __shfl_xor(mx, 32));
+    unsigned sum = 0;
+#pragma unroll
+    for (int kt = 0; kt < NT; ++kt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const unsigned e = softmax_exp_nx((unsigned)(mx - st[kt][i]));
+        st[kt][i] = (int)e;
+        sum += e;
+      }
+    }
+    sum += __shfl_xor(sum, 16);
+    sum += __shfl_xor(sum, 32);
+    const unsigned recip = softmax_recip24(sum);  // sum <= 197 * 65554 < 2^24
+    v4i pk[NC];
+#pragma unroll
+    for (int kc = 0; kc < NC; ++kc) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int kt = kc * 4 + t;
+        unsigned w = 0;
+        if (kt < NT) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            // min(rsa(rsa(e * recip, 16), 8), 255) with one rounding: the
+            // first rounding's discarded bits cannot carry past a multiple
+            // of 2^8, so it equals (e * recip + 2^15 + 2^23) >> 24.
+            const u64 pr = (u64)(unsigned)st[kt][i] * recip + (32768u + (1u << 23));
+            const unsigned p = min((unsigned)(pr >> 24), 255u);
+            w |= p << (8 * i);
+            if (CKPT && g.prob && q < N && kt * 16 + 4 * grp + i < N)
+              g.prob[(((size_t)b * 3 + h) * 197 + q) * 197 + kt * 16 + 4 * grp + i] = (uint8_t)p;
+          }
+        }
+        pk[kc][t] = (int)(w ^ 0x80808080u);  // bytes P - 128
+        // keeps the scheduler from hoisting every tile's 64-bit products
+        // at once (register pressure, spills)
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      v4i acc = v4i{0};
+#pragma unroll
+      for (int kc = 0; kc < NC; ++kc) {
+        const v4i va = *reinterpret_cast<const v4i *>(&Vt[(dt * 16 + ql) * kVStride + kc * 64 + grp * 16]);
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(va, pk[kc], acc, 0, 0, 0);
+      }
+      if (q < N) {
+        const v4i cs = *reinterpret_cast<const v4i *>(&vsum[dt * 16 + 4 * grp]);
+        int word = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int v = acc[i] + cs[i];
+          const int o = g.ctx_fast ? min(max((v + g.ctx_rnd + (v >> 31)) >> g.ctx_shift, -128), 127)
+                                   : attn_ctx_general(v, g.ctx_shift);
+          word |= (o & 0xFF) << (8 * i);
+        }
+        *reinterpret_cast<int *>(g.ctx + (size_t)(row0 + q) * 192 + h * 64 + dt * 16 + 4 * grp) = word;
+      }
+    }
+  }
+}
+
+// At most 168 VGPRs (three workgroups per CU): the 768 items of a 256-image
+// batch then run in one round.
 template <int MODE, bool CKPT>
-__global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
+__global__ __launch_bounds__(256, 3) void k_attention(AttnArgs g) {
   __shared__ __attribute__((aligned(16))) int8_t Ks[kMaxKeys * kKStride];
   __shared__ __attribute__((aligned(16))) int8_t Vt[64 * kVStride];
+  __shared__ __attribute__((aligned(16))) int vsum[64];  // 128 * sum_k V[k][d]
 
   // The grid is a multiple of 8 and workgroups go round-robin over the 8
   // XCDs, so XCD x runs logical items [x*T8, (x+1)*T8): the three heads of
@@ -307,99 +416,25 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
       }
   }
   __syncthreads();
+  // The probabilities enter P V as the signed bytes P - 128: P V =
+  // (P - 128) V + 128 sum_k V[k], one MFMA per tile instead of two.  The
+  // per-channel sums run over the zero-padded keys too.
+  if (tid < 64) {
+    const int *row = reinterpret_cast<const int *>(&Vt[tid * kVStride]);
+    int sv = 0;
+    for (int w = 0; w < n64 * 16; ++w) sv = __builtin_amdgcn_sdot4(row[w], 0x01010101, sv, false);
+    vsum[tid] = sv * 128;
+  }
+  __syncthreads();
 
-  const int ql = lane & 15, grp = lane >> 4;
-  // Query tiles round-robin over the wavefronts, rotated by workgroup so
-  // the wavefront that gets the extra tile sits on a different SIMD in
-  // neighbouring workgroups.
-  for (int qt = (wave + blockIdx.x) & 3; qt < n16; qt += 4) {
-    const int q = qt * 16 + ql;  // this lane's query
-    v4i qb = v4i{0};
-    if (q < N) qb = *reinterpret_cast<const v4i *>(qkv + (size_t)q * 576 + h * 64 + grp * 16);
-    int val[13][4];
-    int mx = -(1 << 30);
-#pragma unroll
-    for (int kt = 0; kt < 13; ++kt) {
-      if (kt < n16) {
-        const v4i ka = *reinterpret_cast<const v4i *>(&Ks[(kt * 16 + ql) * kKStride + grp * 16]);
-        const v4i st = __builtin_amdgcn_mfma_i32_16x16x64_i8(ka, qb, v4i{0}, 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = kt * 16 + 4 * grp + i;
-          // Padded keys get -2^30: below every q16 value, and their
-          // exponential is exactly zero (z > 31), so the later passes need no mask.
-          const int v = key < N ? attn_q16<MODE>(st[i], g) : -(1 << 30);
-          val[kt][i] = v;
-          mx = v > mx ? v : mx;
-          if (CKPT && g.score && q < N && key < N)
-            g.score[(((size_t)b * 3 + h) * 197 + q) * 197 + key] = attn_score_ckpt(st[i], g.score_shift);
-        }
-      }
-    }
-    mx = max(mx, __shfl_xor(mx, 16));
-    mx = max(mx, __shfl_xor(mx, 32));
-    unsigned sum = 0;
-#pragma unroll
-    for (int kt = 0; kt < 13; ++kt) {
-      if (kt < n16) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const unsigned e = softmax_exp(val[kt][i] - mx);
-          val[kt][i] = (int)e;
-          sum += e;
-        }
-      }
-    }
-    sum += __shfl_xor(sum, 16);
-    sum += __shfl_xor(sum, 32);
-    const unsigned recip = softmax_recip24(sum);  // sum <= 197 * 65554 < 2^24
-    v4i pk_hi[4], pk_lo[4];
-#pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int kt = kc * 4 + t;
-        unsigned w = 0;
-        if (kt < 13 && kt < n16) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            // min(rsa(rsa(e * recip, 16), 8), 255) with one rounding: the
-            // first rounding's discarded bits cannot carry past a multiple
-            // of 2^8, so it equals (e * recip + 2^15 + 2^23) >> 24.
-            const u64 pr = (u64)(unsigned)val[kt][i] * recip + (32768u + (1u << 23));
-            const unsigned p = min((unsigned)(pr >> 24), 255u);
-            w |= p << (8 * i);
-            if (CKPT && g.prob && q < N && kt * 16 + 4 * grp + i < N)
-              g.prob[(((size_t)b * 3 + h) * 197 + q) * 197 + kt * 16 + 4 * grp + i] = (uint8_t)p;
-          }
-        }
-        pk_hi[kc][t] = (int)((w >> 1) & 0x7F7F7F7Fu);
-        pk_lo[kc][t] = (int)(w & 0x01010101u);
-      }
-    }
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      v4i ahi = v4i{0}, alo = v4i{0};
-#pragma unroll
-      for (int kc = 0; kc < 4; ++kc) {
-        if (kc < n64) {
-          const v4i va = *reinterpret_cast<const v4i *>(&Vt[(dt * 16 + ql) * kVStride + kc * 64 + grp * 16]);
-          ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(va, pk_hi[kc], ahi, 0, 0, 0);
-          alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(va, pk_lo[kc], alo, 0, 0, 0);
-        }
-      }
-      if (q < N) {
-        int word = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int v = 2 * ahi[i] + alo[i];
-          const int o = g.ctx_fast ? min(max((v + g.ctx_rnd + (v >> 31)) >> g.ctx_shift, -128), 127)
-                                   : attn_ctx_general(v, g.ctx_shift);
-          word |= (o & 0xFF) << (8 * i);
-        }
-        *reinterpret_cast<int *>(g.ctx + (size_t)(row0 + q) * 192 + h * 64 + dt * 16 + 4 * grp) = word;
-      }
-    }
+  switch (n16) {
+#define HV_ATTN_CASE(n) \
+    case n: attn_tiles<MODE, CKPT, n>(g, Ks, Vt, vsum, qkv, b, h, N, row0, wave, lane); break;
+    HV_ATTN_CASE(1) HV_ATTN_CASE(2) HV_ATTN_CASE(3) HV_ATTN_CASE(4) HV_ATTN_CASE(5)
+    HV_ATTN_CASE(6) HV_ATTN_CASE(7) HV_ATTN_CASE(8) HV_ATTN_CASE(9) HV_ATTN_CASE(10)
+    HV_ATTN_CASE(11) HV_ATTN_CASE(12) HV_ATTN_CASE(13)
+#undef HV_ATTN_CASE
+    default: break;
   }
 }
 

@@ -72,6 +72,22 @@ static long check_exp() {
   return bad;
 }
 
+// softmax_exp_nx(nx) against the oracle's exp of -nx for every nx in
+// [0, 2^25] and a million larger values up to 2^31 - 1.
+static long check_exp_nx() {
+  long bad = 0;
+  for (unsigned nx = 0; nx <= (1u << 25); ++nx)
+    if ((long long)softmax_exp_nx(nx) != hvo_softmax_exp(-(long long)nx))
+      if (++bad < 5) std::printf("softmax_exp_nx mismatch at %u\n", nx);
+  std::mt19937_64 rng(10);
+  for (int i = 0; i < 1000000; ++i) {
+    const unsigned nx = (unsigned)(rng() % 2147483648u);
+    if ((long long)softmax_exp_nx(nx) != hvo_softmax_exp(-(long long)nx))
+      if (++bad < 5) std::printf("softmax_exp_nx mismatch at %u\n", nx);
+  }
+  return bad;
+}
+
 static long check_softmax(int rows) {
   std::mt19937_64 rng(3);
   int32_t x[256], ref_sel[256];
@@ -151,7 +167,8 @@ static long check_layernorm(int rows) {
 
 int main(int argc, char **argv) {
   const int rows = argc > 1 ? std::atoi(argv[1]) : 100000;
-  const long g = check_gelu(), s = check_softmax(rows) + check_recip24() + check_exp(),
+  const long g = check_gelu(),
+             s = check_softmax(rows) + check_recip24() + check_exp() + check_exp_nx(),
              l = check_layernorm(rows);
   std::printf("gelu_bad=%ld softmax_bad=%ld layernorm_bad=%ld\n", g, s, l);
   return (g || s || l) ? 1 : 0;
