@@ -70,6 +70,26 @@ def test_layernorm_random_rows_vs_oracle(ops, oracle):
         assert np.array_equal(out, oracle.layernorm_rows(x, g, b, *exps)), exps
 
 
+@pytest.mark.parametrize("rows", [40001, 9003, 257])
+def test_layernorm_row_groups_vs_oracle(ops, oracle, rows):
+    """The int32 LayerNorm shares each row's constants among R rows of an
+    8-lane group, R = 4 or 1 by the live row count (>= 32768 or
+    fewer); ragged tails, degenerate rows (constant, one outlier, extremes)
+    and negative-variance flags included."""
+    rng = np.random.default_rng(rows)
+    x = rng.integers(-128, 128, (rows, 192))
+    x[::7] = rng.integers(-128, 128, (len(x[::7]), 1))          # constant rows
+    x[3::11, 5] = 127                                          # one outlier
+    x[5::13] = rng.choice([-128, 127], (len(x[5::13]), 192))    # extremes
+    g = rng.integers(-128, 128, 192)
+    b = rng.integers(-128, 128, 192)
+    for exps in ((-7, -6, -7, -7), (-12, -5, -20, -9), (-16, -4, -20, -3), (-4, -8, -24, -2)):
+        out, neg = ops.layernorm_rows(x, g, b, *exps)
+        assert np.array_equal(out, oracle.layernorm_rows(x, g, b, *exps)), (rows, exps)
+        want_neg = [oracle.layernorm(x[r], g, b, *exps)[1] for r in range(0, rows, 997)]
+        assert [bool(v) for v in neg[::997]] == [bool(v) for v in want_neg], (rows, exps)
+
+
 def test_gemm_scenarios(ops):
     for sc in fx.gemm_scenarios():
         if sc["unsigned"]:
