@@ -3,11 +3,10 @@
 //
 // k_selector_head, one workgroup per (image, head): local MLP + head
 //   statistic (:253, :358), candidate mean (:273), concat + 64->32->16->2
-//   score MLP + 2-way selector softmax (:292, :307, :338).  Two adjacent
-//   lanes own one candidate, each computing half of every layer's outputs
-//   and swapping halves by a lane shuffle; the tiny GEMMs (K = 64/32/16)
-//   run on v_dot4_i32_i8 from LDS-held, output-major weights.  Head scores
-//   and statistics go to a workspace.
+//   score MLP + 2-way selector softmax (:292, :307, :338).  The MLP layers
+//   run as int8 MFMAs over tiles of 16 candidates with the weights and
+//   every intermediate in LDS; head scores and statistics go to a
+//   workspace.
 // k_selector_keep, one wavefront per image: head-weight MLP with PLAN
 //   (:370) and the head fuse (:392) per candidate (skipped when the fused
 //   scores are given), then the stable keep list (fused >= 32768) and the
@@ -45,21 +44,44 @@ __device__ __forceinline__ int sel_gelu(int acc, int bias, bool fast, const Rq &
   return gelu_exact(acc, bias, sh_in, sh_out);
 }
 
-constexpr int kHeadThreads = 512;  // two lanes per candidate, kMaxCand <= 256
 
-__global__ __launch_bounds__(kHeadThreads) void k_selector_head(hv_selector_dev p, const int8_t *tokens,
-                                                       const int32_t *offsets, int batch,
-                                                       const uint8_t *pkg_in, int32_t *hs_out,
-                                                       int8_t *stats_out, int fast_shifts,
-                                                       hv_selector_ckpt ck) {
-  __shared__ int wl[32 * 16];   // local_wt[h] [32][64] as int words
-  __shared__ int w1[32 * 16];   // w1t[h] [32][64]
-  __shared__ int w2[16 * 8];    // w2t[h] [16][32]
-  __shared__ int w3[2 * 4];     // w3t[h] [2][16]
-  __shared__ int bl[32], bb1[32], bb2[16];
-  __shared__ int local_s[kMaxCand * 8];  // [C][32] int8 as words
-  __shared__ int glob[8];                 // [32] int8 as words
-  __shared__ int hbuf[kHeadThreads];      // partial channel sums of the candidate mean
+// The same with a 64-bit bias (score layer 1 after its global half is
+// folded into the bias, below).
+__device__ __noinline__ int gelu_exact64(int acc, i64 bias, int sh_in, int sh_out) {
+  return gelu_post((i64)acc + bias, sh_in, sh_out);
+}
+
+constexpr int kHeadThreads = 256;
+constexpr int kCandTiles = (kMaxCand + 15) / 16;  // 13 tiles of 16 candidates
+constexpr int kCandPad = kCandTiles * 16;
+
+// One workgroup per (image, head).  The three MLP layers run as int8 MFMAs
+// over tiles of 16 candidates, with the weights (output-major, as stored)
+// and every intermediate in LDS:
+//   local = GELU(x_h [C][64] . Wl [64][32] + bl)          16x16x64, 2 column tiles
+//   h1    = GELU(local . W1[0:32] + b1')                  16x16x32, 2 column tiles
+//   h2    = GELU(h1 . W2 + b2)                            16x16x32, 1 column tile
+// where b1' = b1 + global . W1[32:64] (the global feature is the same for
+// every candidate, so the concat's second half is a per-head bias, exact in
+// 64 bits).  Result lane l of a tile holds output channel 16 ct + l % 16 of
+// candidates 4 (l / 16) + i.  The logits (16 -> 2), the 2-way softmax and
+// the lane mean of the head slice (the head statistic) are per candidate.
+__global__ __launch_bounds__(kHeadThreads) void k_selector_head(
+    hv_selector_dev p, const int8_t *tokens, const int32_t *offsets, int batch,
+    const uint8_t *pkg_in, int32_t *hs_out, int8_t *stats_out, int fast_shifts,
+    hv_selector_ckpt ck) {
+  __shared__ __attribute__((aligned(16))) int8_t wl[32 * 64];   // local_wt[h] [32][64]
+  __shared__ __attribute__((aligned(16))) int8_t w1[32 * 64];   // w1t[h] [32][64]
+  __shared__ __attribute__((aligned(16))) int8_t w2[16 * 32];   // w2t[h] [16][32]
+  __shared__ int w3[2 * 4];                                     // w3t[h] [2][16] as words
+  __shared__ int bl[32], bb2[16];
+  __shared__ i64 bb1[32];                                       // b1 + global . W1[32:64]
+  __shared__ __attribute__((aligned(16))) int8_t local_s[kCandPad * 32];
+  __shared__ __attribute__((aligned(16))) int8_t h1_s[kCandPad * 32];
+  __shared__ __attribute__((aligned(16))) int8_t h2_s[kCandPad * 16];
+  __shared__ int part[8 * 32];
+  __shared__ int glob_s[32];
+  __shared__ int fast_s[3];
 
   // The grid is a multiple of 8 and workgroups go round-robin over the 8
   // XCDs, so XCD x runs logical items [x*T8, (x+1)*T8): the three heads of
@@ -68,192 +90,167 @@ __global__ __launch_bounds__(kHeadThreads) void k_selector_head(hv_selector_dev 
   const int L = (blockIdx.x & 7) * T8 + (blockIdx.x >> 3);
   if (L >= T) return;
   const int b = L / 3, h = L - 3 * b, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6, col = lane & 15, grp = lane >> 4;
   const int row0 = offsets[b], N = offsets[b + 1] - row0, C = N - 1;
   const int pkg = pkg_in ? (pkg_in[b] ? 1 : 0) : 0;
   if (C < 1 || C > kMaxCand || C - pkg < 1 || row0 < 0) return;  // k_selector_keep reports
+  const int ntiles = (C + 15) >> 4;
 
   {
-    const int *src = reinterpret_cast<const int *>(p.local_wt) + h * 512;
-    for (int i = tid; i < 512; i += kHeadThreads) wl[i] = src[i];
-    src = reinterpret_cast<const int *>(p.w1t) + h * 512;
-    for (int i = tid; i < 512; i += kHeadThreads) w1[i] = src[i];
-    src = reinterpret_cast<const int *>(p.w2t) + h * 128;
-    if (tid < 128) w2[tid] = src[tid];
-    src = reinterpret_cast<const int *>(p.w3t) + h * 8;
-    if (tid < 8) w3[tid] = src[tid];
-    if (tid < 32) bl[tid] = p.local_b[h * 32 + tid];
-    if (tid < 32) bb1[tid] = p.b1[h * 32 + tid];
-    if (tid < 16) bb2[tid] = p.b2[h * 16 + tid];
+    const v4i *src = reinterpret_cast<const v4i *>(p.local_wt + h * 2048);
+    if (tid < 128) reinterpret_cast<v4i *>(wl)[tid] = src[tid];
+    src = reinterpret_cast<const v4i *>(p.w1t + h * 2048);
+    if (tid >= 128) reinterpret_cast<v4i *>(w1)[tid - 128] = src[tid - 128];
+    src = reinterpret_cast<const v4i *>(p.w2t + h * 512);
+    if (tid < 32) reinterpret_cast<v4i *>(w2)[tid] = src[tid];
+    if (tid >= 64 && tid < 72) w3[tid - 64] = reinterpret_cast<const int *>(p.w3t)[h * 8 + tid - 64];
+    if (tid >= 96 && tid < 128) bl[tid - 96] = p.local_b[h * 32 + tid - 96];
+    if (tid >= 160 && tid < 176) bb2[tid - 160] = p.b2[h * 16 + tid - 160];
   }
   __syncthreads();
-  // int32 GELU preconditions: |acc| <= K*2^14 with K = 64 (32 for layer 2).
-  bool fast = fast_shifts != 0;
-  {
-    const int lim64 = (1 << 30) - 1 - 64 * 16384, lim32 = (1 << 30) - 1 - 32 * 16384;
-#pragma unroll 4
-    for (int j = 0; j < 32; ++j)
-      fast = fast && bl[j] <= lim64 && bl[j] >= -lim64 && bb1[j] <= lim64 && bb1[j] >= -lim64;
-#pragma unroll 4
-    for (int j = 0; j < 16; ++j) fast = fast && bb2[j] <= lim32 && bb2[j] >= -lim32;
+  // int32 GELU preconditions: |acc| <= K*2^14 for the layer's K.
+  const int lim64 = (1 << 30) - 1 - 64 * 16384, lim32 = (1 << 30) - 1 - 32 * 16384;
+  if (tid < 2) {
+    bool f = fast_shifts != 0;
+    if (tid == 0)
+      for (int j = 0; j < 32; ++j) f = f && bl[j] <= lim64 && bl[j] >= -lim64;
+    else
+      for (int j = 0; j < 16; ++j) f = f && bb2[j] <= lim32 && bb2[j] >= -lim32;
+    fast_s[tid == 0 ? 0 : 2] = f;
   }
 
-  const int8_t *cand = tokens + (size_t)(row0 + 1) * 192;
-  // Stage 1: local MLP with GELU and the head lane mean.
+  const int8_t *cand = tokens + (size_t)(row0 + 1) * 192 + h * 64;
+  // Local MLP and head statistic.
   {
     const int sh_in = -16 - (p.in_exp + p.local_w_exp), sh_out = p.local_out_exp + 16;
     const Rq ra = rq_setup(sh_in, -(1 << 23), (1 << 23) - 1), rb = rq_setup(sh_out, -128, 127);
-    // LPC lanes per candidate: four when the candidates fit (shorter
-    // chains), else two.
-    auto stage1 = [&](auto lpc) {
-      constexpr int LPC = decltype(lpc)::value, WPL = 8 / LPC;  // output words per lane
-      const int sub = tid & (LPC - 1);
-      for (int c = tid / LPC; c < C; c += kHeadThreads / LPC) {
-        int x[16];
-        const v4i *src = reinterpret_cast<const v4i *>(cand + (size_t)c * 192 + h * 64);
+    __syncthreads();
+    const bool fast = fast_s[0];
+    for (int t = wave; t < ntiles * 2; t += 4) {
+      const int rt = t >> 1, ct = t & 1;
+      const int c = min(rt * 16 + col, C - 1);
+      const v4i a = *reinterpret_cast<const v4i *>(cand + (size_t)c * 192 + grp * 16);
+      const v4i wb = *reinterpret_cast<const v4i *>(&wl[(ct * 16 + col) * 64 + grp * 16]);
+      const v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, wb, v4i{0}, 0, 0, 0);
+      if (ct == 0) {
+        // lane mean of the candidate's 64 head lanes (selector.py:358-367)
+        int sum = 0;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const v4i v = src[k];
-          x[4 * k] = v[0]; x[4 * k + 1] = v[1]; x[4 * k + 2] = v[2]; x[4 * k + 3] = v[3];
-        }
-        if (sub == 0) {
-          int lane_sum = 0;
-#pragma unroll
-          for (int k = 0; k < 16; ++k) lane_sum = dot4(x[k], 0x01010101, lane_sum);
-          const int8_t stat = (int8_t)sat_bits(round_div_pos(lane_sum, 64), 8);
-          stats_out[((size_t)b * kMaxCand + c) * 3 + h] = stat;
-          if (ck.head_stats) ck.head_stats[((size_t)b * kMaxCand + c) * 3 + h] = stat;
-        }
-#pragma unroll 1
-        for (int jg = WPL * sub; jg < WPL * sub + WPL; ++jg) {
-          int word = 0;
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            const int j = jg * 4 + jj;
-            int acc = 0;
-            const int *w = &wl[j * 16];
-#pragma unroll
-            for (int k = 0; k < 16; ++k) acc = dot4(x[k], w[k], acc);
-            const int v = sel_gelu(acc, bl[j], fast, ra, rb, sh_in, sh_out);
-            word |= (v & 0xFF) << (8 * jj);
-          }
-          local_s[c * 8 + jg] = word;
-          if (ck.local)
-            reinterpret_cast<int *>(ck.local + (((size_t)b * 3 + h) * kMaxCand + c) * 32)[jg] = word;
+        for (int k = 0; k < 4; ++k) sum = dot4(a[k], 0x01010101, sum);
+        sum += __shfl_xor(sum, 16);
+        sum += __shfl_xor(sum, 32);
+        if (grp == 0 && rt * 16 + col < C) {
+          const int8_t stat = (int8_t)sat_bits(round_div_pos(sum, 64), 8);
+          const int cc = rt * 16 + col;
+          stats_out[((size_t)b * kMaxCand + cc) * 3 + h] = stat;
+          if (ck.head_stats) ck.head_stats[((size_t)b * kMaxCand + cc) * 3 + h] = stat;
         }
       }
-    };
-    if (C <= kHeadThreads / 4) stage1(std::integral_constant<int, 4>{});
-    else stage1(std::integral_constant<int, 2>{});
+      const int j = ct * 16 + col;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        local_s[(rt * 16 + grp * 4 + i) * 32 + j] =
+            (int8_t)sel_gelu(acc[i], bl[j], fast, ra, rb, sh_in, sh_out);
+    }
   }
   __syncthreads();
-  // Stage 2: global feature = sat8(round_div(sum_c local, C)); sixteen
-  // partial sums per channel, then one thread per channel.
+  // Global feature = sat8(round_div(sum_c local, C)) and the folded bias of
+  // score layer 1.
   {
-    constexpr int kParts = kHeadThreads / 32;
-    const int8_t *l8 = reinterpret_cast<const int8_t *>(local_s);
-    const int ch = tid & 31, part = tid >> 5;
-    int s = 0;
-    for (int c = part; c < C; c += kParts) s += l8[c * 32 + ch];
-    hbuf[tid] = s;
+    const int ch = tid & 31, prt = tid >> 5;
+    int sacc = 0;
+    for (int c = prt; c < C; c += 8) sacc += local_s[c * 32 + ch];
+    part[prt * 32 + ch] = sacc;
   }
   __syncthreads();
   if (tid < 32) {
-    int s = 0;
+    int sacc = 0;
 #pragma unroll
-    for (int part = 0; part < kHeadThreads / 32; ++part) s += hbuf[part * 32 + tid];
-    const int8_t gv = (int8_t)sat_bits(round_div_pos(s, C), 8);
-    reinterpret_cast<int8_t *>(glob)[tid] = gv;
-    if (ck.global) ck.global[((size_t)b * 3 + h) * 32 + tid] = gv;
+    for (int q = 0; q < 8; ++q) sacc += part[q * 32 + tid];
+    const int gv = (int)sat_bits(round_div_pos(sacc, C), 8);
+    glob_s[tid] = gv;
+    if (ck.global) ck.global[((size_t)b * 3 + h) * 32 + tid] = (int8_t)gv;
   }
   __syncthreads();
-  // Stage 3: score MLP on [local | global] and the 2-way selector softmax.
+  if (tid < 32) {
+    i64 v = p.b1[h * 32 + tid];
+#pragma unroll 8
+    for (int k = 0; k < 32; ++k) v += (i64)glob_s[k] * w1[tid * 64 + 32 + k];
+    bb1[tid] = v;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    bool f = fast_shifts != 0;
+    for (int j = 0; j < 32; ++j) f = f && bb1[j] <= lim32 && bb1[j] >= -lim32;
+    fast_s[1] = f;
+  }
+  // Score layer 1 (local half).
   {
-    const int s1_in = -16 - (p.concat_out_exp + p.score_w1_exp), s1_out = p.h1_out_exp + 16;
-    const int s2_in = -16 - (p.h1_out_exp + p.score_w2_exp), s2_out = p.h2_out_exp + 16;
+    const int sh_in = -16 - (p.concat_out_exp + p.score_w1_exp), sh_out = p.h1_out_exp + 16;
+    const Rq ra = rq_setup(sh_in, -(1 << 23), (1 << 23) - 1), rb = rq_setup(sh_out, -128, 127);
+    __syncthreads();
+    const bool fast = fast_s[1];
+    for (int t = wave; t < ntiles * 2; t += 4) {
+      const int rt = t >> 1, ct = t & 1;
+      const long a = *reinterpret_cast<const long *>(&local_s[(rt * 16 + col) * 32 + grp * 8]);
+      const long wb = *reinterpret_cast<const long *>(&w1[(ct * 16 + col) * 64 + grp * 8]);
+      const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, wb, v4i{0}, 0, 0, 0);
+      const int j = ct * 16 + col;
+      const i64 bias = bb1[j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int v = fast ? rq(gelu_q16(rq(acc[i] + (int)bias, ra)), rb)
+                           : gelu_exact64(acc[i], bias, sh_in, sh_out);
+        h1_s[(rt * 16 + grp * 4 + i) * 32 + j] = (int8_t)v;
+      }
+    }
+  }
+  __syncthreads();
+  // Score layer 2.
+  {
+    const int sh_in = -16 - (p.h1_out_exp + p.score_w2_exp), sh_out = p.h2_out_exp + 16;
+    const Rq ra = rq_setup(sh_in, -(1 << 23), (1 << 23) - 1), rb = rq_setup(sh_out, -128, 127);
+    const bool fast = fast_s[2];
+    for (int rt = wave; rt < ntiles; rt += 4) {
+      const long a = *reinterpret_cast<const long *>(&h1_s[(rt * 16 + col) * 32 + grp * 8]);
+      const long wb = *reinterpret_cast<const long *>(&w2[col * 32 + grp * 8]);
+      const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, wb, v4i{0}, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        h2_s[(rt * 16 + grp * 4 + i) * 16 + col] =
+            (int8_t)sel_gelu(acc[i], bb2[col], fast, ra, rb, sh_in, sh_out);
+    }
+  }
+  __syncthreads();
+  // Logits, the 2-way selector softmax (keep = element 1) and checkpoints.
+  {
     const int s3 = p.logits_out_exp - (p.h2_out_exp + p.score_w3_exp);
     const int sq = -16 - p.logits_out_exp;
-    const Rq r1a = rq_setup(s1_in, -(1 << 23), (1 << 23) - 1), r1b = rq_setup(s1_out, -128, 127);
-    const Rq r2a = rq_setup(s2_in, -(1 << 23), (1 << 23) - 1), r2b = rq_setup(s2_out, -128, 127);
-    auto stage3 = [&](auto lpc) {
-      constexpr int LPC = decltype(lpc)::value;
-      constexpr int W1 = 8 / LPC, W2 = 4 / LPC;  // layer-1 / layer-2 words per lane
-      const int sub = tid & (LPC - 1), base = (tid & 63) & ~(LPC - 1);
-      for (int c = tid / LPC; c < C; c += kHeadThreads / LPC) {
-        int lg[16];
+    for (int c = tid; c < C; c += kHeadThreads) {
+      const v4i hv = *reinterpret_cast<const v4i *>(&h2_s[c * 16]);
+      int qv[2];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) lg[k] = local_s[c * 8 + k];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) lg[8 + k] = glob[k];
-        // layer 1: this lane's output words, the group's others by shuffle
-        int mine[W1];
-#pragma unroll 1
-        for (int q = 0; q < W1; ++q) {
-          int word = 0;
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            const int j = (W1 * sub + q) * 4 + jj;
-            int acc = 0;
-            const int *w = &w1[j * 16];
-#pragma unroll
-            for (int k = 0; k < 16; ++k) acc = dot4(lg[k], w[k], acc);
-            const int v = sel_gelu(acc, bb1[j], fast, r1a, r1b, s1_in, s1_out);
-            word |= (v & 0xFF) << (8 * jj);
-          }
-          mine[q] = word;
-        }
-        int h1[8];
-#pragma unroll
-        for (int o = 0; o < LPC; ++o)
-#pragma unroll
-          for (int q = 0; q < W1; ++q) h1[o * W1 + q] = __shfl(mine[q], base + o);
-        // layer 2
-        int mine2[W2];
-#pragma unroll 1
-        for (int q = 0; q < W2; ++q) {
-          int word = 0;
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            const int j = (W2 * sub + q) * 4 + jj;
-            int acc = 0;
-            const int *w = &w2[j * 8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) acc = dot4(h1[k], w[k], acc);
-            const int v = sel_gelu(acc, bb2[j], fast, r2a, r2b, s2_in, s2_out);
-            word |= (v & 0xFF) << (8 * jj);
-          }
-          mine2[q] = word;
-        }
-        int h2[4];
-#pragma unroll
-        for (int o = 0; o < LPC; ++o)
-#pragma unroll
-          for (int q = 0; q < W2; ++q) h2[o * W2 + q] = __shfl(mine2[q], base + o);
-        if (ck.h2 && sub == 0)
-          *reinterpret_cast<v4i *>(ck.h2 + (((size_t)b * 3 + h) * kMaxCand + c) * 16) =
-              v4i{h2[0], h2[1], h2[2], h2[3]};
-        // layer 3: logit (sub & 1) here; the group's first two lanes hold both
-        const int lj = sub & 1;
+      for (int lj = 0; lj < 2; ++lj) {
         int acc = 0;
-        const int *w = &w3[lj * 4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) acc = dot4(h2[k], w[k], acc);
+        for (int k = 0; k < 4; ++k) acc = dot4(hv[k], w3[lj * 4 + k], acc);
         const int logit = (int)requant_shift((i64)acc + p.b3[h * 2 + lj], s3, 8);
-        const int qmine = (int)requant_shift(logit, sq, 24);
-        int qv[2];
-        qv[0] = __shfl(qmine, base);
-        qv[1] = __shfl(qmine, base + 1);
-        const int mx = qv[0] > qv[1] ? qv[0] : qv[1];
-        const unsigned e0 = softmax_exp(qv[0] - mx), e1 = softmax_exp(qv[1] - mx);
-        const unsigned ratio = softmax_ratio(e1, softmax_recip24(e0 + e1));
-        const int hsv = (int)(ratio > 65536u ? 65536u : ratio);
-        if (sub == 0) {
-          hs_out[((size_t)b * 3 + h) * kMaxCand + c] = hsv;
-          if (ck.head_scores) ck.head_scores[((size_t)b * 3 + h) * kMaxCand + c] = hsv;
-        }
+        qv[lj] = (int)requant_shift(logit, sq, 24);
       }
-    };
-    if (C <= kHeadThreads / 4) stage3(std::integral_constant<int, 4>{});
-    else stage3(std::integral_constant<int, 2>{});
+      const int mx = qv[0] > qv[1] ? qv[0] : qv[1];
+      const unsigned e0 = softmax_exp(qv[0] - mx), e1 = softmax_exp(qv[1] - mx);
+      const unsigned ratio = softmax_ratio(e1, softmax_recip24(e0 + e1));
+      const int hsv = (int)(ratio > 65536u ? 65536u : ratio);
+      hs_out[((size_t)b * 3 + h) * kMaxCand + c] = hsv;
+      if (ck.head_scores) ck.head_scores[((size_t)b * 3 + h) * kMaxCand + c] = hsv;
+      if (ck.h2)
+        *reinterpret_cast<v4i *>(ck.h2 + (((size_t)b * 3 + h) * kMaxCand + c) * 16) = hv;
+    }
+    if (ck.local) {
+      int8_t *dst = ck.local + ((size_t)b * 3 + h) * kMaxCand * 32;
+      for (int i = tid; i < C * 2; i += kHeadThreads)
+        reinterpret_cast<v4i *>(dst)[i] = reinterpret_cast<const v4i *>(local_s)[i];
+    }
   }
 }
 
