@@ -493,56 +493,61 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g, int n_blocks) {
   v4i bias4[NT][4], res4[MT][NT];
   epi_operands<MT, NT, EPI>(g, arow, ct0, h, bias4, res4);
   load_step(L, 0);
-  v16i acc[MT][NT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v16i{0};
 
-  int c = 0, buf = 0;
+  // One tile per iteration with its K-chunks unrolled, so the accumulators
+  // are not carried around the loop (a loop-carried accumulator was copied
+  // between VGPRs and AGPRs at every chunk).  The LDS buffers alternate by
+  // chunk; the last chunk prefetches the next tile's first.
+  int8_t *Ab = As[0], *An = As[1];
   while (true) {
-    int8_t *Ab = As[buf];
+    v16i acc[MT][NT];
 #pragma unroll
-    for (int j = 0; j < PPT; ++j) {
-      const int i = tid + j * 256, pr = i / 12, pc = i - pr * 12;
-      *reinterpret_cast<v4i *>(Ab + pr * ROW + pc * 16) = apre[j];
-    }
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
+      for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v16i{0};
+    int Ln = L;
+    bool more = true;
 #pragma unroll
-      for (int kt = 0; kt < KC; ++kt) bcur[nt][kt] = bnext[nt][kt];
-    __syncthreads();
-    // Next step: the following chunk of this tile or the next tile's first.
-    const bool last_chunk = c == NCH - 1;
-    const int Ln = last_chunk ? logical(t + (int)gridDim.x) : L;
-    const int cn = last_chunk ? 0 : c + 1;
-    const bool more = Ln < T;
-    if (more) load_step(Ln, cn);
+    for (int c = 0; c < NCH; ++c) {
 #pragma unroll
-    for (int kt = 0; kt < KC; ++kt)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const v4i af = *reinterpret_cast<const v4i *>(Ab + (wm * 32 * MT + mt * 32 + l32) * ROW +
-                                                      kt * 32 + 16 * h);
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-          acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bcur[nt][kt], af, acc[mt][nt], 0, 0, 0);
+      for (int j = 0; j < PPT; ++j) {
+        const int i = tid + j * 256, pr = i / 12, pc = i - pr * 12;
+        *reinterpret_cast<v4i *>(Ab + pr * ROW + pc * 16) = apre[j];
       }
-    if (last_chunk) {
-      epi_tile<MT, NT, EPI, FAST, DIRS>(g, acc, bias4, res4, r0, ct0, M, h, l32, rq_a, rq_b,
-                                        nullptr);
-      if (!more) break;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v16i{0};
-      t += gridDim.x;
-      tile_rows(Ln, arow, r0, ct0);
-      epi_operands<MT, NT, EPI>(g, arow, ct0, h, bias4, res4);
+        for (int kt = 0; kt < KC; ++kt) bcur[nt][kt] = bnext[nt][kt];
+      __syncthreads();
+      // Next step: the following chunk of this tile or the next tile's first.
+      if (c == NCH - 1) {
+        Ln = logical(t + (int)gridDim.x);
+        more = Ln < T;
+        if (more) load_step(Ln, 0);
+      } else {
+        load_step(L, c + 1);
+      }
+#pragma unroll
+      for (int kt = 0; kt < KC; ++kt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const v4i af = *reinterpret_cast<const v4i *>(Ab + (wm * 32 * MT + mt * 32 + l32) * ROW +
+                                                        kt * 32 + 16 * h);
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bcur[nt][kt], af, acc[mt][nt], 0, 0, 0);
+        }
+      int8_t *tmp = Ab;
+      Ab = An;
+      An = tmp;
     }
+    epi_tile<MT, NT, EPI, FAST, DIRS>(g, acc, bias4, res4, r0, ct0, M, h, l32, rq_a, rq_b,
+                                      nullptr);
+    if (!more) break;
+    t += gridDim.x;
     L = Ln;
-    c = cn;
-    buf ^= 1;
+    tile_rows(L, arow, r0, ct0);
+    epi_operands<MT, NT, EPI>(g, arow, ct0, h, bias4, res4);
   }
 }
 
