@@ -54,8 +54,10 @@ def class_work(counts, params, batch):
     """Algorithmic int8 ops (2 x MACs) and minimal HBM bytes per kernel class
     for one forward, from the per-image token counts [B][4].  Per-unit
     figures: QKV 2*192*576, proj 2*192*192, FFN1 2*192*768, FFN2 2*768*192
-    ops per token; attention 2*384*N^2 per image; patch 2*768*192 per patch;
-    head 2*192*1000 per image; selector 2*13938 per candidate."""
+    ops per token (the fused FFN kernel: both, 576 B per token in and out);
+    attention 2*384*N^2 per image; patch 2*768*192 per patch; head
+    2*192*1000 per image; selector 2*13938 per candidate.  Only the classes
+    a run launches are reported."""
     counts = np.asarray(counts, np.int64)
     stage_of_block = []
     s = 0
@@ -64,7 +66,7 @@ def class_work(counts, params, batch):
             s += 1
         stage_of_block.append(s)
     ops = dict.fromkeys(("patch", "layernorm", "gemm_qkv", "attention", "gemm_proj",
-                         "gemm_ffn1", "gemm_ffn2", "selector", "head"), 0)
+                         "gemm_ffn1", "gemm_ffn2", "ffn", "selector", "head"), 0)
     hbm = dict(ops)
     for st in stage_of_block:
         n = counts[:, st]
@@ -78,6 +80,9 @@ def class_work(counts, params, batch):
         hbm["gemm_proj"] += (192 + 192 + 192) * t
         hbm["gemm_ffn1"] += (192 + 768) * t
         hbm["gemm_ffn2"] += (768 + 192 + 192) * t
+        # fused FFN: LN2 rows and the residual in, block output out
+        ops["ffn"] += 2 * 2 * 192 * 768 * t
+        hbm["ffn"] += (192 + 192 + 192) * t
         hbm["attention"] += (576 + 192) * t
         hbm["layernorm"] += 2 * 2 * 192 * t
     for s in range(len(params.selectors)):
@@ -147,7 +152,8 @@ def _class_ms(L, fn, steps):
     return {n: float(ms[i]) / steps for i, n in enumerate(_lib.PROF_CLASSES) if launches[i]}
 
 
-GEMM_CLASSES = ("patch", "gemm_qkv", "attention", "gemm_proj", "gemm_ffn1", "gemm_ffn2", "head")
+GEMM_CLASSES = ("patch", "gemm_qkv", "attention", "gemm_proj", "gemm_ffn1", "gemm_ffn2", "ffn",
+                "head")
 
 
 def _summary(cls_ms, ops, hbm, batch, ms, exact, cpu_s):
@@ -205,7 +211,7 @@ def config_lines(args, L):
     n = 197
     ops = {"gemm_qkv": 2 * 192 * 576 * n, "gemm_proj": 2 * 192 * 192 * n,
            "gemm_ffn1": 2 * 192 * 768 * n, "gemm_ffn2": 2 * 768 * 192 * n,
-           "attention": 2 * 384 * n * n}
+           "ffn": 2 * 2 * 192 * 768 * n, "attention": 2 * 384 * n * n}
     hbm = {"layernorm": 2 * 2 * 192 * n}
     out["c0_block_b1"] = _summary(_class_ms(L, block, args.steps), ops, hbm, 1, ms,
                                   bool(np.array_equal(z.cpu().numpy(), want)), cpu_s)
@@ -393,7 +399,7 @@ def main():
         if hbm.get(name):
             entry["gbs"] = round(hbm[name] / (t * 1e-3) / 1e9, 1)
         per_class[name] = entry
-    gemm_names = ("patch", "gemm_qkv", "attention", "gemm_proj", "gemm_ffn1", "gemm_ffn2", "head")
+    gemm_names = GEMM_CLASSES
     gemm_ms = sum(per_class[n]["ms_per_step"] for n in gemm_names if n in per_class)
     gemm_ops = sum(ops[n] for n in gemm_names)
     gemm_tops = gemm_ops / (gemm_ms * 1e-3) / 1e12

@@ -24,7 +24,7 @@ HV_A_ROWS, HV_A_GATHER = 0, 1
 HV_SELECTOR_NOALLOC_MAX_BATCH = 1024
 ABI_VERSION = 5
 PROF_CLASSES = ("patch", "layernorm", "gemm_qkv", "attention", "gemm_proj", "gemm_ffn1",
-                "gemm_ffn2", "selector", "head", "other")
+                "gemm_ffn2", "selector", "head", "other", "ffn")
 
 _vp = C.c_void_p
 _i32 = C.c_int32

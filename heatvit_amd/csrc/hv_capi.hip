@@ -226,25 +226,32 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
                           p.gamma2_exp, p.beta2_exp, p.ln2_out_exp, nullptr, lw, s);
   }
   if (rc) return rc;
-  g = GemmArgs{};
-  g.a = ln2; g.b = p.w1_p; g.bias = p.b1; g.c = hidden; g.m_dev = rows_dev;
-  g.m = max_rows; g.n = 768; g.k = 192; g.lda = 192; g.ldc = 768;
-  g.shift_a = -16 - (p.ln2_out_exp + p.w1_exp);
-  g.shift_b = p.hidden_out_exp + 16;
+  GemmArgs g1{};
+  g1.a = ln2; g1.b = p.w1_p; g1.bias = p.b1; g1.c = hidden; g1.m_dev = rows_dev;
+  g1.m = max_rows; g1.n = 768; g1.k = 192; g1.lda = 192; g1.ldc = 768;
+  g1.shift_a = -16 - (p.ln2_out_exp + p.w1_exp);
+  g1.shift_b = p.hidden_out_exp + 16;
+  GemmArgs g2{};
+  g2.a = hidden; g2.b = p.w2_p; g2.bias = p.b2; g2.c = z; g2.res = y;
+  g2.aux = ck ? ck->ffn_out : nullptr;
+  g2.m_dev = rows_dev; g2.m = max_rows; g2.n = 192; g2.k = 768; g2.lda = 768; g2.ldc = 192;
+  g2.ldr = 192;
+  g2.shift_a = p.ffn_out_exp - (p.hidden_out_exp + p.w2_exp);
+  g2.mid_exp = p.ffn_out_exp; g2.res_exp = p.ffn_x_exp; g2.out_exp = p.out_exp;
+  // One fused kernel (hidden rows in LDS) unless the hidden checkpoint is
+  // wanted or the exponents need the general epilogues.
+  if (!(ck && ck->hidden)) {
+    ProfScope ps(HV_PROF_FFN, s);
+    rc = launch_ffn(g1, g2, s);
+    if (rc != 1) return rc;
+  }
   {
     ProfScope ps(HV_PROF_GEMM_FFN1, s);
-    rc = launch_gemm(g, A_ROWS, HV_EPI_GELU, s);
+    rc = launch_gemm(g1, A_ROWS, HV_EPI_GELU, s);
   }
   if (rc) return rc;
-
-  g = GemmArgs{};
-  g.a = hidden; g.b = p.w2_p; g.bias = p.b2; g.c = z; g.res = y;
-  g.aux = ck ? ck->ffn_out : nullptr;
-  g.m_dev = rows_dev; g.m = max_rows; g.n = 192; g.k = 768; g.lda = 768; g.ldc = 192; g.ldr = 192;
-  g.shift_a = p.ffn_out_exp - (p.hidden_out_exp + p.w2_exp);
-  g.mid_exp = p.ffn_out_exp; g.res_exp = p.ffn_x_exp; g.out_exp = p.out_exp;
   ProfScope ps(HV_PROF_GEMM_FFN2, s);
-  return launch_gemm(g, A_ROWS, HV_EPI_RESIDUAL, s);
+  return launch_gemm(g2, A_ROWS, HV_EPI_RESIDUAL, s);
 }
 
 static bool exp_ok(int e) { return e >= -32 && e <= 31; }

@@ -743,6 +743,211 @@ int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Fused FFN (transformer.ffn, transformer.py:328-384) for the int32
+// epilogues with a GELU step table: z = align_add(y, requant(GELU(ln2 W1 +
+// b1) W2 + b2)).  A persistent workgroup owns 64 rows at a time:
+//   phase A  the FFN1 tiles (2 row x 24 column tiles of 32; wavefront w
+//            takes columns w, w+4, ...), the GELU post-op from the step
+//            table, the hidden row block written to LDS ([64][768] at a
+//            784-byte row stride, conflict-free 16-byte reads);
+//   phase B  the FFN2 tiles (2 row x 6 column tiles, three per wavefront)
+//            with K = 768 read from LDS and the residual epilogue.
+// The hidden activations never leave the CU.  Each workgroup stages the
+// GELU table and handles one row block.
+// ---------------------------------------------------------------------------
+static constexpr int kFfnRows = 64, kFfnHRow = 784;
+
+template <int DIRS1, int DIRS2>
+__global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2) {
+  __shared__ __attribute__((aligned(16))) int8_t hid[kFfnRows * kFfnHRow];
+  extern __shared__ __attribute__((aligned(16))) unsigned lut[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int M = g1.m_dev ? min(*g1.m_dev, g1.m) : g1.m;
+  const int nrb = (M + kFfnRows - 1) / kFfnRows;
+  if ((int)blockIdx.x >= nrb) return;  // uniform: before any barrier
+  stage_lut(g1, lut);
+  const Rq r1a = rq_setup(g1.shift_a, -(1 << 23), (1 << 23) - 1);
+  const Rq r2a = rq_setup(g2.shift_a, -128, 127), r2b = rq_setup(g2.os, -128, 127);
+  constexpr bool LA1 = DIRS1 & 1;
+  constexpr int K1 = (DIRS1 & 8) ? 1 : 3;
+  int qhi = g1.lut_qhi;
+  asm("" : "+v"(qhi));  // the table clamp as one med3 (both bounds in VGPRs)
+
+  for (int rb = blockIdx.x; rb < nrb; rb += gridDim.x) {
+    const int r0 = rb * kFfnRows;
+    // Phase A.  A fragments of both row tiles, all six K-steps; the weight
+    // fragments and biases of column tile ci + 1 load while tile ci runs.
+    v4i af[2][6];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int8_t *ap = g1.a + (size_t)min(r0 + 32 * rt + l32, M - 1) * g1.lda + 16 * h;
+#pragma unroll
+      for (int kt = 0; kt < 6; ++kt) af[rt][kt] = *reinterpret_cast<const v4i *>(ap + kt * 32);
+    }
+    // Weight fragments single-buffered: the next column tile's load is
+    // issued after the current tile's MFMAs and lands during its GELU
+    // epilogues; the biases are double-buffered.
+    v4i bf[6], bs[2][4];
+    auto load_w1 = [&](int ci, v4i (&bi)[4]) {
+      const int ct = wave + 4 * ci;
+#pragma unroll
+      for (int kt = 0; kt < 6; ++kt)
+        bf[kt] = *reinterpret_cast<const v4i *>(g1.b + (size_t)(ct * 6 + kt) * 1024 + lane * 16);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        bi[q] = *reinterpret_cast<const v4i *>(g1.bias + ct * 32 + 16 * h + 4 * q);
+    };
+    load_w1(0, bs[0]);
+#pragma unroll 2
+    for (int ci = 0; ci < 6; ++ci) {
+      const int cur = ci & 1;
+      const int c0 = (wave + 4 * ci) * 32 + 16 * h;
+      v16i acc[2];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        acc[rt] = v16i{0};
+#pragma unroll
+        for (int kt = 0; kt < 6; ++kt)
+          acc[rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[kt], af[rt][kt], acc[rt], 0, 0, 0);
+      }
+      if (ci + 1 < 6) load_w1(ci + 1, bs[cur ^ 1]);
+      int bmax = bs[cur][0][0], bmin = bmax;
+#pragma unroll
+      for (int j = 1; j < 16; ++j) {
+        bmax = max(bmax, bs[cur][j >> 2][j & 3]);
+        bmin = min(bmin, bs[cur][j >> 2][j & 3]);
+      }
+      const bool fast = __all(bmax <= g1.acc_lim && bmin >= -g1.acc_lim);
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        int o[16];
+        if (fast) {
+#pragma unroll
+          for (int j = 0; j < 16; ++j)
+            o[j] = gelu_lut<K1>(shift_nowrap<LA1>(acc[rt][j] + bs[cur][j >> 2][j & 3], r1a), lut,
+                                qhi, g1);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 16; ++j)
+            o[j] = epi_exact(EPI_GELU, acc[rt][j], bs[cur][j >> 2][j & 3], 0, g1.shift_a,
+                             g1.shift_b, 0, 0, 0)[0];
+        }
+        *reinterpret_cast<v4i *>(&hid[(32 * rt + l32) * kFfnHRow + c0]) =
+            v4i{pack4(o[0], o[1], o[2], o[3]), pack4(o[4], o[5], o[6], o[7]),
+                pack4(o[8], o[9], o[10], o[11]), pack4(o[12], o[13], o[14], o[15])};
+      }
+    }
+    // The first phase-B tile's operands and first weight chunk load before
+    // the barrier.
+    auto tile_of = [&](int ti, int &rt, int &ct) {
+      const int t = wave + 4 * ti;
+      rt = t / 6;
+      ct = t - rt * 6;
+    };
+    v4i wb[2][4], bias4[1][4], res4[1][1];
+    int rt, ct;
+    tile_of(0, rt, ct);
+    {
+      const int arow[1] = {min(r0 + 32 * rt + l32, M - 1)};
+      epi_operands<1, 1, EPI_RES>(g2, arow, ct, h, bias4, res4);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      wb[0][j] = *reinterpret_cast<const v4i *>(g2.b + ((size_t)ct * 24 + j) * 1024 + lane * 16);
+    __syncthreads();
+    // Phase B: tiles wave, wave + 4, wave + 8 of the 2 x 6; 24 K-steps in
+    // chunks of 4, the next chunk (or the next tile's first) in flight.
+#pragma unroll 1
+    for (int ti = 0; ti < 3; ++ti) {
+      const int8_t *hp = &hid[(32 * rt + l32) * kFfnHRow + 16 * h];
+      const int8_t *bp = g2.b + (size_t)ct * 24 * 1024 + lane * 16;
+      int nrt = rt, nct = ct;
+      if (ti + 1 < 3) tile_of(ti + 1, nrt, nct);
+      v16i acc[1][1] = {{v16i{0}}};
+#pragma unroll
+      for (int c = 0; c < 6; ++c) {
+        const int cur = c & 1;
+        if (c + 1 < 6) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            wb[cur ^ 1][j] = *reinterpret_cast<const v4i *>(bp + ((c + 1) * 4 + j) * 1024);
+        } else if (ti + 1 < 3) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            wb[cur ^ 1][j] =
+                *reinterpret_cast<const v4i *>(g2.b + ((size_t)nct * 24 + j) * 1024 + lane * 16);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+              wb[cur][j], *reinterpret_cast<const v4i *>(hp + (c * 4 + j) * 32), acc[0][0], 0, 0,
+              0);
+        __builtin_amdgcn_sched_barrier(0);  // one chunk of LDS reads in flight at a time
+      }
+      epi_tile<1, 1, EPI_RES, true, DIRS2>(g2, acc, bias4, res4, r0 + 32 * rt, ct, M, h, l32,
+                                           r2a, r2b, nullptr);
+      if (ti + 1 < 3) {
+        rt = nrt;
+        ct = nct;
+        const int arow[1] = {min(r0 + 32 * rt + l32, M - 1)};
+        epi_operands<1, 1, EPI_RES>(g2, arow, ct, h, bias4, res4);
+      }
+    }
+    __syncthreads();  // the next row block rewrites hid
+  }
+}
+
+template <int DIRS1>
+static void launch_ffn_d(const GemmArgs &g1, const GemmArgs &g2, int dirs2, dim3 grid, size_t lds,
+                         hipStream_t s) {
+  switch (dirs2) {
+    case 0: hv_launch(k_ffn<DIRS1, 0>, grid, dim3(256), lds, s, g1, g2); break;
+    case 1: hv_launch(k_ffn<DIRS1, 1>, grid, dim3(256), lds, s, g1, g2); break;
+    case 2: hv_launch(k_ffn<DIRS1, 2>, grid, dim3(256), lds, s, g1, g2); break;
+    default: hv_launch(k_ffn<DIRS1, 3>, grid, dim3(256), lds, s, g1, g2); break;
+  }
+}
+
+// Returns HV_OK when the fused kernel was launched, 1 when the shapes or
+// exponents need the two GEMM launches instead.
+int launch_ffn(const GemmArgs &g1_in, const GemmArgs &g2_in, hipStream_t s) {
+  GemmArgs g1 = g1_in, g2 = g2_in;
+  if (g1.k != 192 || g1.n != 768 || g2.k != 768 || g2.n != 192 || g1.lda != 192 ||
+      g2.ldc != 192 || g2.ldr != 192 || !g1.bias || !g2.bias || !g2.res || g1.m <= 0)
+    return 1;
+  if (((uintptr_t)g1.a | (uintptr_t)g1.bias | (uintptr_t)g2.bias | (uintptr_t)g2.c |
+       (uintptr_t)g2.res | (uintptr_t)g2.aux) & 15)
+    return 1;
+  if (g1.shift_b < kGeluLutSoMin || g1.shift_b > kGeluLutSoMax) return 1;
+  epilogue_limits_pub(g1, EPI_GELU);
+  epilogue_limits_pub(g2, EPI_RES);
+  if (!fast_epilogue(g1, EPI_GELU) || !fast_epilogue(g2, EPI_RES)) return 1;
+  const GeluLutInfo &t = kGeluLutInfo[g1.shift_b - kGeluLutSoMin];
+  g1.lut_off = t.off;
+  g1.lut_k = t.k;
+  g1.lut_words = t.words;
+  g1.lut_n1e = t.n1e;
+  g1.lut_qlo = t.qlo;
+  g1.lut_qhi = t.qhi;
+  g2.vec_out = 1;
+  g2.vec_res = 1;
+  const size_t lds = (size_t)g1.lut_words * 4;
+  // One workgroup per row block (the dispatcher balances them; a persistent
+  // grid left half the workgroups with one block more than the others).
+  const dim3 grid((g1.m + kFfnRows - 1) / kFfnRows);
+  const int d1 = epilogue_dirs(g1, EPI_GELU) & 1, d2 = epilogue_dirs(g2, EPI_RES);
+  if (g1.lut_k == 1) {
+    if (d1) launch_ffn_d<13>(g1, g2, d2, grid, lds, s);
+    else launch_ffn_d<12>(g1, g2, d2, grid, lds, s);
+  } else {
+    if (d1) launch_ffn_d<5>(g1, g2, d2, grid, lds, s);
+    else launch_ffn_d<4>(g1, g2, d2, grid, lds, s);
+  }
+  return check_hip(hipGetLastError(), "k_ffn launch");
+}
+
 // The GELU post-op of the FFN epilogue over int64 Q8.16 values (saturated
 // to 24 bits): evaluated as the int32 epilogue does, or from the step table.
 __global__ __launch_bounds__(256) void k_gelu_post(int table, const int64_t *in, int64_t *out,

@@ -57,6 +57,11 @@ struct GemmArgs {
 
 // epilogue: HV_EPI_* or 4 (patch: A_PATCH gather, position-row residual).
 int launch_gemm(const GemmArgs &g, int a_mode, int epilogue, hipStream_t s);
+// FFN1 + GELU + FFN2 + residual in one kernel (hidden rows in LDS): g1 as
+// for the GELU GEMM (c unused), g2 as for the residual GEMM (a unused).
+// Returns HV_OK when launched, 1 when the shapes or exponents need the two
+// GEMM launches (no GELU step table, wide shifts, unaligned pointers).
+int launch_ffn(const GemmArgs &g1, const GemmArgs &g2, hipStream_t s);
 // Fills acc_lim / narrow_ok / da / db / os of the int32 epilogue paths.
 void epilogue_limits_pub(GemmArgs &g, int epilogue);
 

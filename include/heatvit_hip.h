@@ -389,7 +389,8 @@ int hv_model_forward_f32(const hv_model_dev *p, const float *images, int batch, 
 #define HV_PROF_SELECTOR 7
 #define HV_PROF_HEAD 8
 #define HV_PROF_OTHER 9
-#define HV_PROF_CLASSES 10
+#define HV_PROF_FFN 10 /* FFN1 + GELU + FFN2 + residual in one kernel */
+#define HV_PROF_CLASSES 11
 
 int hv_profile_enable(int on);
 int hv_profile_read(float *ms, int32_t *launches, int n);

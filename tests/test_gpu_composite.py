@@ -43,6 +43,28 @@ def test_block_ragged_batch_vs_oracle(oracle):
             assert np.array_equal(cks[i][k], ck[k]), (i, k)
 
 
+def test_fused_ffn_wide_biases_and_ragged_rows_vs_oracle(oracle):
+    """Without checkpoints the block's FFN runs as one fused kernel (hidden
+    rows in LDS); FFN1 biases beyond the int32 epilogue bound send their
+    column tiles to the exact 64-bit GELU, and ragged images leave partial
+    64-row blocks."""
+    import dataclasses
+    from heatvit_amd.transformer import transformer_block_batch
+    _, bp = synth.block_workload()
+    b1 = np.asarray(bp.ffn.b1).astype(np.int64).copy()
+    b1[5] = (1 << 31) - 1
+    b1[300:310] = -(1 << 31)
+    b1[700] = (1 << 30)
+    bp = dataclasses.replace(bp, ffn=dataclasses.replace(bp.ffn, b1=b1))
+    rng = np.random.default_rng(8)
+    lens = [197, 63, 1, 65, 130, 197, 7]
+    xs = [rng.integers(-128, 128, (n, 192)).astype(np.int8) for n in lens]
+    zs = transformer_block_batch(xs, bp)
+    for i, x in enumerate(xs):
+        z, _ = oracle.transformer_block(x, bp, checkpoints=False)
+        assert np.array_equal(zs[i], z), i
+
+
 def test_selector_matches_golden():
     from heatvit_amd.selector import token_selector_batch
     meta, arrays = gio.load("selector")
