@@ -20,7 +20,7 @@ HV_PRIM_REQUANT, HV_PRIM_GELU, HV_PRIM_PLAN, HV_PRIM_RSA = 0, 1, 2, 3
 HV_PRIM_GELU_POST, HV_PRIM_GELU_TABLE = 4, 5
 GELU_TABLE_SO = range(3, 13)
 HV_EPI_I8, HV_EPI_I32, HV_EPI_GELU, HV_EPI_RESIDUAL = 0, 1, 2, 3
-HV_A_ROWS, HV_A_GATHER = 0, 1
+HV_A_ROWS, HV_A_GATHER, HV_A_UNSIGNED = 0, 1, 4
 HV_SELECTOR_NOALLOC_MAX_BATCH = 1024
 ABI_VERSION = 5
 PROF_CLASSES = ("patch", "layernorm", "gemm_qkv", "attention", "gemm_proj", "gemm_ffn1",

@@ -68,7 +68,7 @@ static constexpr int kLutGridCap = 256 * 5;
 
 template <int AMODE>
 __device__ __forceinline__ const int8_t *a_row(const GemmArgs &g, int r) {
-  if (AMODE == A_GATHER) return g.a + (size_t)g.a_rows[r] * g.lda;
+  if ((AMODE & 3) == A_GATHER) return g.a + (size_t)g.a_rows[r] * g.lda;
   return g.a + (size_t)r * g.lda;
 }
 
@@ -289,6 +289,12 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
   constexpr int BM = 32 * MT * WM;  // rows per tile
   constexpr int BT = NT * WN;       // 32-column weight tiles per tile
   constexpr bool RESLIKE = EPI == EPI_RES || EPI == EPI_PATCH;
+  // Unsigned A (runtime K only): the MFMA takes s = u - 128 (the byte with
+  // its top bit flipped) and a second MFMA per weight tile, with every A
+  // byte -128, accumulates corr = -128 * (column sums of W), so
+  // sum(u w) = sum(s w) - corr; both stay below 2^31 for K <= 65536.
+  constexpr bool AU = (AMODE & A_UNSIGNED) != 0;
+  static_assert(!AU || KTC == 0, "unsigned A uses the runtime-K loop");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave - wm * WN;
   const int h = lane >> 5, l32 = lane & 31;
@@ -329,7 +335,9 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
     auto load_a = [&](int mt, int kt) -> v4i {
       const int8_t *p = AMODE == A_PATCH ? patch_ptr(g.a, arow[mt], kt * 32 + 16 * h)
                                          : ap[mt] + kt * 32;
-      return *reinterpret_cast<const v4i *>(p);
+      const v4i v = *reinterpret_cast<const v4i *>(p);
+      if constexpr (AU) return v ^ (int)0x80808080;
+      return v;
     };
     auto load_b = [&](int nt, int kt) -> v4i {
       return *reinterpret_cast<const v4i *>(bp[nt] + kt * 1024);
@@ -397,6 +405,9 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
     } else {
       // Runtime K: one step of prefetch.
       v4i ac[MT], bc[NT], an[MT], bn[NT];
+      v16i corr[NT];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) corr[nt] = v16i{0};
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) ac[mt] = load_a(mt, 0);
 #pragma unroll
@@ -413,12 +424,25 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g, int n_blocks) {
 #pragma unroll
           for (int nt = 0; nt < NT; ++nt)
             acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bc[nt], ac[mt], acc[mt][nt], 0, 0, 0);
+        if constexpr (AU) {
+          const v4i m128 = v4i{(int)0x80808080, (int)0x80808080, (int)0x80808080,
+                               (int)0x80808080};
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            corr[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bc[nt], m128, corr[nt], 0, 0, 0);
+        }
         if (kt + 1 < KT) {
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) ac[mt] = an[mt];
 #pragma unroll
           for (int nt = 0; nt < NT; ++nt) bc[nt] = bn[nt];
         }
+      }
+      if constexpr (AU) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) acc[mt][nt] -= corr[nt];
       }
     }
 
@@ -553,7 +577,8 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g, int n_blocks) {
 
 // Host-side set-up of the epilogue preconditions.
 void epilogue_limits_pub(GemmArgs &g, int epi) {
-  const long long acc_max = (long long)g.k * 128 * 128;  // |A W| bound (int8 x int8)
+  // |A W| bound: int8 x int8, or uint8 x int8
+  const long long acc_max = (long long)g.k * (g.a_unsigned ? 255 : 128) * 128;
   long long lim = (1ll << 30) - 1 - acc_max;
   if (g.shift_a < 0) {
     // the first requant shifts v = acc + bias left by -shift_a: keep that
@@ -691,6 +716,7 @@ static int dispatch(const GemmArgs &g, int a_mode, hipStream_t s) {
     if (a_mode == A_ROWS) return run_lds<2, 1, 2, EPI_PATCH, A_ROWS, 24>(g, s);
     return run_lds<2, 1, 2, EPI_PATCH, A_PATCH, 24>(g, s);
   } else {
+    if (a_mode == (A_ROWS | A_UNSIGNED)) return run<1, 1, 2, EPI, A_ROWS | A_UNSIGNED, 0>(g, s);
     if (a_mode == A_GATHER) return run<1, 1, 2, EPI, A_GATHER, 0>(g, s);
     if (a_mode != A_ROWS) return fail(HV_EVALUE, HV_ERR_OPCODE, "gemm: bad A mode %d", a_mode);
     if constexpr (EPI == EPI_GELU) {
@@ -705,9 +731,15 @@ static int dispatch(const GemmArgs &g, int a_mode, hipStream_t s) {
 
 int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
   GemmArgs g = g_in;
+  g.a_unsigned = (a_mode & A_UNSIGNED) != 0;
+  if (g.a_unsigned && (a_mode != (A_ROWS | A_UNSIGNED) || epi == EPI_PATCH))
+    return fail(HV_EVALUE, HV_ERR_OPCODE, "gemm: unsigned A needs HV_A_ROWS and a plain epilogue");
   epilogue_limits_pub(g, epi);
   if (g.k <= 0 || g.k % 32)
     return fail(HV_EVALUE, HV_ERR_DIMENSION, "gemm: K=%d must be a positive multiple of 32", g.k);
+  if (g.a_unsigned && g.k > 65536)
+    return fail(HV_EOVERFLOW, HV_ERR_DIMENSION, "gemm: unsigned A with K=%d may overflow int32",
+                g.k);
   if (g.n <= 0) return fail(HV_EVALUE, HV_ERR_DIMENSION, "gemm: N=%d must be positive", g.n);
   if (g.m < 0) return fail(HV_EVALUE, HV_ERR_DIMENSION, "gemm: M=%d must be non-negative", g.m);
   if (a_mode != A_PATCH && (g.lda % 16 || ((uintptr_t)g.a & 15)))

@@ -27,7 +27,8 @@ inline void hv_launch(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t
 }
 
 // A-operand sources of the GEMM.
-enum { A_ROWS = HV_A_ROWS, A_GATHER = HV_A_GATHER, A_PATCH = 2 };
+// A_UNSIGNED is a flag bit of the A mode (A_ROWS only).
+enum { A_ROWS = HV_A_ROWS, A_GATHER = HV_A_GATHER, A_PATCH = 2, A_UNSIGNED = HV_A_UNSIGNED };
 
 struct GemmArgs {
   const int8_t *a;
@@ -43,6 +44,8 @@ struct GemmArgs {
   int shift_a;  // epilogue shifts, see k_gemm
   int shift_b;
   int res_exp, mid_exp, out_exp;
+  // Filled by launch_gemm: A bytes unsigned (A_UNSIGNED in the A mode).
+  int a_unsigned;
   // Filled by launch_gemm: int32 epilogue preconditions.
   int acc_lim;     // a column takes the int32 path when |bias| <= acc_lim
   int narrow_ok;   // acc_lim > 0

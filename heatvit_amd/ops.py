@@ -154,20 +154,27 @@ def attention(fused_qkv, qkv_exp, score_exp, prob_exp, context_exp):
 
 
 def gemm_writeback(a, w, bias, src_exp, dst_exp, output_bits, *, epilogue=None, mid_exp=0,
-                   residual=None, res_exp=0, a_rows=None):
+                   residual=None, res_exp=0, a_rows=None, a_unsigned=False):
     """requant(A W + bias) as gemm_writeback(gemm_numpy(...)) computes it,
-    on the MFMA GEMM.  A [M][K] int8, W [K][N] int8 (row-major, reference
-    layout), bias [N] int32 or None.  K is zero-padded to a multiple of 32.
-    `epilogue` selects the fused variants ('gelu', 'residual')."""
+    on the MFMA GEMM.  A [M][K] int8 (uint8 with a_unsigned, gemm.py:93-114),
+    W [K][N] int8 (row-major, reference layout), bias [N] int32 or None.  K
+    is zero-padded to a multiple of 32.  `epilogue` selects the fused
+    variants ('gelu', 'residual')."""
     a = np.asarray(a)
     w = np.asarray(w)
     m, k = a.shape
     if w.shape[0] != k:
         raise ValueError(f"K mismatch: a has {k}, b has {w.shape[0]}")
+    lo, hi = (0, 255) if a_unsigned else (-128, 127)
+    if a.size and (a.min() < lo or a.max() > hi):
+        raise ValueError(f"A values must lie in [{lo}, {hi}]")
+    if a_unsigned and a_rows is not None:
+        raise ValueError("unsigned A takes whole rows (no a_rows)")
     n = w.shape[1]
     kp = -(-k // 32) * 32
-    ap = np.zeros((m, kp), np.int8)
+    ap = np.zeros((m, kp), np.uint8 if a_unsigned else np.int8)
     ap[:, :k] = a
+    ap = ap.view(np.int8)
     wp = np.zeros((kp, n), np.int8)
     wp[:k] = w
     ad = _to_dev(ap, torch.int8)
@@ -188,6 +195,8 @@ def gemm_writeback(a, w, bias, src_exp, dst_exp, output_bits, *, epilogue=None, 
     d.a_rows = None if rows is None else rows.data_ptr()
     d.m, d.n, d.k, d.lda, d.ldc, d.ldr = (len(rows) if rows is not None else m), n, kp, kp, n, n
     d.a_mode = _lib.HV_A_GATHER if rows is not None else _lib.HV_A_ROWS
+    if a_unsigned:
+        d.a_mode |= _lib.HV_A_UNSIGNED
     d.epilogue = epi
     d.src_exp, d.dst_exp, d.mid_exp, d.res_exp = src_exp, dst_exp, mid_exp, res_exp
     if rows is not None:

@@ -143,6 +143,9 @@ int hv_attention_i8(const int8_t *qkv, const int32_t *offsets, int batch, int ro
 
 #define HV_A_ROWS 0   /* A row r at a + r*lda                                         */
 #define HV_A_GATHER 1 /* A row r at a + a_rows[r]*lda                                 */
+/* ORed onto HV_A_ROWS: A bytes are unsigned 0..255 (gemm_numpy a_unsigned,
+ * gemm.py:93-114); K <= 65536 so the int32 accumulator cannot overflow. */
+#define HV_A_UNSIGNED 4
 
 typedef struct {
   const int8_t *a;         /* [M][lda] int8                                  */

@@ -71,6 +71,14 @@ def test_gemm_validation(L):
     _expect(L, L.hv_gemm_i8(C.byref(d), None), _lib.HV_EVALUE, _lib.HV_ERR_ADDRESS)
     d.lda, d.k = 131104, 131104  # int32 accumulator bound (gemm.py:116-117)
     _expect(L, L.hv_gemm_i8(C.byref(d), None), _lib.HV_EOVERFLOW, _lib.HV_ERR_DIMENSION)
+    # unsigned A: K <= 65536 (255 * 128 * K < 2^31), whole rows only
+    d.a_mode = _lib.HV_A_ROWS | _lib.HV_A_UNSIGNED
+    d.lda, d.k = 65568, 65568
+    _expect(L, L.hv_gemm_i8(C.byref(d), None), _lib.HV_EOVERFLOW, _lib.HV_ERR_DIMENSION)
+    d.lda, d.k = 32, 32
+    d.a_mode = _lib.HV_A_GATHER | _lib.HV_A_UNSIGNED
+    d.a_rows = C.addressof(a)
+    _expect(L, L.hv_gemm_i8(C.byref(d), None), _lib.HV_EVALUE, _lib.HV_ERR_OPCODE)
 
 
 def test_block_selector_model_validation(L):

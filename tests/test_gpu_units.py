@@ -91,15 +91,63 @@ def test_layernorm_row_groups_vs_oracle(ops, oracle, rows):
 
 
 def test_gemm_scenarios(ops):
+    """Every scenario of the reference's GEMM vectors, the unsigned-A one
+    (gemm_numpy a_unsigned) included."""
+    names = []
     for sc in fx.gemm_scenarios():
-        if sc["unsigned"]:
-            continue  # unsigned A runs only inside the attention kernel (P V)
         s0, s1, dst = sc["scales"]
         for h in range(sc["heads"]):
             w = sc["b"][h].T if sc["transpose"] else sc["b"][h]
             bias = None if sc["bias"] is None else sc["bias"][h * sc["n"]:(h + 1) * sc["n"]]
-            got = ops.gemm_writeback(sc["a"][h], w, bias, s0 + s1, dst, sc["bits"])
+            got = ops.gemm_writeback(sc["a"][h], w, bias, s0 + s1, dst, sc["bits"],
+                                     a_unsigned=sc["unsigned"])
             assert np.array_equal(got, sc["expected"][h]), (sc["name"], h)
+        names.append(sc["name"])
+    assert "unsigned" in names and len(names) == 8
+
+
+@pytest.mark.parametrize("m,n,k", [(197, 197, 64), (64, 100, 64), (1000, 192, 224),
+                                   (33, 40, 2048)])
+def test_gemm_unsigned_a_vs_oracle(ops, oracle, m, n, k):
+    """Unsigned A (gemm.py:93-114) against the oracle: every epilogue, A
+    bytes across 0..255 with all-255 rows and columns, weights at -128."""
+    rng = np.random.default_rng(m + 3 * n + k)
+    a = rng.integers(0, 256, (m, k))
+    a[::5] = 255
+    a[:, ::7] = 0
+    w = rng.integers(-128, 128, (k, n))
+    w[:, ::3] = -128
+    bias = rng.integers(-(1 << 20), 1 << 20, n)
+    acc = oracle.gemm(a, w, bias, a_unsigned=True)
+    for src, dst in ((-14, -7), (-8, -15), (-30, 5)):
+        assert np.array_equal(ops.gemm_writeback(a, w, bias, src, dst, 8, a_unsigned=True),
+                              oracle.gemm_writeback(acc, src, dst, 8)), (src, dst)
+    assert np.array_equal(ops.gemm_writeback(a, w, bias, -14, -14, 32, a_unsigned=True),
+                          oracle.gemm_writeback(acc, -14, -14, 32))
+    q = oracle.requant_array(acc, -14, -16, 24)
+    want = oracle.requant_array(oracle.gelu_array(q).astype(np.int64), -16, -7, 8)
+    assert np.array_equal(ops.gemm_writeback(a, w, bias, -14, -7, 8, epilogue="gelu",
+                                             a_unsigned=True), want)
+    # wide biases take the exact 64-bit epilogue
+    wide = bias.copy()
+    wide[::2] = rng.choice([(1 << 31) - 1, -(1 << 31)], len(wide[::2]))
+    acc = oracle.gemm(a, w, wide, a_unsigned=True)
+    assert np.array_equal(ops.gemm_writeback(a, w, wide, -20, -4, 8, a_unsigned=True),
+                          oracle.gemm_writeback(acc, -20, -4, 8))
+
+
+def test_gemm_unsigned_a_extremes(ops, oracle):
+    """K = 65536 with A = 255 and W = -128 or 127 everywhere: the largest
+    accumulators unsigned A allows (-2^31 + 2^23 and 2^31 - 2^24 - 2^23 ...),
+    through the int32 output."""
+    k = 65536
+    a = np.full((3, k), 255)
+    w = np.full((k, 64), -128)
+    w[:, 1::2] = 127
+    acc = oracle.gemm(a, w, None, a_unsigned=True)
+    assert acc.min() == -255 * 128 * k and acc.max() == 255 * 127 * k
+    assert np.array_equal(ops.gemm_writeback(a, w, None, 0, 0, 32, a_unsigned=True),
+                          oracle.gemm_writeback(acc, 0, 0, 32))
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 1000, 192), (197, 576, 192), (1000, 768, 192),
