@@ -5,14 +5,18 @@
 (requant(gelu(q), -16, dst, 8) with so = dst + 16; nonlinear.py:60-80 and
 fixed.py:15-45 / transformer.py:349-358), one table per so in [3, 12].
 
-G_so is a step function of q with a few hundred changes.  Table layout
-(32-bit words):
-  L1[b], b = u >> 9 with u = clamp(q, qlo, qhi) - qlo: bits 0..23 a signed
-      byte offset, from the table's start, chosen so that the entry of u is
-      at offset + E * (u >> s2) (E = 4 or 8 bytes per entry; so the bucket's
-      first entry sits at offset + E * (b * 2^(9 - s2))), bits 24..27 s2;
+G_so is a step function of q with a few hundred changes.  qlo is a
+multiple of 2^S1 = 256 (rounded down from the last value below the first
+change).  Table layout (32-bit words):
+  L1[b], b = (c >> S1) - (qlo >> S1) with c = clamp(q, qlo, qhi): bits 0..4
+      s2, bits 5..31 a signed byte offset, from the table's start, chosen
+      so that the entry of c is at offset + E * (c >> s2) (E = 4 or 8 bytes
+      per entry, arithmetic shift; the bucket starts at a multiple of 2^S1,
+      so its entries start at multiples of 2^s2).  A lookup reads c >> s2
+      and c mod 2^s2 with the word itself as the shift amount and the
+      field width (the hardware takes its low five bits);
   (L1 holds n1e words, its length rounded up to even; L2 follows it)
-  L2, one entry per 2^s2 values of u: G at the entry's first u and up to K
+  L2, one entry per 2^s2 values of c: G at the entry's first c and up to K
       changes inside the entry, each an offset (9 bits, 511 = none) and the
       signed 7-bit step taken from that offset on.  K = 1: one word per entry,
         T[0:8] B1[8:17] D1[17:24];
@@ -21,8 +25,10 @@ G_so is a step function of q with a few hundred changes.  Table layout
         word 1: B2[0:9] D2[9:16] B3[16:25] D3[25:32].
   G is constant for q <= qlo and for q >= qhi.  Each table is padded to a
   multiple of four words, so tables start on 16-byte boundaries.  s2 is the largest value in
-  [0, 9] that leaves at most K changes inside every entry of the bucket.
-  Each so gets the one-change form when that table fits in 32 KB (fewer
+  [0, S1] that leaves at most K changes inside every entry of the bucket.
+  Each so gets the one-change form when that table fits in 31,744 bytes,
+  the LDS the fused FFN kernel has beside its 50,176-byte hidden block at
+  two workgroups per CU (fewer
   operations per lookup), the three-change form otherwise (a smaller table
   where the rounding of rsa makes G wiggle).
 
@@ -38,8 +44,8 @@ import sys
 import numpy as np
 
 SO_MIN, SO_MAX = 3, 12
-S1 = 9
-K1_MAX_BYTES = 32768
+S1 = 8
+K1_MAX_BYTES = 31744
 
 
 def gelu_q16(x):
@@ -74,7 +80,7 @@ def build_table(so, q, o, K):
     changes per entry, given o = G_so(q) over the whole domain q
     (ascending)."""
     ch = np.nonzero(np.diff(o))[0] + 1          # o[i] != o[i - 1]
-    qlo, qhi = int(q[ch[0]] - 1), int(q[ch[-1]])
+    qlo, qhi = (int(q[ch[0]] - 1) // (1 << S1)) << S1, int(q[ch[-1]])
     base = qlo - int(q[0])
     span = qhi - qlo
     uo = o[base:base + span + 1]                # G at u = 0 .. span
@@ -98,10 +104,10 @@ def build_table(so, q, o, K):
         if worst(s2) > K:
             raise RuntimeError(f"so={so}: more than {K} changes at one offset")
         first = len(l2) // (2 if K == 3 else 1)
-        base = 4 * n1e + esize * (first - b * (1 << (S1 - s2)))
-        if not -(1 << 23) <= base < (1 << 23):
-            raise RuntimeError(f"so={so}: coarse offset {base} exceeds 24 bits")
-        l1[b] = (base & 0xFFFFFF) | (s2 << 24)
+        base = 4 * n1e + esize * (first - ((qlo + lo) >> s2))
+        if not -(1 << 26) <= base < (1 << 26):
+            raise RuntimeError(f"so={so}: coarse offset {base} exceeds 27 bits")
+        l1[b] = ((base << 5) & 0xFFFFFFFF) | s2
         for fb in range(1 << (S1 - s2)):
             u0 = lo + (fb << s2)
             fields = []
@@ -130,14 +136,14 @@ def lookup(qlo, qhi, l1, l2, q, K):
         v = v.astype(np.int64)
         return np.where(v >= 1 << (bits - 1), v - (1 << bits), v)
 
-    u = np.clip(q, qlo, qhi) - qlo
-    w1 = l1[u >> S1].astype(np.int64)
-    s2 = w1 >> 24
+    c = np.clip(q, qlo, qhi)
+    w1 = sx(l1[(c >> S1) - (qlo >> S1)], 32)
+    s2 = w1 & 31
     n1e = len(l1) + (len(l1) & 1)
     # byte address in the whole table (L1, padding, L2) -> L2 word index
-    addr = sx(w1 & 0xFFFFFF, 24) + (8 if K == 3 else 4) * (u >> s2)
+    addr = (w1 >> 5) + (8 if K == 3 else 4) * (c >> s2)
     f2 = addr // 4 - n1e
-    off = u & ((1 << s2) - 1)
+    off = c & ((1 << s2) - 1)
     a = l2[f2].astype(np.int64)
     o = sx(a & 255, 8)
     o = o + np.where(off >= ((a >> 8) & 511), sx((a >> 17) & 127, 7), 0)
@@ -156,7 +162,7 @@ def main(out):
         o = post(y, so)
         K = 1
         qlo, qhi, l1, l2 = build_table(so, q, o, K)
-        if 4 * (len(l1) + len(l2)) > K1_MAX_BYTES:
+        if 4 * (len(l1) + (len(l1) & 1) + len(l2)) > K1_MAX_BYTES:
             K = 3
             qlo, qhi, l1, l2 = build_table(so, q, o, K)
         if not np.array_equal(lookup(qlo, qhi, l1, l2, q, K), o):
@@ -172,6 +178,7 @@ def main(out):
         f"[{SO_MIN}, {SO_MAX}] (layout in the generator).",
         "namespace hv {",
         f"constexpr int kGeluLutSoMin = {SO_MIN}, kGeluLutSoMax = {SO_MAX};",
+        f"static_assert(kGeluCoarseShift == {S1}, \"coarse bucket width of the tables\");",
         "// n2 entries of k words (k = 1 or 3 changes per entry: 1 or 2 words);",
         "// a table is `words` words from `off`, both multiples of 4",
         "struct GeluLutInfo { int qlo, qhi, n1e, n2, off, k, words; };",

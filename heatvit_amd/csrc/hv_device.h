@@ -241,21 +241,28 @@ __device__ __forceinline__ int gelu_post(i64 v, int shift_in, int shift_out) {
 }
 
 // requant(gelu(q), -16, so - 16, 8) from a GELU step table (layout in
-// gen_gelu_lut.py) staged in LDS at `lut`: [qlo, qhi] the table's clamp.
-// The coarse word of u = clamp(q) - qlo gives the width 2^s2 of its fine
-// entries and a byte offset such that u's entry (K = 1: one word, K = 3:
-// two) sits at offset + entry size * (u >> s2); the entry holds the value
-// at its start and up to K (offset, step) changes inside it.
+// gen_gelu_lut.py) staged in LDS at `lut`: [qlo, qhi] the table's clamp
+// (qlo a multiple of 2^kGeluCoarseShift), cb = -4 * (qlo >> kGeluCoarseShift)
+// the byte offset that makes (c >> kGeluCoarseShift) << 2 address the coarse
+// words.  The coarse word of c = clamp(q)
+// holds s2 in its low five bits and, above them, a byte offset such that
+// c's entry (K = 1: one word, K = 3: two) sits at offset + entry size *
+// (c >> s2); the word itself is the shift amount and the field width (the
+// hardware reads their low five bits).  The entry holds the value at its
+// start and up to K (offset, step) changes inside it.
+constexpr int kGeluCoarseShift = 8;
+
 template <int K>
-__device__ __forceinline__ int gelu_table(int q, const unsigned *lut, int qlo, int qhi) {
+__device__ __forceinline__ int gelu_table(int q, const unsigned *lut, int cb, int qlo, int qhi) {
   int c;
   asm("v_med3_i32 %0, %1, %2, %3" : "=v"(c) : "v"(q), "v"(qlo), "v"(qhi));
-  const unsigned u = (unsigned)(c - qlo);
-  const unsigned w1 = lut[(int)u >> 9];  // u >= 0; the signed shift folds into the address
-  const unsigned s2 = w1 >> 24;
-  const unsigned off = __builtin_amdgcn_ubfe(u, 0, s2);  // u mod 2^s2
-  const int at = __builtin_amdgcn_sbfe((int)w1, 0, 24) + (int)((u >> s2) * (K == 1 ? 4u : 8u));
-  const char *e = reinterpret_cast<const char *>(lut) + at;
+  const char *t = reinterpret_cast<const char *>(lut);
+  int b = c >> kGeluCoarseShift;
+  asm("" : "+v"(b));  // keeps b * 4 + cb one shift-add (not a shift, mask and add)
+  const int w1 = *reinterpret_cast<const int *>(t + cb + b * 4);
+  const unsigned off = __builtin_amdgcn_ubfe((unsigned)c, 0, (unsigned)w1);  // c mod 2^s2
+  const int at = (w1 >> 5) + (c >> (w1 & 31)) * (K == 1 ? 4 : 8);
+  const char *e = t + at;
   if constexpr (K == 1) {
     const unsigned w = *reinterpret_cast<const unsigned *>(e);
     const int o = __builtin_amdgcn_sbfe((int)w, 0, 8);

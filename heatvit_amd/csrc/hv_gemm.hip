@@ -101,7 +101,7 @@ __device__ __noinline__ v2i epi_exact(int epi, int acc, int bias, int res, int s
 // The launch's GELU step table in LDS (gelu_table in hv_device.h).
 template <int K>
 __device__ __forceinline__ int gelu_lut(int q, const unsigned *lut, int qhi, const GemmArgs &g) {
-  return gelu_table<K>(q, lut, g.lut_qlo, qhi);
+  return gelu_table<K>(q, lut, g.lut_cb, g.lut_qlo, qhi);
 }
 
 // Stages the launch's GELU step table in LDS (all threads, then a barrier).
@@ -757,7 +757,7 @@ int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
     g.lut_k = t.k;
     g.lut_words = t.words;
     g.lut_n1e = t.n1e;
-    g.lut_qlo = t.qlo;
+    g.lut_qlo = t.qlo; g.lut_cb = -4 * (t.qlo >> kGeluCoarseShift);
     g.lut_qhi = t.qhi;
   }
   const int esz = epi == EPI_I32 ? 4 : 1;
@@ -789,11 +789,14 @@ int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
 // GELU table and handles one row block.
 // ---------------------------------------------------------------------------
 static constexpr int kFfnRows = 64, kFfnHRow = 784;
+static_assert(kFfnRows * kFfnHRow + 4 * kGeluLutMaxWords <= 160 * 1024 / 2,
+              "the fused FFN's LDS must allow two workgroups per CU");
 
 template <int DIRS1, int DIRS2>
 __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2) {
   __shared__ __attribute__((aligned(16))) int8_t hid[kFfnRows * kFfnHRow];
-  extern __shared__ __attribute__((aligned(16))) unsigned lut[];
+  // static, so its LDS address is a constant the table reads can fold
+  __shared__ __attribute__((aligned(16))) unsigned lut[kGeluLutMaxWords];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, l32 = lane & 31;
   const int M = g1.m_dev ? min(*g1.m_dev, g1.m) : g1.m;
@@ -961,11 +964,11 @@ int launch_ffn(const GemmArgs &g1_in, const GemmArgs &g2_in, hipStream_t s) {
   g1.lut_k = t.k;
   g1.lut_words = t.words;
   g1.lut_n1e = t.n1e;
-  g1.lut_qlo = t.qlo;
+  g1.lut_qlo = t.qlo; g1.lut_cb = -4 * (t.qlo >> kGeluCoarseShift);
   g1.lut_qhi = t.qhi;
   g2.vec_out = 1;
   g2.vec_res = 1;
-  const size_t lds = (size_t)g1.lut_words * 4;
+  const size_t lds = 0;  // the table's LDS is static in k_ffn
   // One workgroup per row block (the dispatcher balances them; a persistent
   // grid left half the workgroups with one block more than the others).
   const dim3 grid((g1.m + kFfnRows - 1) / kFfnRows);
@@ -1009,7 +1012,7 @@ int launch_gelu_post(bool table, const int64_t *in, int64_t *out, int64_t n, int
     g.lut_k = t.k;
     g.lut_words = t.words;
     g.lut_n1e = t.n1e;
-    g.lut_qlo = t.qlo;
+    g.lut_qlo = t.qlo; g.lut_cb = -4 * (t.qlo >> kGeluCoarseShift);
     g.lut_qhi = t.qhi;
   }
   if (n <= 0) return HV_OK;

@@ -49,10 +49,13 @@ def test_table_lookup_is_exact_and_checked(gen, domain, so, k):
     assert np.array_equal(gen.lookup(qlo, qhi, l1, l2, q, k), o)
     # G is constant outside [qlo, qhi]
     assert (o[q <= qlo] == o[q == qlo][0]).all() and (o[q >= qhi] == o[q == qhi][0]).all()
+    assert qlo % (1 << gen.S1) == 0
     bad = l2.copy()
-    # the entry of u = 0 (q = qlo) sits at the first coarse word's byte offset
-    # into the whole table (coarse words, padded to even, then entries)
-    at = int(l1[0]) & 0xFFFFFF
-    at = at - (1 << 24) if at >= 1 << 23 else at
+    # the entry of q = qlo sits at the first coarse word's byte offset plus
+    # the entry size times qlo >> s2, into the whole table (coarse words,
+    # padded to even, then entries)
+    w = int(l1[0])
+    w = w - (1 << 32) if w >= 1 << 31 else w
+    at = (w >> 5) + (8 if k == 3 else 4) * (qlo >> (w & 31))
     bad[at // 4 - (len(l1) + (len(l1) & 1))] ^= 1   # value at qlo, off by one
     assert not np.array_equal(gen.lookup(qlo, qhi, l1, bad, q, k), o)
