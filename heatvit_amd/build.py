@@ -23,6 +23,9 @@ FLAGS = [
     "-Wno-unused-function", "-Wno-unused-variable",
     # Packed FP32 instructions are kept out of every code object.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs: the epilogues then read them
+    # without a v_accvgpr_read per element (and need fewer registers).
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I", str(HERE.parent / "include"), "-I", str(OBJ),
 ]
 
