@@ -10,27 +10,23 @@ multiple of 2^S1 = 256 (rounded down from the last value below the first
 change).  Table layout (32-bit words):
   L1[b], b = (c >> S1) - (qlo >> S1) with c = clamp(q, qlo, qhi): bits 0..4
       s2, bits 5..31 a signed byte offset, from the table's start, chosen
-      so that the entry of c is at offset + E * (c >> s2) (E = 4 or 8 bytes
-      per entry, arithmetic shift; the bucket starts at a multiple of 2^S1,
-      so its entries start at multiples of 2^s2).  A lookup reads c >> s2
-      and c mod 2^s2 with the word itself as the shift amount and the
-      field width (the hardware takes its low five bits);
+      so that the entry of c is at offset + 4 * (c >> s2) (arithmetic
+      shift; the bucket starts at a multiple of 2^S1, so its entries start
+      at multiples of 2^s2).  A lookup reads c >> s2 and c mod 2^s2 with the
+      word itself as the shift amount and the field width (the hardware
+      takes its low five bits);
   (L1 holds n1e words, its length rounded up to even; L2 follows it)
-  L2, one entry per 2^s2 values of c: G at the entry's first c and up to K
-      changes inside the entry, each an offset (9 bits, 511 = none) and the
-      signed 7-bit step taken from that offset on.  K = 1: one word per entry,
-        T[0:8] B1[8:17] D1[17:24];
-      K = 3: two words per entry,
-        word 0: T[0:8] B1[8:17] D1[17:24]
-        word 1: B2[0:9] D2[9:16] B3[16:25] D3[25:32].
+  L2, one word per 2^s2 values of c, at most one change inside it: byte 0
+      G at the entry's first c, byte 1 G from the change on (byte 0 again
+      when there is none), byte 2 the change's offset inside the entry
+      (< 2^s2 <= 256).  The lookup is byte 1 when c mod 2^s2 >= byte 2, else
+      byte 0: one byte compare and one byte select.
   G is constant for q <= qlo and for q >= qhi.  Each table is padded to a
-  multiple of four words, so tables start on 16-byte boundaries.  s2 is the largest value in
-  [0, S1] that leaves at most K changes inside every entry of the bucket.
-  Each so gets the one-change form when that table fits in 31,744 bytes,
-  the LDS the fused FFN kernel has beside its 50,176-byte hidden block at
-  two workgroups per CU (fewer
-  operations per lookup), the three-change form otherwise (a smaller table
-  where the rounding of rsa makes G wiggle).
+  multiple of four words, so tables start on 16-byte boundaries.  s2 is the
+  largest value in [0, S1] that leaves at most one change inside every entry
+  of the bucket.  Every table must fit in 31,744 bytes, the LDS the fused
+  FFN kernel has beside its 50,176-byte hidden block at two workgroups per
+  CU.
 
 The generator restates gelu in numpy, builds each table, emulates the
 lookup for every q of the 24-bit domain and refuses to write a table that
@@ -45,7 +41,7 @@ import numpy as np
 
 SO_MIN, SO_MAX = 3, 12
 S1 = 8
-K1_MAX_BYTES = 31744
+MAX_BYTES = 31744
 
 
 def gelu_q16(x):
@@ -75,19 +71,17 @@ def post(y, so):
     return np.clip(rsa(y, so), -128, 127)
 
 
-def build_table(so, q, o, K):
-    """(qlo, qhi, L1 words, L2 words) of G_so with at most K (1 or 3)
-    changes per entry, given o = G_so(q) over the whole domain q
-    (ascending)."""
+def build_table(so, q, o):
+    """(qlo, qhi, L1 words, L2 words) of G_so with at most one change per
+    entry, given o = G_so(q) over the whole domain q (ascending)."""
     ch = np.nonzero(np.diff(o))[0] + 1          # o[i] != o[i - 1]
     qlo, qhi = (int(q[ch[0]] - 1) // (1 << S1)) << S1, int(q[ch[-1]])
     base = qlo - int(q[0])
     span = qhi - qlo
-    uo = o[base:base + span + 1]                # G at u = 0 .. span
+    uo = o[base:base + span + 1]                # G at u = c - qlo = 0 .. span
     cu = ch - base                              # change positions in u
     n1 = span // (1 << S1) + 1
     n1e = n1 + (n1 & 1)
-    esize = 8 if K == 3 else 4
     l1 = np.zeros(n1, np.uint32)
     l2 = []
     for b in range(n1):
@@ -99,38 +93,27 @@ def build_table(so, q, o, K):
             return int(np.bincount(inner >> s2).max()) if len(inner) else 0
 
         s2 = S1
-        while s2 > 0 and worst(s2) > K:
+        while s2 > 0 and worst(s2) > 1:
             s2 -= 1
-        if worst(s2) > K:
-            raise RuntimeError(f"so={so}: more than {K} changes at one offset")
-        first = len(l2) // (2 if K == 3 else 1)
-        base = 4 * n1e + esize * (first - ((qlo + lo) >> s2))
-        if not -(1 << 26) <= base < (1 << 26):
-            raise RuntimeError(f"so={so}: coarse offset {base} exceeds 27 bits")
-        l1[b] = ((base << 5) & 0xFFFFFFFF) | s2
+        if worst(s2) > 1:
+            raise RuntimeError(f"so={so}: more than one change at one offset")
+        off = 4 * n1e + 4 * (len(l2) - ((qlo + lo) >> s2))
+        if not -(1 << 26) <= off < (1 << 26):
+            raise RuntimeError(f"so={so}: coarse offset {off} exceeds 27 bits")
+        l1[b] = ((off << 5) & 0xFFFFFFFF) | s2
         for fb in range(1 << (S1 - s2)):
             u0 = lo + (fb << s2)
-            fields = []
+            t0 = int(uo[min(u0, span)])
+            t1, at = t0, 255
             for c in sel[(sel >> s2) == fb]:
                 d = int(c) - (fb << s2)
-                if d == 0:
-                    continue                    # T already holds it
-                step = int(uo[lo + c] - uo[lo + c - 1])
-                if not -64 <= step < 64:
-                    raise RuntimeError(f"so={so}: step {step} exceeds 7 bits")
-                fields.append((d, step & 127))
-            fields += [(511, 0)] * (K - len(fields))
-            t = int(uo[min(u0, span)]) & 255
-            w0 = t | (fields[0][0] << 8) | (fields[0][1] << 17)
-            if K == 1:
-                l2.append(w0)
-            else:
-                w1 = fields[1][0] | (fields[1][1] << 9) | (fields[2][0] << 16) | (fields[2][1] << 25)
-                l2 += [w0, w1]
+                if d:                           # d == 0: t0 already holds it
+                    t1, at = int(uo[lo + c]), d
+            l2.append((t0 & 255) | ((t1 & 255) << 8) | (at << 16))
     return qlo, qhi, l1, np.array(l2, np.uint32)
 
 
-def lookup(qlo, qhi, l1, l2, q, K):
+def lookup(qlo, qhi, l1, l2, q):
     """The device lookup, restated over an array of q."""
     def sx(v, bits):
         v = v.astype(np.int64)
@@ -141,17 +124,10 @@ def lookup(qlo, qhi, l1, l2, q, K):
     s2 = w1 & 31
     n1e = len(l1) + (len(l1) & 1)
     # byte address in the whole table (L1, padding, L2) -> L2 word index
-    addr = (w1 >> 5) + (8 if K == 3 else 4) * (c >> s2)
-    f2 = addr // 4 - n1e
+    f2 = ((w1 >> 5) + 4 * (c >> s2)) // 4 - n1e
     off = c & ((1 << s2) - 1)
     a = l2[f2].astype(np.int64)
-    o = sx(a & 255, 8)
-    o = o + np.where(off >= ((a >> 8) & 511), sx((a >> 17) & 127, 7), 0)
-    if K == 3:
-        b = l2[f2 + 1].astype(np.int64)
-        o = o + np.where(off >= (b & 511), sx((b >> 9) & 127, 7), 0)
-        o = o + np.where(off >= ((b >> 16) & 511), sx((b >> 25) & 127, 7), 0)
-    return o
+    return sx(np.where(off >= ((a >> 16) & 255), (a >> 8) & 255, a & 255), 8)
 
 
 def main(out):
@@ -160,17 +136,15 @@ def main(out):
     words, info = [], []
     for so in range(SO_MIN, SO_MAX + 1):
         o = post(y, so)
-        K = 1
-        qlo, qhi, l1, l2 = build_table(so, q, o, K)
-        if 4 * (len(l1) + (len(l1) & 1) + len(l2)) > K1_MAX_BYTES:
-            K = 3
-            qlo, qhi, l1, l2 = build_table(so, q, o, K)
-        if not np.array_equal(lookup(qlo, qhi, l1, l2, q, K), o):
+        qlo, qhi, l1, l2 = build_table(so, q, o)
+        if not np.array_equal(lookup(qlo, qhi, l1, l2, q), o):
             raise RuntimeError(f"so={so}: table lookup differs from the post-op")
         n1e = len(l1) + (len(l1) & 1)
         body = list(l1) + [0] * (n1e - len(l1)) + list(l2)
         body += [0] * (-len(body) % 4)          # 16-byte multiples
-        info.append((qlo, qhi, n1e, len(l2) // (2 if K == 3 else 1), len(words), K, len(body)))
+        if 4 * len(body) > MAX_BYTES:
+            raise RuntimeError(f"so={so}: table of {4 * len(body)} bytes exceeds {MAX_BYTES}")
+        info.append((qlo, qhi, n1e, len(l2), len(words), len(body)))
         words += body
     lines = [
         "// Generated by gen_gelu_lut.py: step tables of",
@@ -179,9 +153,9 @@ def main(out):
         "namespace hv {",
         f"constexpr int kGeluLutSoMin = {SO_MIN}, kGeluLutSoMax = {SO_MAX};",
         f"static_assert(kGeluCoarseShift == {S1}, \"coarse bucket width of the tables\");",
-        "// n2 entries of k words (k = 1 or 3 changes per entry: 1 or 2 words);",
-        "// a table is `words` words from `off`, both multiples of 4",
-        "struct GeluLutInfo { int qlo, qhi, n1e, n2, off, k, words; };",
+        "// n2 one-word entries; a table is `words` words from `off`, both",
+        "// multiples of 4",
+        "struct GeluLutInfo { int qlo, qhi, n1e, n2, off, words; };",
         "constexpr GeluLutInfo kGeluLutInfo[] = {",
     ]
     lines += [f"  {{{', '.join(str(v) for v in t)}}}," for t in info]

@@ -244,16 +244,16 @@ __device__ __forceinline__ int gelu_post(i64 v, int shift_in, int shift_out) {
 // gen_gelu_lut.py) staged in LDS at `lut`: [qlo, qhi] the table's clamp
 // (qlo a multiple of 2^kGeluCoarseShift), cb = -4 * (qlo >> kGeluCoarseShift)
 // the byte offset that makes (c >> kGeluCoarseShift) << 2 address the coarse
-// words.  The coarse word of c = clamp(q)
-// holds s2 in its low five bits and, above them, a byte offset such that
-// c's entry (K = 1: one word, K = 3: two) sits at offset + entry size *
-// (c >> s2); the word itself is the shift amount and the field width (the
-// hardware reads their low five bits).  The entry holds the value at its
-// start and up to K (offset, step) changes inside it.
+// words.  The coarse word of c = clamp(q) holds s2 in its low five bits and,
+// above them, a byte offset such that c's entry sits at offset + 4 * (c >>
+// s2); the word itself is the shift amount and the field width (the hardware
+// reads their low five bits).  The entry's bytes are the value before and
+// after its one change and the change's offset: the result is the value in
+// the low byte of the returned word (the upper bits are not cleared).
 constexpr int kGeluCoarseShift = 8;
 
-template <int K>
-__device__ __forceinline__ int gelu_table(int q, const unsigned *lut, int cb, int qlo, int qhi) {
+__device__ __forceinline__ unsigned gelu_table_u8(int q, const unsigned *lut, int cb, int qlo,
+                                                  int qhi) {
   int c;
   asm("v_med3_i32 %0, %1, %2, %3" : "=v"(c) : "v"(q), "v"(qlo), "v"(qhi));
   const char *t = reinterpret_cast<const char *>(lut);
@@ -261,20 +261,13 @@ __device__ __forceinline__ int gelu_table(int q, const unsigned *lut, int cb, in
   asm("" : "+v"(b));  // keeps b * 4 + cb one shift-add (not a shift, mask and add)
   const int w1 = *reinterpret_cast<const int *>(t + cb + b * 4);
   const unsigned off = __builtin_amdgcn_ubfe((unsigned)c, 0, (unsigned)w1);  // c mod 2^s2
-  const int at = (w1 >> 5) + (c >> (w1 & 31)) * (K == 1 ? 4 : 8);
-  const char *e = t + at;
-  if constexpr (K == 1) {
-    const unsigned w = *reinterpret_cast<const unsigned *>(e);
-    const int o = __builtin_amdgcn_sbfe((int)w, 0, 8);
-    return o + (off >= __builtin_amdgcn_ubfe(w, 8, 9) ? __builtin_amdgcn_sbfe((int)w, 17, 7) : 0);
-  } else {
-    const uint2 w2 = *reinterpret_cast<const uint2 *>(e);
-    int o = __builtin_amdgcn_sbfe((int)w2.x, 0, 8);
-    o += off >= __builtin_amdgcn_ubfe(w2.x, 8, 9) ? __builtin_amdgcn_sbfe((int)w2.x, 17, 7) : 0;
-    o += off >= __builtin_amdgcn_ubfe(w2.y, 0, 9) ? __builtin_amdgcn_sbfe((int)w2.y, 9, 7) : 0;
-    o += off >= __builtin_amdgcn_ubfe(w2.y, 16, 9) ? __builtin_amdgcn_sbfe((int)w2.y, 25, 7) : 0;
-    return o;
-  }
+  const unsigned w = *reinterpret_cast<const unsigned *>(t + (w1 >> 5) + (c >> (w1 & 31)) * 4);
+  return off >= __builtin_amdgcn_ubfe(w, 16, 8) ? w >> 8 : w;
+}
+
+// The same as a sign-extended int.
+__device__ __forceinline__ int gelu_table(int q, const unsigned *lut, int cb, int qlo, int qhi) {
+  return (int)(int8_t)gelu_table_u8(q, lut, cb, qlo, qhi);
 }
 
 // plan_sigmoid (nonlinear.py:83-95).

@@ -98,10 +98,10 @@ __device__ __noinline__ v2i epi_exact(int epi, int acc, int bias, int res, int s
              t};
 }
 
-// The launch's GELU step table in LDS (gelu_table in hv_device.h).
-template <int K>
-__device__ __forceinline__ int gelu_lut(int q, const unsigned *lut, int qhi, const GemmArgs &g) {
-  return gelu_table<K>(q, lut, g.lut_cb, g.lut_qlo, qhi);
+// The launch's GELU step table in LDS (gelu_table_u8 in hv_device.h): the
+// post-op's int8 value in the low byte.
+__device__ __forceinline__ unsigned gelu_lut(int q, const unsigned *lut, int qhi, const GemmArgs &g) {
+  return gelu_table_u8(q, lut, g.lut_cb, g.lut_qlo, qhi);
 }
 
 // Stages the launch's GELU step table in LDS (all threads, then a barrier).
@@ -221,7 +221,7 @@ __device__ __forceinline__ void epi_tile(const GemmArgs &g, const v16i (&acc)[MT
             o[j] = rq_dir_nowrap<LA>(v, rq_a);
           } else if (EPI == EPI_GELU && (DIRS & 4)) {
             // the table's clamp [qlo, qhi] lies inside the 24-bit range
-            o[j] = gelu_lut<(DIRS & 8) ? 1 : 3>(shift_nowrap<LA>(v, rq_a), lut, qhi, g);
+            o[j] = (int)gelu_lut(shift_nowrap<LA>(v, rq_a), lut, qhi, g);
           } else if (EPI == EPI_GELU) {
             o[j] = rq_dir<LB>(gelu_q16(rq_dir_nowrap<LA>(v, rq_a)), rq_b);
           } else if (RESLIKE) {
@@ -626,8 +626,7 @@ static int epilogue_dirs(const GemmArgs &g, int epi) {
 
 // Launches kernel template K with FAST = false, or FAST = true and the
 // launch's requant directions (bit 2: the GELU post-op from its step table,
-// staged in dynamic LDS, direct kernel only; bit 3: that table has one
-// change per entry).
+// staged in dynamic LDS, direct kernel only).
 template <int EPI, template <bool, int> class K>
 static int launch_epi(const GemmArgs &g, long long grid, int n_blocks, hipStream_t s) {
   const dim3 gd((unsigned)grid), bd(256);
@@ -640,13 +639,8 @@ static int launch_epi(const GemmArgs &g, long long grid, int n_blocks, hipStream
         // persistent: each workgroup stages the table once
         const dim3 gp((unsigned)(grid < kLutGridCap ? grid : kLutGridCap));
         const size_t lds = (size_t)g.lut_words * 4;
-        if (g.lut_k == 1) {
-          if (dirs & 1) hv_launch(K<true, 13>::fn(), gp, bd, lds, s, g, n_blocks);
-          else hv_launch(K<true, 12>::fn(), gp, bd, lds, s, g, n_blocks);
-        } else {
-          if (dirs & 1) hv_launch(K<true, 5>::fn(), gp, bd, lds, s, g, n_blocks);
-          else hv_launch(K<true, 4>::fn(), gp, bd, lds, s, g, n_blocks);
-        }
+        if (dirs & 1) hv_launch(K<true, 5>::fn(), gp, bd, lds, s, g, n_blocks);
+        else hv_launch(K<true, 4>::fn(), gp, bd, lds, s, g, n_blocks);
         return check_hip(hipGetLastError(), "k_gemm launch");
       }
     }
@@ -754,7 +748,6 @@ int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
   if (epi == EPI_GELU && g.shift_b >= kGeluLutSoMin && g.shift_b <= kGeluLutSoMax) {
     const GeluLutInfo &t = kGeluLutInfo[g.shift_b - kGeluLutSoMin];
     g.lut_off = t.off;
-    g.lut_k = t.k;
     g.lut_words = t.words;
     g.lut_n1e = t.n1e;
     g.lut_qlo = t.qlo; g.lut_cb = -4 * (t.qlo >> kGeluCoarseShift);
@@ -806,7 +799,6 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2) {
   const Rq r1a = rq_setup(g1.shift_a, -(1 << 23), (1 << 23) - 1);
   const Rq r2a = rq_setup(g2.shift_a, -128, 127), r2b = rq_setup(g2.os, -128, 127);
   constexpr bool LA1 = DIRS1 & 1;
-  constexpr int K1 = (DIRS1 & 8) ? 1 : 3;
   int qhi = g1.lut_qhi;
   asm("" : "+v"(qhi));  // the table clamp as one med3 (both bounds in VGPRs)
 
@@ -861,8 +853,8 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2) {
         if (fast) {
 #pragma unroll
           for (int j = 0; j < 16; ++j)
-            o[j] = gelu_lut<K1>(shift_nowrap<LA1>(acc[rt][j] + bs[cur][j >> 2][j & 3], r1a), lut,
-                                qhi, g1);
+            o[j] = (int)gelu_lut(shift_nowrap<LA1>(acc[rt][j] + bs[cur][j >> 2][j & 3], r1a),
+                                 lut, qhi, g1);
         } else {
 #pragma unroll
           for (int j = 0; j < 16; ++j)
@@ -961,7 +953,6 @@ int launch_ffn(const GemmArgs &g1_in, const GemmArgs &g2_in, hipStream_t s) {
   if (!fast_epilogue(g1, EPI_GELU) || !fast_epilogue(g2, EPI_RES)) return 1;
   const GeluLutInfo &t = kGeluLutInfo[g1.shift_b - kGeluLutSoMin];
   g1.lut_off = t.off;
-  g1.lut_k = t.k;
   g1.lut_words = t.words;
   g1.lut_n1e = t.n1e;
   g1.lut_qlo = t.qlo; g1.lut_cb = -4 * (t.qlo >> kGeluCoarseShift);
@@ -973,13 +964,8 @@ int launch_ffn(const GemmArgs &g1_in, const GemmArgs &g2_in, hipStream_t s) {
   // grid left half the workgroups with one block more than the others).
   const dim3 grid((g1.m + kFfnRows - 1) / kFfnRows);
   const int d1 = epilogue_dirs(g1, EPI_GELU) & 1, d2 = epilogue_dirs(g2, EPI_RES);
-  if (g1.lut_k == 1) {
-    if (d1) launch_ffn_d<13>(g1, g2, d2, grid, lds, s);
-    else launch_ffn_d<12>(g1, g2, d2, grid, lds, s);
-  } else {
-    if (d1) launch_ffn_d<5>(g1, g2, d2, grid, lds, s);
-    else launch_ffn_d<4>(g1, g2, d2, grid, lds, s);
-  }
+  if (d1) launch_ffn_d<5>(g1, g2, d2, grid, lds, s);
+  else launch_ffn_d<4>(g1, g2, d2, grid, lds, s);
   return check_hip(hipGetLastError(), "k_ffn launch");
 }
 
@@ -994,7 +980,7 @@ __global__ __launch_bounds__(256) void k_gelu_post(int table, const int64_t *in,
     const int64_t v = in[i];
     const int q = (int)(v < -(1 << 23) ? -(1 << 23) : (v > (1 << 23) - 1 ? (1 << 23) - 1 : v));
     out[i] = !table ? rq(gelu_q16(q), rb)
-                    : g.lut_k == 1 ? gelu_lut<1>(q, lut, g.lut_qhi, g) : gelu_lut<3>(q, lut, g.lut_qhi, g);
+                    : (int)(int8_t)gelu_lut(q, lut, g.lut_qhi, g);
   }
 }
 
@@ -1009,7 +995,6 @@ int launch_gelu_post(bool table, const int64_t *in, int64_t *out, int64_t n, int
                   so, kGeluLutSoMin, kGeluLutSoMax);
     const GeluLutInfo &t = kGeluLutInfo[so - kGeluLutSoMin];
     g.lut_off = t.off;
-    g.lut_k = t.k;
     g.lut_words = t.words;
     g.lut_n1e = t.n1e;
     g.lut_qlo = t.qlo; g.lut_cb = -4 * (t.qlo >> kGeluCoarseShift);

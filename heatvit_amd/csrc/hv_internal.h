@@ -53,9 +53,9 @@ struct GemmArgs {
   int vec_out;     // c (and aux) allow 16-byte row stores
   int vec_res;     // res (or pos) allow 16-byte row loads
   // GELU post-op step table (gen_gelu_lut.py), staged in LDS when
-  // lut_words > 0: words [lut_off, lut_off + lut_words) of kGeluLut, with
-  // lut_k (1 or 3) changes per fine entry; lut_cb = -4 * (lut_qlo >> kGeluCoarseShift).
-  int lut_off, lut_words, lut_n1e, lut_qlo, lut_qhi, lut_k, lut_cb;
+  // lut_words > 0: words [lut_off, lut_off + lut_words) of kGeluLut;
+  // lut_cb = -4 * (lut_qlo >> kGeluCoarseShift).
+  int lut_off, lut_words, lut_n1e, lut_qlo, lut_qhi, lut_cb;
 };
 
 // epilogue: HV_EPI_* or 4 (patch: A_PATCH gather, position-row residual).

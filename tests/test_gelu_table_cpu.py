@@ -41,21 +41,23 @@ def test_post_op_matches_requant(oracle, gen, domain):
         assert np.array_equal(gen.post(y[idx], so), want), so
 
 
-@pytest.mark.parametrize("so,k", [(3, 1), (3, 3), (7, 3), (12, 1)])
-def test_table_lookup_is_exact_and_checked(gen, domain, so, k):
+@pytest.mark.parametrize("so", [3, 6, 7, 12])
+def test_table_lookup_is_exact_and_checked(gen, domain, so):
     q, y = domain
     o = gen.post(y, so)
-    qlo, qhi, l1, l2 = gen.build_table(so, q, o, k)
-    assert np.array_equal(gen.lookup(qlo, qhi, l1, l2, q, k), o)
+    qlo, qhi, l1, l2 = gen.build_table(so, q, o)
+    assert np.array_equal(gen.lookup(qlo, qhi, l1, l2, q), o)
     # G is constant outside [qlo, qhi]
     assert (o[q <= qlo] == o[q == qlo][0]).all() and (o[q >= qhi] == o[q == qhi][0]).all()
     assert qlo % (1 << gen.S1) == 0
+    n1e = len(l1) + (len(l1) & 1)
+    assert 4 * (n1e + len(l2)) <= gen.MAX_BYTES
     bad = l2.copy()
     # the entry of q = qlo sits at the first coarse word's byte offset plus
-    # the entry size times qlo >> s2, into the whole table (coarse words,
-    # padded to even, then entries)
+    # 4 * (qlo >> s2), into the whole table (coarse words, padded to even,
+    # then entries)
     w = int(l1[0])
     w = w - (1 << 32) if w >= 1 << 31 else w
-    at = (w >> 5) + (8 if k == 3 else 4) * (qlo >> (w & 31))
-    bad[at // 4 - (len(l1) + (len(l1) & 1))] ^= 1   # value at qlo, off by one
-    assert not np.array_equal(gen.lookup(qlo, qhi, l1, bad, q, k), o)
+    at = (w >> 5) + 4 * (qlo >> (w & 31))
+    bad[at // 4 - n1e] ^= 1   # value at qlo, off by one
+    assert not np.array_equal(gen.lookup(qlo, qhi, l1, bad, q), o)
