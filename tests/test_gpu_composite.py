@@ -43,19 +43,26 @@ def test_block_ragged_batch_vs_oracle(oracle):
             assert np.array_equal(cks[i][k], ck[k]), (i, k)
 
 
-def test_fused_ffn_wide_biases_and_ragged_rows_vs_oracle(oracle):
+@pytest.mark.parametrize("wide", ["b1", "b2", "both"])
+def test_fused_ffn_wide_biases_and_ragged_rows_vs_oracle(oracle, wide):
     """Without checkpoints the block's FFN runs as one fused kernel (hidden
-    rows in LDS); FFN1 biases beyond the int32 epilogue bound send their
-    column tiles to the exact 64-bit GELU, and ragged images leave partial
+    rows in LDS); an FFN1 or FFN2 bias beyond the int32 epilogue bound sends
+    that phase to the exact 64-bit forms, and ragged images leave partial
     64-row blocks."""
     import dataclasses
     from heatvit_amd.transformer import transformer_block_batch
     _, bp = synth.block_workload()
     b1 = np.asarray(bp.ffn.b1).astype(np.int64).copy()
-    b1[5] = (1 << 31) - 1
-    b1[300:310] = -(1 << 31)
-    b1[700] = (1 << 30)
-    bp = dataclasses.replace(bp, ffn=dataclasses.replace(bp.ffn, b1=b1))
+    b2 = np.asarray(bp.ffn.b2).astype(np.int64).copy()
+    if wide in ("b1", "both"):
+        b1[5] = (1 << 31) - 1
+        b1[300:310] = -(1 << 31)
+        b1[700] = (1 << 30)
+    if wide in ("b2", "both"):
+        b2[0] = -(1 << 31)
+        b2[191] = (1 << 31) - 1
+        b2[77] = -(1 << 30)
+    bp = dataclasses.replace(bp, ffn=dataclasses.replace(bp.ffn, b1=b1, b2=b2))
     rng = np.random.default_rng(8)
     lens = [197, 63, 1, 65, 130, 197, 7]
     xs = [rng.integers(-128, 128, (n, 192)).astype(np.int8) for n in lens]
