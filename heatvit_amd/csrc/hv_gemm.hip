@@ -873,7 +873,7 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2) {
       rt = t / 6;
       ct = t - rt * 6;
     };
-    v4i wb[2][4], bias4[1][4], res4[1][1];
+    v4i wb[3][4], bias4[1][4], res4[1][1];
     int rt, ct;
     tile_of(0, rt, ct);
     {
@@ -881,11 +881,15 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2) {
       epi_operands<1, 1, EPI_RES>(g2, arow, ct, h, bias4, res4);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      wb[0][j] = *reinterpret_cast<const v4i *>(g2.b + ((size_t)ct * 24 + j) * 1024 + lane * 16);
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        wb[c][j] = *reinterpret_cast<const v4i *>(g2.b + ((size_t)ct * 24 + c * 4 + j) * 1024 +
+                                                  lane * 16);
     __syncthreads();
     // Phase B: tiles wave, wave + 4, wave + 8 of the 2 x 6; 24 K-steps in
-    // chunks of 4, the next chunk (or the next tile's first) in flight.
+    // chunks of 4 through a ring of three chunk buffers: the chunk two
+    // ahead (within the tile or the next tile's first two) is in flight.
 #pragma unroll 1
     for (int ti = 0; ti < 3; ++ti) {
       const int8_t *hp = &hid[(32 * rt + l32) * kFfnHRow + 16 * h];
@@ -895,16 +899,16 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2) {
       v16i acc[1][1] = {{v16i{0}}};
 #pragma unroll
       for (int c = 0; c < 6; ++c) {
-        const int cur = c & 1;
-        if (c + 1 < 6) {
+        const int cur = c % 3, nxt = (c + 2) % 3;
+        if (c + 2 < 6) {
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            wb[cur ^ 1][j] = *reinterpret_cast<const v4i *>(bp + ((c + 1) * 4 + j) * 1024);
+            wb[nxt][j] = *reinterpret_cast<const v4i *>(bp + ((c + 2) * 4 + j) * 1024);
         } else if (ti + 1 < 3) {
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            wb[cur ^ 1][j] =
-                *reinterpret_cast<const v4i *>(g2.b + ((size_t)nct * 24 + j) * 1024 + lane * 16);
+            wb[nxt][j] = *reinterpret_cast<const v4i *>(
+                g2.b + ((size_t)nct * 24 + (c - 4) * 4 + j) * 1024 + lane * 16);
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
