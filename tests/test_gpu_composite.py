@@ -72,6 +72,51 @@ def test_fused_ffn_wide_biases_and_ragged_rows_vs_oracle(oracle, wide):
         assert np.array_equal(zs[i], z), i
 
 
+# Ragged token counts of a pruned stage: partial 32-row tiles and 64-row
+# FFN blocks, images of one and two key tiles, many small images.
+RAGGED_LENS = [1, 2, 16, 17, 31, 32, 33, 63, 64, 65, 100, 128, 129, 150, 197] + [3] * 16
+
+
+def _ragged_batch(rng, lens=RAGGED_LENS):
+    return [rng.integers(-128, 128, (n, 192)).astype(np.int8) for n in lens]
+
+
+@pytest.mark.parametrize("blk", range(12))
+def test_block_every_model_block_ragged_vs_oracle(oracle, blk):
+    """Every block of the 256-image workload's model (its requant
+    directions, attention modes and GELU tables differ) over a ragged batch
+    of mostly small images, against the oracle."""
+    from heatvit_amd.transformer import transformer_block_batch
+    _, params = synth.throughput_workload(1)
+    bp = params.blocks[blk]
+    xs = _ragged_batch(np.random.default_rng(100 + blk))
+    zs = transformer_block_batch(xs, bp)
+    for i, x in enumerate(xs):
+        z, _ = oracle.transformer_block(x, bp, checkpoints=False)
+        assert np.array_equal(zs[i], z), (blk, i, len(x))
+
+
+def test_block_wide_biases_all_gemms_vs_oracle(oracle):
+    """Biases beyond the int32 epilogue bounds in all four GEMMs send their
+    tiles to the exact 64-bit forms."""
+    import dataclasses
+    from heatvit_amd.transformer import transformer_block_batch
+    _, bp = synth.block_workload()
+    f = lambda v: np.asarray(v).astype(np.int64).copy()
+    bqkv, bproj, b1, b2 = f(bp.mhsa.bqkv), f(bp.mhsa.bproj), f(bp.ffn.b1), f(bp.ffn.b2)
+    bqkv[[0, 200, 575]] = [(1 << 31) - 1, -(1 << 31), 1 << 30]
+    bproj[[3, 191]] = [-(1 << 31), (1 << 31) - 1]
+    b1[[5, 300, 767]] = [(1 << 31) - 1, -(1 << 31), -(1 << 30)]
+    b2[[0, 100]] = [-(1 << 31), (1 << 31) - 1]
+    bp = dataclasses.replace(bp, mhsa=dataclasses.replace(bp.mhsa, bqkv=bqkv, bproj=bproj),
+                             ffn=dataclasses.replace(bp.ffn, b1=b1, b2=b2))
+    xs = _ragged_batch(np.random.default_rng(9))
+    zs = transformer_block_batch(xs, bp)
+    for i, x in enumerate(xs):
+        z, _ = oracle.transformer_block(x, bp, checkpoints=False)
+        assert np.array_equal(zs[i], z), (i, len(x))
+
+
 def test_selector_matches_golden():
     from heatvit_amd.selector import token_selector_batch
     meta, arrays = gio.load("selector")
