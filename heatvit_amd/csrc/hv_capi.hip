@@ -220,12 +220,6 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   }
   if (rc) return rc;
 
-  {
-    ProfScope ps(HV_PROF_LAYERNORM, s);
-    rc = launch_layernorm(y, p.ln2_gamma, p.ln2_beta, ln2, max_rows, rows_dev, p.ffn_x_exp,
-                          p.gamma2_exp, p.beta2_exp, p.ln2_out_exp, nullptr, lw, s);
-  }
-  if (rc) return rc;
   GemmArgs g1{};
   g1.a = ln2; g1.b = p.w1_p; g1.bias = p.b1; g1.c = hidden; g1.m_dev = rows_dev;
   g1.m = max_rows; g1.n = 768; g1.k = 192; g1.lda = 192; g1.ldc = 768;
@@ -238,6 +232,24 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   g2.ldr = 192;
   g2.shift_a = p.ffn_out_exp - (p.hidden_out_exp + p.w2_exp);
   g2.mid_exp = p.ffn_out_exp; g2.res_exp = p.ffn_x_exp; g2.out_exp = p.out_exp;
+  // LayerNorm 2 inside the fused FFN kernel (its rows pass through LDS)
+  // when neither its output nor the hidden rows are wanted and its
+  // exponents take the int32 form.
+  Ln32 ln;
+  if (!(ck && (ck->hidden || ck->ln2)) &&
+      ln32_setup(p.ln2_gamma, p.ln2_beta, ln2, p.ffn_x_exp, p.gamma2_exp, p.beta2_exp,
+                 p.ln2_out_exp, &ln)) {
+    const FfnLn fl{y, ln, lw};
+    ProfScope ps(HV_PROF_FFN, s);
+    rc = launch_ffn(g1, g2, s, &fl);
+    if (rc != 1) return rc;
+  }
+  {
+    ProfScope ps(HV_PROF_LAYERNORM, s);
+    rc = launch_layernorm(y, p.ln2_gamma, p.ln2_beta, ln2, max_rows, rows_dev, p.ffn_x_exp,
+                          p.gamma2_exp, p.beta2_exp, p.ln2_out_exp, nullptr, lw, s);
+  }
+  if (rc) return rc;
   // One fused kernel (hidden rows in LDS) unless the hidden checkpoint is
   // wanted or the exponents need the general epilogues.
   if (!(ck && ck->hidden)) {

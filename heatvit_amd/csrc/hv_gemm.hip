@@ -781,12 +781,102 @@ int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
 // The hidden activations never leave the CU.  Each workgroup stages the
 // GELU table and handles one row block.
 // ---------------------------------------------------------------------------
-static constexpr int kFfnRows = 64, kFfnHRow = 784;
+static constexpr int kFfnRows = 64, kFfnHRow = 784, kFfnLnRow = 208;
 static_assert(kFfnRows * kFfnHRow + 4 * kGeluLutMaxWords <= 160 * 1024 / 2,
               "the fused FFN's LDS must allow two workgroups per CU");
+static_assert(kFfnRows * kFfnLnRow <= kFfnRows * kFfnHRow, "LayerNorm rows fit the hidden block");
 
-template <int DIRS1, int DIRS2>
-__global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2) {
+// The LayerNorm in front of FFN1 (transformer.py:349-352; nonlinear.py:
+// 136-186, the int32 form of k_layernorm32): rows r0 .. r0 + 63 of x by the
+// workgroup's 32 eight-lane groups, group j taking rows j and j + 32 (rows
+// past M repeat row M - 1 and are not reported), each lane 24 channels.
+// Lane sub works out the constants of row sub % 2 and the group reads them
+// from lanes 0 and 1, so the 64/128-bit set-up runs four times per row
+// instead of eight.  The int8 rows go to dst at a 208-byte stride, which
+// the A-fragment reads (16 bytes at row l, offset 32k + 16h) take without
+// bank conflicts.
+__device__ __forceinline__ void ffn_layernorm(const FfnLn &f, int r0, int M, int8_t *dst) {
+  const int tid = threadIdx.x, sub = tid & 7, grp = tid >> 3;
+  const Ln32 &ln = f.ln;
+  int w[2][6];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int2 *xr = reinterpret_cast<const int2 *>(
+        f.x + (size_t)min(r0 + grp + 32 * r, M - 1) * 192 + sub * 24);
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const int2 v = xr[q];
+      w[r][2 * q] = v.x;
+      w[r][2 * q + 1] = v.y;
+    }
+  }
+  int gw[6], bw[6];
+  {
+    const int2 *gp = reinterpret_cast<const int2 *>(ln.gamma + sub * 24);
+    const int2 *bp = reinterpret_cast<const int2 *>(ln.beta + sub * 24);
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const int2 a = gp[q], c = bp[q];
+      gw[2 * q] = a.x; gw[2 * q + 1] = a.y;
+      bw[2 * q] = c.x; bw[2 * q + 1] = c.y;
+    }
+  }
+  int sx[2], sxx[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    sx[r] = 0;
+    sxx[r] = 0;
+#pragma unroll
+    for (int q = 0; q < 6; ++q) {
+      sx[r] = __builtin_amdgcn_sdot4(w[r][q], 0x01010101, sx[r], false);
+      sxx[r] = __builtin_amdgcn_sdot4(w[r][q], w[r][q], sxx[r], false);
+    }
+  }
+#pragma unroll
+  for (int off = 1; off < 8; off <<= 1)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      sx[r] += __shfl_xor(sx[r], off);
+      sxx[r] += __shfl_xor(sxx[r], off);
+    }
+  const int mr = sub & 1;
+  const LnRow mine = ln_row_consts(mr ? sx[1] : sx[0], mr ? sxx[1] : sxx[0], ln.s, ln.t);
+  if (sub < 2 && mine.neg_var && f.lw.img_warn && r0 + grp + 32 * sub < M)
+    ln_warn_row(f.lw.offsets, f.lw.batch, f.lw.img_warn, r0 + grp + 32 * sub);
+  const int rnd = 1 << (ln.os - 1);
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    LnRow c;
+    const int src = (threadIdx.x & 63 & ~7) + r;
+    c.a0 = __shfl(mine.a0, src);
+    c.a1 = __shfl(mine.a1, src);
+    c.a2 = __shfl(mine.a2, src);
+    c.c0 = __shfl(mine.c0, src);
+    c.c1 = __shfl(mine.c1, src);
+    c.c2 = __shfl(mine.c2, src);
+    c.xt = __shfl(mine.xt, src);
+    int out[6];
+#pragma unroll
+    for (int q = 0; q < 6; ++q) out[q] = 0;
+#pragma unroll
+    for (int j = 0; j < 24; ++j) {
+      const int sh = 8 * (j & 3);
+      const int xv = __builtin_amdgcn_sbfe(w[r][j >> 2], sh, 8);
+      const int g = __builtin_amdgcn_sbfe(gw[j >> 2], sh, 8);
+      const int bb = __builtin_amdgcn_sbfe(bw[j >> 2], sh, 8) * (1 << ln.bs);
+      const int a = ln_norm(xv, c) * g + bb;
+      int o = (a + rnd + (a >> 31)) >> ln.os;
+      o = min(max(o, -128), 127);
+      out[j >> 2] |= (o & 0xFF) << sh;
+    }
+    int2 *yr = reinterpret_cast<int2 *>(dst + (grp + 32 * r) * kFfnLnRow + sub * 24);
+#pragma unroll
+    for (int q = 0; q < 3; ++q) yr[q] = int2{out[2 * q], out[2 * q + 1]};
+  }
+}
+
+template <int DIRS1, int DIRS2, bool LN>
+__global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, FfnLn fl) {
   __shared__ __attribute__((aligned(16))) int8_t hid[kFfnRows * kFfnHRow];
   // static, so its LDS address is a constant the table reads can fold
   __shared__ __attribute__((aligned(16))) unsigned lut[kGeluLutMaxWords];
@@ -804,15 +894,6 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2) {
 
   for (int rb = blockIdx.x; rb < nrb; rb += gridDim.x) {
     const int r0 = rb * kFfnRows;
-    // Phase A.  A fragments of both row tiles, all six K-steps; the weight
-    // fragments and biases of column tile ci + 1 load while tile ci runs.
-    v4i af[2][6];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      const int8_t *ap = g1.a + (size_t)min(r0 + 32 * rt + l32, M - 1) * g1.lda + 16 * h;
-#pragma unroll
-      for (int kt = 0; kt < 6; ++kt) af[rt][kt] = *reinterpret_cast<const v4i *>(ap + kt * 32);
-    }
     // Weight fragments single-buffered: the next column tile's load is
     // issued after the current tile's MFMAs and lands during its GELU
     // epilogues; the biases are double-buffered.
@@ -826,7 +907,31 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2) {
       for (int q = 0; q < 4; ++q)
         bi[q] = *reinterpret_cast<const v4i *>(g1.bias + ct * 32 + 16 * h + 4 * q);
     };
-    load_w1(0, bs[0]);
+    // Phase A.  A fragments of both row tiles, all six K-steps; the weight
+    // fragments and biases of column tile ci + 1 load while tile ci runs.
+    v4i af[2][6];
+    if constexpr (LN) {
+      // the first weight tile loads while the LayerNorm runs; its rows
+      // pass through hid (free until phase A writes it)
+      load_w1(0, bs[0]);
+      ffn_layernorm(fl, r0, M, hid);
+      __syncthreads();
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int kt = 0; kt < 6; ++kt)
+          af[rt][kt] = *reinterpret_cast<const v4i *>(&hid[(32 * rt + l32) * kFfnLnRow +
+                                                           kt * 32 + 16 * h]);
+      __syncthreads();
+    } else {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const int8_t *ap = g1.a + (size_t)min(r0 + 32 * rt + l32, M - 1) * g1.lda + 16 * h;
+#pragma unroll
+        for (int kt = 0; kt < 6; ++kt) af[rt][kt] = *reinterpret_cast<const v4i *>(ap + kt * 32);
+      }
+      load_w1(0, bs[0]);
+    }
 #pragma unroll 2
     for (int ci = 0; ci < 6; ++ci) {
       const int cur = ci & 1;
@@ -930,26 +1035,29 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2) {
   }
 }
 
-template <int DIRS1>
-static void launch_ffn_d(const GemmArgs &g1, const GemmArgs &g2, int dirs2, dim3 grid, size_t lds,
-                         hipStream_t s) {
+template <int DIRS1, bool LN>
+static void launch_ffn_d(const GemmArgs &g1, const GemmArgs &g2, const FfnLn &fl, int dirs2,
+                         dim3 grid, size_t lds, hipStream_t s) {
   switch (dirs2) {
-    case 0: hv_launch(k_ffn<DIRS1, 0>, grid, dim3(256), lds, s, g1, g2); break;
-    case 1: hv_launch(k_ffn<DIRS1, 1>, grid, dim3(256), lds, s, g1, g2); break;
-    case 2: hv_launch(k_ffn<DIRS1, 2>, grid, dim3(256), lds, s, g1, g2); break;
-    default: hv_launch(k_ffn<DIRS1, 3>, grid, dim3(256), lds, s, g1, g2); break;
+    case 0: hv_launch(k_ffn<DIRS1, 0, LN>, grid, dim3(256), lds, s, g1, g2, fl); break;
+    case 1: hv_launch(k_ffn<DIRS1, 1, LN>, grid, dim3(256), lds, s, g1, g2, fl); break;
+    case 2: hv_launch(k_ffn<DIRS1, 2, LN>, grid, dim3(256), lds, s, g1, g2, fl); break;
+    default: hv_launch(k_ffn<DIRS1, 3, LN>, grid, dim3(256), lds, s, g1, g2, fl); break;
   }
 }
 
 // Returns HV_OK when the fused kernel was launched, 1 when the shapes or
 // exponents need the two GEMM launches instead.
-int launch_ffn(const GemmArgs &g1_in, const GemmArgs &g2_in, hipStream_t s) {
+int launch_ffn(const GemmArgs &g1_in, const GemmArgs &g2_in, hipStream_t s, const FfnLn *ln) {
   GemmArgs g1 = g1_in, g2 = g2_in;
   if (g1.k != 192 || g1.n != 768 || g2.k != 768 || g2.n != 192 || g1.lda != 192 ||
       g2.ldc != 192 || g2.ldr != 192 || !g1.bias || !g2.bias || !g2.res || g1.m <= 0)
     return 1;
-  if (((uintptr_t)g1.a | (uintptr_t)g1.bias | (uintptr_t)g2.bias | (uintptr_t)g2.c |
-       (uintptr_t)g2.res | (uintptr_t)g2.aux) & 15)
+  if (((uintptr_t)(ln ? nullptr : g1.a) | (uintptr_t)g1.bias | (uintptr_t)g2.bias |
+       (uintptr_t)g2.c | (uintptr_t)g2.res | (uintptr_t)g2.aux) & 15)
+    return 1;
+  if (ln && (!ln->x || ((uintptr_t)ln->x & 7) || ((uintptr_t)ln->ln.gamma & 7) ||
+             ((uintptr_t)ln->ln.beta & 7)))
     return 1;
   if (g1.shift_b < kGeluLutSoMin || g1.shift_b > kGeluLutSoMax) return 1;
   epilogue_limits_pub(g1, EPI_GELU);
@@ -968,8 +1076,14 @@ int launch_ffn(const GemmArgs &g1_in, const GemmArgs &g2_in, hipStream_t s) {
   // grid left half the workgroups with one block more than the others).
   const dim3 grid((g1.m + kFfnRows - 1) / kFfnRows);
   const int d1 = epilogue_dirs(g1, EPI_GELU) & 1, d2 = epilogue_dirs(g2, EPI_RES);
-  if (d1) launch_ffn_d<5>(g1, g2, d2, grid, lds, s);
-  else launch_ffn_d<4>(g1, g2, d2, grid, lds, s);
+  const FfnLn fl = ln ? *ln : FfnLn{};
+  if (ln) {
+    if (d1) launch_ffn_d<5, true>(g1, g2, fl, d2, grid, lds, s);
+    else launch_ffn_d<4, true>(g1, g2, fl, d2, grid, lds, s);
+  } else {
+    if (d1) launch_ffn_d<5, false>(g1, g2, fl, d2, grid, lds, s);
+    else launch_ffn_d<4, false>(g1, g2, fl, d2, grid, lds, s);
+  }
   return check_hip(hipGetLastError(), "k_ffn launch");
 }
 

@@ -26,6 +26,15 @@ inline void hv_launch(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t
   hipExtLaunchKernelGGL(kernel, grid, block, shm, s, a, b, 0, args...);
 }
 
+// Per-image warning sink of the LayerNorm kernels: a row with a negative
+// variance ORs HV_WARN_LN_NEGATIVE_VARIANCE into img_warn[b] of the image b
+// whose rows offsets[b] .. offsets[b+1] hold it.  img_warn NULL: off.
+struct LnWarn {
+  const int32_t *offsets;
+  int batch;
+  int32_t *img_warn;
+};
+
 // A-operand sources of the GEMM.
 // A_UNSIGNED is a flag bit of the A mode (A_ROWS only).
 enum { A_ROWS = HV_A_ROWS, A_GATHER = HV_A_GATHER, A_PATCH = 2, A_UNSIGNED = HV_A_UNSIGNED };
@@ -64,7 +73,16 @@ int launch_gemm(const GemmArgs &g, int a_mode, int epilogue, hipStream_t s);
 // for the GELU GEMM (c unused), g2 as for the residual GEMM (a unused).
 // Returns HV_OK when launched, 1 when the shapes or exponents need the two
 // GEMM launches (no GELU step table, wide shifts, unaligned pointers).
-int launch_ffn(const GemmArgs &g1, const GemmArgs &g2, hipStream_t s);
+// ln (optional): the LayerNorm in front of FFN1 runs in the same kernel
+// over the rows of ln->x (row stride 192, 8-byte aligned; int32 form of
+// ln32_setup, whose output pointer is unused), g1.a unused; negative
+// variances reach ln->lw.
+struct FfnLn {
+  const int8_t *x;
+  Ln32 ln;
+  LnWarn lw;
+};
+int launch_ffn(const GemmArgs &g1, const GemmArgs &g2, hipStream_t s, const FfnLn *ln = nullptr);
 // Fills acc_lim / narrow_ok / da / db / os of the int32 epilogue paths.
 void epilogue_limits_pub(GemmArgs &g, int epilogue);
 
@@ -90,14 +108,18 @@ int launch_image_front(const float *chw, int batch, int input_exp, int8_t *out, 
 bool ln32_setup(const int8_t *g, const int8_t *b, int8_t *y, int x_exp, int g_exp, int b_exp,
                 int out_exp, Ln32 *ln);
 
-// Per-image warning sink of the LayerNorm kernels: a row with a negative
-// variance ORs HV_WARN_LN_NEGATIVE_VARIANCE into img_warn[b] of the image b
-// whose rows offsets[b] .. offsets[b+1] hold it.  img_warn NULL: off.
-struct LnWarn {
-  const int32_t *offsets;
-  int batch;
-  int32_t *img_warn;
-};
+// Image of `row` (the last b with offsets[b] <= row, in [0, batch)) gets
+// the negative-variance warning bit.  Rare: only rows that clamp reach it.
+static __device__ __noinline__ void ln_warn_row(const int32_t *offsets, int batch,
+                                                int32_t *img_warn, int row) {
+  int lo = 0, hi = batch - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (offsets[mid] <= row) lo = mid;
+    else hi = mid - 1;
+  }
+  atomicOr(img_warn + lo, HV_WARN_LN_NEGATIVE_VARIANCE);
+}
 
 int launch_layernorm(const int8_t *x, const int8_t *g, const int8_t *b, int8_t *y, int rows,
                      const int32_t *rows_dev, int x_exp, int g_exp, int b_exp, int out_exp,

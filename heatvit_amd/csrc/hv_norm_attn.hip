@@ -16,19 +16,6 @@ namespace hv {
 //  * gamma/beta alignment (shifts gs <= 30, bs <= 54): |aligned| < 2^62.
 // Other exponents take the 128-bit route (mean^2 < 2^78 always does).
 // ---------------------------------------------------------------------------
-// Image of `row` (the last b with offsets[b] <= row, in [0, batch)) gets
-// the negative-variance warning bit.  Rare: only rows that clamp reach it.
-__device__ __noinline__ void ln_warn_row(const int32_t *offsets, int batch, int32_t *img_warn,
-                                         int row) {
-  int lo = 0, hi = batch - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (offsets[mid] <= row) lo = mid;
-    else hi = mid - 1;
-  }
-  atomicOr(img_warn + lo, HV_WARN_LN_NEGATIVE_VARIANCE);
-}
-
 template <bool FAST_NORM, bool FAST_ALIGN>
 __global__ __launch_bounds__(256) void k_layernorm(const int8_t *__restrict__ x,
                                                    const int8_t *__restrict__ gamma,

@@ -96,6 +96,42 @@ def test_block_every_model_block_ragged_vs_oracle(oracle, blk):
         assert np.array_equal(zs[i], z), (blk, i, len(x))
 
 
+def _block_launches(xs, bp, checkpoints):
+    """Block forward with kernel-class profiling: outputs and launches per class."""
+    from heatvit_amd import _lib
+    from heatvit_amd.transformer import transformer_block_batch
+    L = _lib.lib()
+    L.hv_profile_enable(1)
+    try:
+        out = transformer_block_batch(xs, bp, checkpoints=checkpoints)
+        ms = np.zeros(len(_lib.PROF_CLASSES), np.float32)
+        n = np.zeros(len(_lib.PROF_CLASSES), np.int32)
+        _lib.check(L.hv_profile_read(ms.ctypes.data, n.ctypes.data, len(ms)), "profile")
+    finally:
+        L.hv_profile_enable(0)
+    return out, dict(zip(_lib.PROF_CLASSES, n.tolist()))
+
+
+def test_block_ln2_inside_fused_ffn_vs_oracle(oracle):
+    """Without checkpoints LayerNorm 2 runs inside the fused FFN kernel (its
+    rows pass through LDS): one LayerNorm launch per block (LN1) and one FFN
+    launch.  With checkpoints LN2 has its own launch, which writes the ln2
+    checkpoint, and FFN1 / FFN2 run as two GEMMs (the hidden checkpoint).
+    Both match the oracle over ragged images (partial 64-row blocks)."""
+    _, bp = synth.block_workload()
+    xs = _ragged_batch(np.random.default_rng(21))
+    zs, n = _block_launches(xs, bp, False)
+    assert n["layernorm"] == 1 and n["ffn"] == 1, n
+    assert n["gemm_ffn1"] == 0 and n["gemm_ffn2"] == 0, n
+    (zs_ck, cks), n_ck = _block_launches(xs, bp, True)
+    assert n_ck["layernorm"] == 2 and n_ck["ffn"] == 0, n_ck
+    for i, x in enumerate(xs):
+        z, ck = oracle.transformer_block(x, bp, checkpoints=True)
+        assert np.array_equal(zs[i], z), (i, len(x))
+        assert np.array_equal(zs_ck[i], z), (i, len(x))
+        assert np.array_equal(cks[i]["ln2"], ck["ln2"]), (i, len(x))
+
+
 def test_block_wide_biases_all_gemms_vs_oracle(oracle):
     """Biases beyond the int32 epilogue bounds in all four GEMMs send their
     tiles to the exact 64-bit forms."""
