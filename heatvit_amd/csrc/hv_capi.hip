@@ -164,12 +164,25 @@ static BlockWs carve_block(Carve &cv, size_t rows) {
   return w;
 }
 
+// Chaining of LayerNorm 1 between consecutive blocks of the model: ln1_in
+// (optional) holds this block's LayerNorm 1 of x, written by the previous
+// block's FFN kernel; next (optional) is the following block, whose
+// LayerNorm 1 of z this block's FFN kernel then writes to next_ln1 when it
+// can (*next_done tells).
+struct LnChain {
+  const int8_t *ln1_in;
+  const hv_block_dev *next;
+  int8_t *next_ln1;
+  bool *next_done;
+};
+
 // transformer_block (transformer.py:401-431) on rows [0, offsets[batch]):
 // LN1, QKV, attention, proj + residual, LN2, FFN1 + GELU, FFN2 + residual.
 // warnings (optional, [B]) receive the LayerNorms' negative-variance bit.
 static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *offsets,
                          int batch, int max_rows, int8_t *z, const hv_block_ckpt *ck,
-                         int32_t *warnings, const BlockWs &w, hipStream_t s) {
+                         int32_t *warnings, const BlockWs &w, hipStream_t s,
+                         const LnChain &chain = LnChain{}) {
   const int32_t *rows_dev = offsets + batch;
   const LnWarn lw{offsets, batch, warnings};
   int8_t *qkv = ck && ck->fused_qkv ? ck->fused_qkv : w.qkv;
@@ -178,14 +191,18 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   int8_t *hidden = ck && ck->hidden ? ck->hidden : w.hidden;
   int rc;
 
-  int8_t *ln1 = ck && ck->ln1 ? ck->ln1 : w.ln;
+  const int8_t *ln1 = ck && ck->ln1 ? ck->ln1 : w.ln;
   int8_t *ln2 = ck && ck->ln2 ? ck->ln2 : w.ln;
-  {
+  if (chain.next_done) *chain.next_done = false;
+  if (chain.ln1_in && !ck) {
+    ln1 = chain.ln1_in;
+  } else {
     ProfScope ps(HV_PROF_LAYERNORM, s);
-    rc = launch_layernorm(x, p.ln1_gamma, p.ln1_beta, ln1, max_rows, rows_dev, p.x_exp,
-                          p.gamma1_exp, p.beta1_exp, p.ln1_out_exp, nullptr, lw, s);
+    rc = launch_layernorm(x, p.ln1_gamma, p.ln1_beta, const_cast<int8_t *>(ln1), max_rows,
+                          rows_dev, p.x_exp, p.gamma1_exp, p.beta1_exp, p.ln1_out_exp, nullptr,
+                          lw, s);
+    if (rc) return rc;
   }
-  if (rc) return rc;
   GemmArgs g{};
   g.a = ln1; g.b = p.wqkv_p; g.bias = p.bqkv; g.c = qkv; g.m_dev = rows_dev;
   g.m = max_rows; g.n = 576; g.k = 192; g.lda = 192; g.ldc = 576;
@@ -239,10 +256,21 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   if (!(ck && (ck->hidden || ck->ln2)) &&
       ln32_setup(p.ln2_gamma, p.ln2_beta, ln2, p.ffn_x_exp, p.gamma2_exp, p.beta2_exp,
                  p.ln2_out_exp, &ln)) {
-    const FfnLn fl{y, ln, lw};
+    const LnPrologue fl{y, ln, lw};
+    // The next block's LayerNorm 1 of z at the kernel's end, when its
+    // exponents take the int32 form.
+    const hv_block_dev *nx = ck ? nullptr : chain.next;
+    Ln32 ln_n;
+    const bool chained = nx && chain.next_ln1 &&
+                         ln32_setup(nx->ln1_gamma, nx->ln1_beta, chain.next_ln1, nx->x_exp,
+                                    nx->gamma1_exp, nx->beta1_exp, nx->ln1_out_exp, &ln_n);
+    const LnPrologue fe{nullptr, ln_n, lw};
     ProfScope ps(HV_PROF_FFN, s);
-    rc = launch_ffn(g1, g2, s, &fl);
-    if (rc != 1) return rc;
+    rc = launch_ffn(g1, g2, s, &fl, chained ? &fe : nullptr);
+    if (rc != 1) {
+      if (rc == HV_OK && chained && chain.next_done) *chain.next_done = true;
+      return rc;
+    }
   }
   {
     ProfScope ps(HV_PROF_LAYERNORM, s);
@@ -597,6 +625,7 @@ static int model_forward(const hv_model_dev *p, const void *images, bool float_i
   if (ckpt && (rc = launch_copy_ckpt(w.xa, w.off_a, batch, ckpt, ckpt_rows, 0, s))) return rc;
 
   int sel = 0;
+  const int8_t *ln1_ready = nullptr;  // this block's LayerNorm 1, from the previous FFN
   for (int blk = 1; blk <= 12; ++blk) {
     if (sel < p->n_selectors && p->selector_blocks[sel] == blk) {
       SelectorArgs a{};
@@ -617,9 +646,16 @@ static int model_forward(const hv_model_dev *p, const void *images, bool float_i
       ++sel;
       if (ckpt && (rc = launch_copy_ckpt(w.xa, w.off_a, batch, ckpt, ckpt_rows, sel, s))) return rc;
     }
+    // The next block's LayerNorm 1 inside this block's FFN kernel, unless a
+    // selector changes the rows in between.
+    const bool chain_next =
+        blk < 12 && !(sel < p->n_selectors && p->selector_blocks[sel] == blk + 1);
+    bool next_done = false;
+    const LnChain chain{ln1_ready, chain_next ? &p->blocks[blk] : nullptr, w.blk.ln, &next_done};
     if ((rc = block_forward(p->blocks[blk - 1], w.xa, w.off_a, batch, max_rows, w.xb, nullptr,
-                            warnings, w.blk, s)))
+                            warnings, w.blk, s, chain)))
       return rc;
+    ln1_ready = next_done ? w.blk.ln : nullptr;
     std::swap(w.xa, w.xb);
     if (ckpt && (rc = launch_copy_ckpt(w.xa, w.off_a, batch, ckpt, ckpt_rows, 3 + blk, s))) return rc;
   }

@@ -176,11 +176,14 @@ __device__ __forceinline__ void epi_operands(const GemmArgs &g, const int (&arow
 
 // Epilogue of one wavefront tile: lane l finishes row r0 + 32*mt + l%32,
 // channels c0 .. c0+15 of each column tile.
+// lds_out (optional, EPI_RES with 16-byte stores): the output bytes also go
+// to lds_out + (32 * mt + l32) * lds_stride + c0.
 template <int MT, int NT, int EPI, bool FAST, int DIRS>
 __device__ __forceinline__ void epi_tile(const GemmArgs &g, const v16i (&acc)[MT][NT],
                                          const v4i (&bias4)[NT][4], const v4i (&res4)[MT][NT],
                                          int r0, int ct0, int M, int h, int l32, const Rq &rq_a,
-                                         const Rq &rq_b, const unsigned *lut) {
+                                         const Rq &rq_b, const unsigned *lut,
+                                         int8_t *lds_out = nullptr, int lds_stride = 0) {
   constexpr bool RESLIKE = EPI == EPI_RES || EPI == EPI_PATCH;
   // the table's upper clamp in a vector register: with both bounds in
   // scalar registers the clamp cannot be a single med3
@@ -258,9 +261,11 @@ __device__ __forceinline__ void epi_tile(const GemmArgs &g, const v16i (&acc)[MT
       } else {
         int8_t *cp = reinterpret_cast<int8_t *>(g.c) + orow * g.ldc + c0;
         if (full) {
-          *reinterpret_cast<v4i *>(cp) = v4i{pack4(o[0], o[1], o[2], o[3]), pack4(o[4], o[5], o[6], o[7]),
-                                             pack4(o[8], o[9], o[10], o[11]),
-                                             pack4(o[12], o[13], o[14], o[15])};
+          const v4i ov = v4i{pack4(o[0], o[1], o[2], o[3]), pack4(o[4], o[5], o[6], o[7]),
+                             pack4(o[8], o[9], o[10], o[11]), pack4(o[12], o[13], o[14], o[15])};
+          *reinterpret_cast<v4i *>(cp) = ov;
+          if (EPI == EPI_RES && lds_out)
+            *reinterpret_cast<v4i *>(lds_out + (32 * mt + l32) * lds_stride + c0) = ov;
         } else {
 #pragma unroll
           for (int j = 0; j < 16; ++j)
@@ -781,28 +786,32 @@ int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
 // The hidden activations never leave the CU.  Each workgroup stages the
 // GELU table and handles one row block.
 // ---------------------------------------------------------------------------
-static constexpr int kFfnRows = 64, kFfnHRow = 784, kFfnLnRow = 208;
+static constexpr int kFfnRows = 64, kFfnHRow = 784, kLnPrologueRow = 208;
 static_assert(kFfnRows * kFfnHRow + 4 * kGeluLutMaxWords <= 160 * 1024 / 2,
               "the fused FFN's LDS must allow two workgroups per CU");
-static_assert(kFfnRows * kFfnLnRow <= kFfnRows * kFfnHRow, "LayerNorm rows fit the hidden block");
+static_assert(kLnPrologueRow <= kFfnHRow, "LayerNorm rows fit the hidden block");
+static_assert(kFfnRows * kLnPrologueRow <= 4 * kGeluLutMaxWords, "output rows fit the table");
 
-// The LayerNorm in front of FFN1 (transformer.py:349-352; nonlinear.py:
-// 136-186, the int32 form of k_layernorm32): rows r0 .. r0 + 63 of x by the
-// workgroup's 32 eight-lane groups, group j taking rows j and j + 32 (rows
-// past M repeat row M - 1 and are not reported), each lane 24 channels.
-// Lane sub works out the constants of row sub % 2 and the group reads them
-// from lanes 0 and 1, so the 64/128-bit set-up runs four times per row
-// instead of eight.  The int8 rows go to dst at a 208-byte stride, which
-// the A-fragment reads (16 bytes at row l, offset 32k + 16h) take without
-// bank conflicts.
-__device__ __forceinline__ void ffn_layernorm(const FfnLn &f, int r0, int M, int8_t *dst) {
+// LayerNorm (nonlinear.py:136-186, the int32 form of k_layernorm32) of a
+// block of 64 rows by 256 threads: 32 eight-lane groups, group j taking rows
+// j and j + 32, each lane 24 channels.  Lane sub works out the constants of
+// row sub % 2 and the group reads them from lanes 0 and 1, so the
+// 64/128-bit set-up runs four times per row instead of eight.  Row i is
+// read from src + min(i, clamp) * SS and written to dst + i * DS when
+// i < store_rows; rows with i < report_rows (row r0 + i of the batch)
+// report a negative variance to lw (the int32 form cannot produce one:
+// with x_scale >= -16 the sum of squares is exact and the rounding of the
+// mean moves mean^2 by less than the smallest nonzero variance).
+template <int SS, int DS>
+__device__ __forceinline__ void ln_rows(const int8_t *src, int clamp, int8_t *dst, int store_rows,
+                                        const Ln32 &ln, const LnWarn &lw, int r0,
+                                        int report_rows) {
   const int tid = threadIdx.x, sub = tid & 7, grp = tid >> 3;
-  const Ln32 &ln = f.ln;
   int w[2][6];
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
-    const int2 *xr = reinterpret_cast<const int2 *>(
-        f.x + (size_t)min(r0 + grp + 32 * r, M - 1) * 192 + sub * 24);
+    const int2 *xr =
+        reinterpret_cast<const int2 *>(src + min(grp + 32 * r, clamp) * SS + sub * 24);
 #pragma unroll
     for (int q = 0; q < 3; ++q) {
       const int2 v = xr[q];
@@ -841,20 +850,20 @@ __device__ __forceinline__ void ffn_layernorm(const FfnLn &f, int r0, int M, int
     }
   const int mr = sub & 1;
   const LnRow mine = ln_row_consts(mr ? sx[1] : sx[0], mr ? sxx[1] : sxx[0], ln.s, ln.t);
-  if (sub < 2 && mine.neg_var && f.lw.img_warn && r0 + grp + 32 * sub < M)
-    ln_warn_row(f.lw.offsets, f.lw.batch, f.lw.img_warn, r0 + grp + 32 * sub);
+  if (sub < 2 && mine.neg_var && lw.img_warn && grp + 32 * sub < report_rows)
+    ln_warn_row(lw.offsets, lw.batch, lw.img_warn, r0 + grp + 32 * sub);
   const int rnd = 1 << (ln.os - 1);
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     LnRow c;
-    const int src = (threadIdx.x & 63 & ~7) + r;
-    c.a0 = __shfl(mine.a0, src);
-    c.a1 = __shfl(mine.a1, src);
-    c.a2 = __shfl(mine.a2, src);
-    c.c0 = __shfl(mine.c0, src);
-    c.c1 = __shfl(mine.c1, src);
-    c.c2 = __shfl(mine.c2, src);
-    c.xt = __shfl(mine.xt, src);
+    const int src_lane = (threadIdx.x & 63 & ~7) + r;
+    c.a0 = __shfl(mine.a0, src_lane);
+    c.a1 = __shfl(mine.a1, src_lane);
+    c.a2 = __shfl(mine.a2, src_lane);
+    c.c0 = __shfl(mine.c0, src_lane);
+    c.c1 = __shfl(mine.c1, src_lane);
+    c.c2 = __shfl(mine.c2, src_lane);
+    c.xt = __shfl(mine.xt, src_lane);
     int out[6];
 #pragma unroll
     for (int q = 0; q < 6; ++q) out[q] = 0;
@@ -869,14 +878,21 @@ __device__ __forceinline__ void ffn_layernorm(const FfnLn &f, int r0, int M, int
       o = min(max(o, -128), 127);
       out[j >> 2] |= (o & 0xFF) << sh;
     }
-    int2 *yr = reinterpret_cast<int2 *>(dst + (grp + 32 * r) * kFfnLnRow + sub * 24);
+    if (grp + 32 * r < store_rows) {
+      int2 *yr = reinterpret_cast<int2 *>(dst + (grp + 32 * r) * DS + sub * 24);
 #pragma unroll
-    for (int q = 0; q < 3; ++q) yr[q] = int2{out[2 * q], out[2 * q + 1]};
+      for (int q = 0; q < 3; ++q) yr[q] = int2{out[2 * q], out[2 * q + 1]};
+    }
   }
 }
 
-template <int DIRS1, int DIRS2, bool LN>
-__global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, FfnLn fl) {
+// LN: LayerNorm 2 in front (fl); LNE: the next block's LayerNorm 1 of the
+// output rows behind (fe, output fe.ln.out): phase B also writes its rows to
+// LDS where the GELU table was (phase A is done with it), and the rows are
+// normalised once they are complete.
+template <int DIRS1, int DIRS2, bool LN, bool LNE>
+__global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologue fl,
+                                             LnPrologue fe) {
   __shared__ __attribute__((aligned(16))) int8_t hid[kFfnRows * kFfnHRow];
   // static, so its LDS address is a constant the table reads can fold
   __shared__ __attribute__((aligned(16))) unsigned lut[kGeluLutMaxWords];
@@ -914,13 +930,14 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, FfnLn fl)
       // the first weight tile loads while the LayerNorm runs; its rows
       // pass through hid (free until phase A writes it)
       load_w1(0, bs[0]);
-      ffn_layernorm(fl, r0, M, hid);
+      ln_rows<192, kLnPrologueRow>(fl.x + (size_t)r0 * 192, M - 1 - r0, hid, kFfnRows, fl.ln,
+                                   fl.lw, r0, M - r0);
       __syncthreads();
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
         for (int kt = 0; kt < 6; ++kt)
-          af[rt][kt] = *reinterpret_cast<const v4i *>(&hid[(32 * rt + l32) * kFfnLnRow +
+          af[rt][kt] = *reinterpret_cast<const v4i *>(&hid[(32 * rt + l32) * kLnPrologueRow +
                                                            kt * 32 + 16 * h]);
       __syncthreads();
     } else {
@@ -1022,8 +1039,10 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, FfnLn fl)
               0);
         __builtin_amdgcn_sched_barrier(0);  // one chunk of LDS reads in flight at a time
       }
-      epi_tile<1, 1, EPI_RES, true, DIRS2>(g2, acc, bias4, res4, r0 + 32 * rt, ct, M, h, l32,
-                                           r2a, r2b, nullptr);
+      epi_tile<1, 1, EPI_RES, true, DIRS2>(
+          g2, acc, bias4, res4, r0 + 32 * rt, ct, M, h, l32, r2a, r2b, nullptr,
+          LNE ? reinterpret_cast<int8_t *>(lut) + 32 * rt * kLnPrologueRow : nullptr,
+          kLnPrologueRow);
       if (ti + 1 < 3) {
         rt = nrt;
         ct = nct;
@@ -1032,23 +1051,33 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, FfnLn fl)
       }
     }
     __syncthreads();  // the next row block rewrites hid
+    if constexpr (LNE) {
+      const int8_t *zs = reinterpret_cast<const int8_t *>(lut);
+      ln_rows<kLnPrologueRow, 192>(zs, kFfnRows - 1, fe.ln.out + (size_t)r0 * 192, M - r0, fe.ln,
+                                   fe.lw, r0, M - r0);
+      if (rb + (int)gridDim.x < nrb) {
+        __syncthreads();  // the rows are read; the table comes back
+        stage_lut(g1, lut);
+      }
+    }
   }
 }
 
-template <int DIRS1, bool LN>
-static void launch_ffn_d(const GemmArgs &g1, const GemmArgs &g2, const FfnLn &fl, int dirs2,
-                         dim3 grid, size_t lds, hipStream_t s) {
+template <int DIRS1, bool LN, bool LNE>
+static void launch_ffn_d(const GemmArgs &g1, const GemmArgs &g2, const LnPrologue &fl,
+                         const LnPrologue &fe, int dirs2, dim3 grid, size_t lds, hipStream_t s) {
   switch (dirs2) {
-    case 0: hv_launch(k_ffn<DIRS1, 0, LN>, grid, dim3(256), lds, s, g1, g2, fl); break;
-    case 1: hv_launch(k_ffn<DIRS1, 1, LN>, grid, dim3(256), lds, s, g1, g2, fl); break;
-    case 2: hv_launch(k_ffn<DIRS1, 2, LN>, grid, dim3(256), lds, s, g1, g2, fl); break;
-    default: hv_launch(k_ffn<DIRS1, 3, LN>, grid, dim3(256), lds, s, g1, g2, fl); break;
+    case 0: hv_launch(k_ffn<DIRS1, 0, LN, LNE>, grid, dim3(256), lds, s, g1, g2, fl, fe); break;
+    case 1: hv_launch(k_ffn<DIRS1, 1, LN, LNE>, grid, dim3(256), lds, s, g1, g2, fl, fe); break;
+    case 2: hv_launch(k_ffn<DIRS1, 2, LN, LNE>, grid, dim3(256), lds, s, g1, g2, fl, fe); break;
+    default: hv_launch(k_ffn<DIRS1, 3, LN, LNE>, grid, dim3(256), lds, s, g1, g2, fl, fe); break;
   }
 }
 
 // Returns HV_OK when the fused kernel was launched, 1 when the shapes or
 // exponents need the two GEMM launches instead.
-int launch_ffn(const GemmArgs &g1_in, const GemmArgs &g2_in, hipStream_t s, const FfnLn *ln) {
+int launch_ffn(const GemmArgs &g1_in, const GemmArgs &g2_in, hipStream_t s,
+               const LnPrologue *ln, const LnPrologue *ln_next) {
   GemmArgs g1 = g1_in, g2 = g2_in;
   if (g1.k != 192 || g1.n != 768 || g2.k != 768 || g2.n != 192 || g1.lda != 192 ||
       g2.ldc != 192 || g2.ldr != 192 || !g1.bias || !g2.bias || !g2.res || g1.m <= 0)
@@ -1058,6 +1087,9 @@ int launch_ffn(const GemmArgs &g1_in, const GemmArgs &g2_in, hipStream_t s, cons
     return 1;
   if (ln && (!ln->x || ((uintptr_t)ln->x & 7) || ((uintptr_t)ln->ln.gamma & 7) ||
              ((uintptr_t)ln->ln.beta & 7)))
+    return 1;
+  if (ln_next && (!ln_next->ln.out || ((uintptr_t)ln_next->ln.out & 7) ||
+                  ((uintptr_t)ln_next->ln.gamma & 7) || ((uintptr_t)ln_next->ln.beta & 7)))
     return 1;
   if (g1.shift_b < kGeluLutSoMin || g1.shift_b > kGeluLutSoMax) return 1;
   epilogue_limits_pub(g1, EPI_GELU);
@@ -1076,13 +1108,17 @@ int launch_ffn(const GemmArgs &g1_in, const GemmArgs &g2_in, hipStream_t s, cons
   // grid left half the workgroups with one block more than the others).
   const dim3 grid((g1.m + kFfnRows - 1) / kFfnRows);
   const int d1 = epilogue_dirs(g1, EPI_GELU) & 1, d2 = epilogue_dirs(g2, EPI_RES);
-  const FfnLn fl = ln ? *ln : FfnLn{};
-  if (ln) {
-    if (d1) launch_ffn_d<5, true>(g1, g2, fl, d2, grid, lds, s);
-    else launch_ffn_d<4, true>(g1, g2, fl, d2, grid, lds, s);
-  } else {
-    if (d1) launch_ffn_d<5, false>(g1, g2, fl, d2, grid, lds, s);
-    else launch_ffn_d<4, false>(g1, g2, fl, d2, grid, lds, s);
+  const LnPrologue fl = ln ? *ln : LnPrologue{}, fe = ln_next ? *ln_next : LnPrologue{};
+  const int mode = (ln ? 1 : 0) | (ln_next ? 2 : 0);
+  switch (mode | (d1 ? 4 : 0)) {
+    case 0: launch_ffn_d<4, false, false>(g1, g2, fl, fe, d2, grid, lds, s); break;
+    case 1: launch_ffn_d<4, true, false>(g1, g2, fl, fe, d2, grid, lds, s); break;
+    case 2: launch_ffn_d<4, false, true>(g1, g2, fl, fe, d2, grid, lds, s); break;
+    case 3: launch_ffn_d<4, true, true>(g1, g2, fl, fe, d2, grid, lds, s); break;
+    case 4: launch_ffn_d<5, false, false>(g1, g2, fl, fe, d2, grid, lds, s); break;
+    case 5: launch_ffn_d<5, true, false>(g1, g2, fl, fe, d2, grid, lds, s); break;
+    case 6: launch_ffn_d<5, false, true>(g1, g2, fl, fe, d2, grid, lds, s); break;
+    default: launch_ffn_d<5, true, true>(g1, g2, fl, fe, d2, grid, lds, s); break;
   }
   return check_hip(hipGetLastError(), "k_ffn launch");
 }

@@ -75,14 +75,17 @@ int launch_gemm(const GemmArgs &g, int a_mode, int epilogue, hipStream_t s);
 // GEMM launches (no GELU step table, wide shifts, unaligned pointers).
 // ln (optional): the LayerNorm in front of FFN1 runs in the same kernel
 // over the rows of ln->x (row stride 192, 8-byte aligned; int32 form of
-// ln32_setup, whose output pointer is unused), g1.a unused; negative
-// variances reach ln->lw.
-struct FfnLn {
+// ln32_setup, whose output pointer is unused), g1.a unused.  ln_next
+// (optional): a LayerNorm of the output rows (the next block's LayerNorm 1)
+// runs at the kernel's end and writes ln_next->ln.out (row stride 192;
+// ln_next->x unused).  Negative variances reach the lw of each.
+struct LnPrologue {
   const int8_t *x;
   Ln32 ln;
   LnWarn lw;
 };
-int launch_ffn(const GemmArgs &g1, const GemmArgs &g2, hipStream_t s, const FfnLn *ln = nullptr);
+int launch_ffn(const GemmArgs &g1, const GemmArgs &g2, hipStream_t s,
+               const LnPrologue *ln = nullptr, const LnPrologue *ln_next = nullptr);
 // Fills acc_lim / narrow_ok / da / db / os of the int32 epilogue paths.
 void epilogue_limits_pub(GemmArgs &g, int epilogue);
 

@@ -298,3 +298,34 @@ def test_pipeline_slots_match_engine():
             for g, w in zip(got, want[start + k]):
                 assert np.array_equal(g, w)
     pipe.synchronize()
+
+
+@pytest.mark.parametrize("pruned", [True, False])
+def test_model_chains_layernorm1_through_ffn_kernels(oracle, pruned):
+    """Each block's FFN kernel also writes the next block's LayerNorm 1 unless
+    a selector changes the rows in between, so the LayerNorm launches are
+    block 1's, one after each selector and the final one; logits, token
+    counts and warnings match the oracle."""
+    from heatvit_amd import _lib
+    from heatvit_amd.model import HeatViTModel
+    imgs, params = synth.pruned_workload(6)
+    if not pruned:
+        params = synth.unpruned_control(params)
+    L = _lib.lib()
+    m = HeatViTModel()
+    L.hv_profile_enable(1)
+    try:
+        r = m.infer_batch(imgs, params)
+        ms = np.zeros(len(_lib.PROF_CLASSES), np.float32)
+        n = np.zeros(len(_lib.PROF_CLASSES), np.int32)
+        _lib.check(L.hv_profile_read(ms.ctypes.data, n.ctypes.data, len(ms)), "profile")
+    finally:
+        L.hv_profile_enable(0)
+    n = dict(zip(_lib.PROF_CLASSES, n.tolist()))
+    assert n["layernorm"] == 2 + len(params.selectors) and n["ffn"] == 12, n
+    logits, counts, status, warnings = oracle.model_infer_batch(imgs, params)
+    assert not status.any()
+    assert np.array_equal(r.logits, logits)
+    assert np.array_equal(r.warnings, warnings)
+    if pruned:
+        assert np.array_equal(r.token_counts, counts)
