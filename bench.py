@@ -54,10 +54,14 @@ def class_work(counts, params, batch):
     """Algorithmic int8 ops (2 x MACs) and minimal HBM bytes per kernel class
     for one forward, from the per-image token counts [B][4].  Per-unit
     figures: QKV 2*192*576, proj 2*192*192, FFN1 2*192*768, FFN2 2*768*192
-    ops per token (the fused FFN kernel: both, 576 B per token in and out);
-    attention 2*384*N^2 per image; patch 2*768*192 per patch; head
-    2*192*1000 per image; selector 2*13938 per candidate.  Only the classes
-    a run launches are reported."""
+    ops per token; attention 2*384*N^2 per image; patch 2*768*192 per
+    patch; head 2*192*1000 per image; selector 2*13938 per candidate.  The
+    fused FFN kernel runs LayerNorm 2 on its input rows (y in once, it is
+    also the residual) and writes the block output and, when the next block
+    follows without a selector in between, that block's LayerNorm 1: 384 B
+    per token plus 192 B for those blocks; the LayerNorm class is then each
+    stage's first LayerNorm 1 and the final one.  Only the classes a run
+    launches are reported."""
     counts = np.asarray(counts, np.int64)
     stage_of_block = []
     s = 0
@@ -68,9 +72,11 @@ def class_work(counts, params, batch):
     ops = dict.fromkeys(("patch", "layernorm", "gemm_qkv", "attention", "gemm_proj",
                          "gemm_ffn1", "gemm_ffn2", "ffn", "selector", "head"), 0)
     hbm = dict(ops)
-    for st in stage_of_block:
+    for b, st in enumerate(stage_of_block, start=1):
         n = counts[:, st]
         t = int(n.sum())
+        chained = b < 12 and (b + 1) not in params.selector_blocks
+        stage_first = b == 1 or b in params.selector_blocks
         ops["gemm_qkv"] += 2 * 192 * 576 * t
         ops["gemm_proj"] += 2 * 192 * 192 * t
         ops["gemm_ffn1"] += 2 * 192 * 768 * t
@@ -80,11 +86,12 @@ def class_work(counts, params, batch):
         hbm["gemm_proj"] += (192 + 192 + 192) * t
         hbm["gemm_ffn1"] += (192 + 768) * t
         hbm["gemm_ffn2"] += (768 + 192 + 192) * t
-        # fused FFN: LN2 rows and the residual in, block output out
+        # fused FFN: y in, block output (and the next LayerNorm 1) out
         ops["ffn"] += 2 * 2 * 192 * 768 * t
-        hbm["ffn"] += (192 + 192 + 192) * t
+        hbm["ffn"] += (192 + 192 + (192 if chained else 0)) * t
         hbm["attention"] += (576 + 192) * t
-        hbm["layernorm"] += 2 * 2 * 192 * t
+        if stage_first:
+            hbm["layernorm"] += 2 * 192 * t
     for s in range(len(params.selectors)):
         c = counts[:, s] - 1
         ops["selector"] += int(2 * 13938 * c.sum())
