@@ -4,6 +4,9 @@ CPU oracle, bit-exact:
 * every selector bias tensor at the int32 limits (selector.py:370-389 adds
   biases in int64, gemm.py:118-119), so the int32 fast paths must hand over
   to the exact forms;
+* the three GELU layers' output exponents over a range of post-op shifts
+  (so = exponent + 16: 3, 12, 13, 14 and the left shift -4), each layer
+  on its own;
 * hv_selector_finalize given Q0.16 scores outside [0, 65536]: the golden
   finalize raises ValueError (selector._q016), the device path rejects that
   image (state token count -1) and leaves the others untouched.
@@ -58,6 +61,26 @@ def test_selector_extreme_biases_vs_oracle(oracle, part, name):
             assert np.array_equal(r.kept_index, want["kept_index"]), (tag, i)
             assert (r.token_count, r.warnings, r.pruned_normal_count) == \
                 (want["token_count"], want["warnings"], want["pruned_normal_count"]), (tag, i)
+
+
+@pytest.mark.parametrize("field", ["local_out_scale_exp", "h1_out_scale_exp",
+                                   "h2_out_scale_exp"])
+def test_selector_gelu_table_range_vs_oracle(oracle, field):
+    from heatvit_amd.selector import token_selector_batch
+    tokens, sp = synth.selector_workload()
+    sets = [tokens[0], tokens[1][:40], tokens[2][:3]]
+    flags = [False, True, False]
+    for e in (-13, -4, -3, -2, -20):
+        p = dataclasses.replace(sp, **{field: e})
+        print(f"selector {field} = {e}", flush=True)
+        res = token_selector_batch(sets, flags, p)
+        for i, (t, f) in enumerate(zip(sets, flags)):
+            want = oracle.token_selector(t, f, p)
+            r = res[i]
+            for k in ("local", "h2", "head_scores", "fused_scores"):
+                assert np.array_equal(getattr(r, k), want[k]), (e, i, k)
+            assert np.array_equal(r.tokens, want["tokens"]), (e, i)
+            assert r.token_count == want["token_count"], (e, i)
 
 
 @pytest.mark.parametrize("bad", [65537, -1, I32_MAX, I32_MIN])
