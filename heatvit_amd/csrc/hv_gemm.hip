@@ -776,7 +776,8 @@ int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
 // ---------------------------------------------------------------------------
 // Fused FFN (transformer.ffn, transformer.py:328-384) for the int32
 // epilogues with a GELU step table: z = align_add(y, requant(GELU(ln2 W1 +
-// b1) W2 + b2)).  A persistent workgroup owns 64 rows at a time:
+// b1) W2 + b2)).  A workgroup owns one block of 64 rows (the grid has one
+// per row block):
 //   phase A  the FFN1 tiles (2 row x 24 column tiles of 32; wavefront w
 //            takes columns w, w+4, ...), the GELU post-op from the step
 //            table, the hidden row block written to LDS ([64][768] at a
@@ -784,7 +785,7 @@ int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
 //   phase B  the FFN2 tiles (2 row x 6 column tiles, three per wavefront)
 //            with K = 768 read from LDS and the residual epilogue.
 // The hidden activations never leave the CU.  Each workgroup stages the
-// GELU table and handles one row block.
+// GELU table, its loads in flight while the first rows load.
 // ---------------------------------------------------------------------------
 static constexpr int kFfnRows = 64, kFfnHRow = 784, kLnPrologueRow = 208;
 static_assert(kFfnRows * kFfnHRow + 4 * kGeluLutMaxWords <= 160 * 1024 / 2,
@@ -901,15 +902,28 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
   const int M = g1.m_dev ? min(*g1.m_dev, g1.m) : g1.m;
   const int nrb = (M + kFfnRows - 1) / kFfnRows;
   if ((int)blockIdx.x >= nrb) return;  // uniform: before any barrier
-  stage_lut(g1, lut);
+  // The step table loads in one round (at most eight 16-byte vectors per
+  // thread) and lands while the first row block's LayerNorm or A fragments
+  // load; its LDS writes precede the barrier in front of phase A.  Threads
+  // past the end reload the last vector (no predicated loads or writes).
+  static_assert(kGeluLutMaxWords / 4 <= 8 * 256, "one staging round");
+  const int n4 = g1.lut_words >> 2;
+  v4i tv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    tv[i] = reinterpret_cast<const v4i *>(kGeluLut + g1.lut_off)[min(tid + 256 * i, n4 - 1)];
+  auto write_lut = [&]() {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) reinterpret_cast<v4i *>(lut)[min(tid + 256 * i, n4 - 1)] = tv[i];
+  };
   const Rq r1a = rq_setup(g1.shift_a, -(1 << 23), (1 << 23) - 1);
   const Rq r2a = rq_setup(g2.shift_a, -128, 127), r2b = rq_setup(g2.os, -128, 127);
   constexpr bool LA1 = DIRS1 & 1;
   int qhi = g1.lut_qhi;
   asm("" : "+v"(qhi));  // the table clamp as one med3 (both bounds in VGPRs)
 
-  for (int rb = blockIdx.x; rb < nrb; rb += gridDim.x) {
-    const int r0 = rb * kFfnRows;
+  {
+    const int r0 = blockIdx.x * kFfnRows;  // one row block per workgroup
     // Weight fragments single-buffered: the next column tile's load is
     // issued after the current tile's MFMAs and lands during its GELU
     // epilogues; the biases are double-buffered.
@@ -932,6 +946,7 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
       load_w1(0, bs[0]);
       ln_rows<192, kLnPrologueRow>(fl.x + (size_t)r0 * 192, M - 1 - r0, hid, kFfnRows, fl.ln,
                                    fl.lw, r0, M - r0);
+      write_lut();
       __syncthreads();
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt)
@@ -948,6 +963,8 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
         for (int kt = 0; kt < 6; ++kt) af[rt][kt] = *reinterpret_cast<const v4i *>(ap + kt * 32);
       }
       load_w1(0, bs[0]);
+      write_lut();
+      __syncthreads();
     }
 #pragma unroll 2
     for (int ci = 0; ci < 6; ++ci) {
@@ -1050,15 +1067,11 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
         epi_operands<1, 1, EPI_RES>(g2, arow, ct, h, bias4, res4);
       }
     }
-    __syncthreads();  // the next row block rewrites hid
     if constexpr (LNE) {
+      __syncthreads();  // every output row is in zs
       const int8_t *zs = reinterpret_cast<const int8_t *>(lut);
       ln_rows<kLnPrologueRow, 192>(zs, kFfnRows - 1, fe.ln.out + (size_t)r0 * 192, M - r0, fe.ln,
                                    fe.lw, r0, M - r0);
-      if (rb + (int)gridDim.x < nrb) {
-        __syncthreads();  // the rows are read; the table comes back
-        stage_lut(g1, lut);
-      }
     }
   }
 }
