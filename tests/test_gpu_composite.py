@@ -329,3 +329,41 @@ def test_model_chains_layernorm1_through_ffn_kernels(oracle, pruned):
     assert np.array_equal(r.warnings, warnings)
     if pruned:
         assert np.array_equal(r.token_counts, counts)
+
+
+def test_model_layernorm_fallbacks_vs_oracle(oracle):
+    """Blocks whose LayerNorm leaves the int32 form (beta 17 binary places
+    below gamma, so gamma no longer sits at the common exponent): block 2's
+    LayerNorm 1 then runs as a launch of the general kernel (block 1's FFN
+    kernel does not write it) and block 5's LayerNorm 2 runs outside its FFN
+    kernel, which then writes no LayerNorm 1 for block 6 either; the other
+    blocks stay fused.  The LayerNorm launch count follows, and logits,
+    token counts and warnings match the oracle."""
+    import dataclasses
+    from heatvit_amd import _lib
+    from heatvit_amd.model import HeatViTModel
+    imgs, params = synth.pruned_workload(6)
+    blocks = list(params.blocks)
+    m1, f4 = blocks[1].mhsa, blocks[4].ffn
+    blocks[1] = dataclasses.replace(
+        blocks[1], mhsa=dataclasses.replace(m1, beta1_scale_exp=m1.gamma1_scale_exp - 17))
+    blocks[4] = dataclasses.replace(
+        blocks[4], ffn=dataclasses.replace(f4, beta2_scale_exp=f4.gamma2_scale_exp - 17))
+    p = dataclasses.replace(params, blocks=tuple(blocks))
+    L = _lib.lib()
+    L.hv_profile_enable(1)
+    try:
+        r = HeatViTModel().infer_batch(imgs, p)
+        ms = np.zeros(len(_lib.PROF_CLASSES), np.float32)
+        n = np.zeros(len(_lib.PROF_CLASSES), np.int32)
+        _lib.check(L.hv_profile_read(ms.ctypes.data, n.ctypes.data, len(ms)), "profile")
+    finally:
+        L.hv_profile_enable(0)
+    n = dict(zip(_lib.PROF_CLASSES, n.tolist()))
+    # blocks 1, 4, 7, 10 and the final one; block 2's LN1, block 5's LN2, block 6's LN1
+    assert n["layernorm"] == 5 + 3 and n["ffn"] == 12, n
+    logits, counts, status, warnings = oracle.model_infer_batch(imgs, p)
+    assert not status.any()
+    assert np.array_equal(r.logits, logits)
+    assert np.array_equal(r.token_counts, counts)
+    assert np.array_equal(r.warnings, warnings)
