@@ -9,10 +9,14 @@ selectors with stream compaction, final LayerNorm and the 1000-class head,
 with the images already resident in HBM.  Every output is bit-exact with
 the reference's golden model (tests/test_gpu_composite.py).
 
-`value` is the throughput with --streams batches in flight (default 3),
+`value` is the throughput with --streams batches in flight (default 4),
 each on its own HIP stream with its own workspace (heatvit_amd.model.Pipeline):
 the timed region holds exactly --steps forwards of 256 images, and the GPU
-overlaps one batch's latency-bound stages with another batch's GEMMs.  The
+overlaps one batch's latency-bound stages with another batch's GEMMs.  HIP
+maps streams onto GPU_MAX_HW_QUEUES hardware queues per process (4 by
+default); with fewer queues than streams plus the default one, batches share
+a queue and serialise, so the bench asks the runtime for --hw-queues (8)
+before it starts.  The
 same line reports one batch at a time (the per-batch latency), and checks
 that every pipeline slot's logits equal the single-stream forward's.
 
@@ -315,8 +319,11 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=256)
-    ap.add_argument("--streams", type=int, default=3,
+    ap.add_argument("--streams", type=int, default=4,
                     help="batches in flight, each on its own HIP stream (1: one at a time)")
+    ap.add_argument("--hw-queues", type=int, default=8,
+                    help="HIP hardware queues per process (GPU_MAX_HW_QUEUES, at most 32), "
+                         "set before the runtime starts; 0 leaves the environment's value")
     ap.add_argument("--cpu-passes", type=int, default=30,
                     help="most passes of the CPU oracle over the whole batch (0 skips it)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
@@ -335,6 +342,9 @@ def main():
               "(images are independent; see DESIGN.md for how the path would shard). "
               "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if args.hw_queues:
+        # before anything initialises HIP (torch and the library load below)
+        os.environ["GPU_MAX_HW_QUEUES"] = str(min(max(args.hw_queues, 1), 32))
 
     import torch
 
@@ -527,6 +537,7 @@ def main():
                                "224x224x3 int8, selectors before blocks 4/7/10 "
                                "(197->88->45->32 budget)",
                    "global_batch": args.batch, "batches_in_flight": args.streams,
+                   "hw_queues": int(os.environ.get("GPU_MAX_HW_QUEUES", "4")),
                    "mean_tokens_per_stage": mean_tokens},
         "one_batch_at_a_time": {"value": round(args.batch / (latency_ms / 1e3), 1),
                                 "ms_per_batch": round(latency_ms, 4)},
