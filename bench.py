@@ -321,6 +321,9 @@ def main():
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--streams", type=int, default=4,
                     help="batches in flight, each on its own HIP stream (1: one at a time)")
+    ap.add_argument("--control-streams", type=int, default=3,
+                    help="batches in flight for the unpruned control (its best: its "
+                         "stage-0 work fills the GPU with fewer)")
     ap.add_argument("--hw-queues", type=int, default=8,
                     help="HIP hardware queues per process (GPU_MAX_HW_QUEUES, at most 32), "
                          "set before the runtime starts; 0 leaves the environment's value")
@@ -453,14 +456,15 @@ def main():
         ctrl_logits = ctrl.logits[:args.batch].cpu().numpy()
         c_lat = timed(ctrl.forward, args.steps)
         c_wall = c_lat
-        if args.streams > 1:
-            cpipe = Pipeline(ctrl.model, args.batch, depth=args.streams)
-            for _ in range(max(1, args.warmup // 2, args.streams)):
+        cs = args.control_streams
+        if cs > 1:
+            cpipe = Pipeline(ctrl.model, args.batch, depth=cs)
+            for _ in range(max(1, args.warmup // 2, cs)):
                 cpipe.submit(dev)
             c_wall = timed(cpipe.submit, args.steps)
             del cpipe
         control = {"workload": "unpruned HeatViT-T (same weights, no selectors), batch "
-                               f"{args.batch}, {args.streams} in flight",
+                               f"{args.batch}, {cs} in flight",
                    "value": round(args.batch / (c_wall / 1e3), 1),
                    "ms_per_step": round(c_wall, 4),
                    "one_at_a_time": round(args.batch / (c_lat / 1e3), 1)}
