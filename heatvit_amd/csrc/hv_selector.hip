@@ -24,8 +24,32 @@
 
 #include "hv_device.h"
 #include "hv_internal.h"
+#include "gelu_lut.inc"  // generated at build time by gen_gelu_lut.py
 
 namespace hv {
+
+// A GELU layer's step table (gen_gelu_lut.py) when its output shift has one:
+// words [off, off + words) of kGeluLut, clamp [qlo, qhi], cb as gelu_table
+// takes it; off < 0: the layer evaluates ShiftGELU.
+struct SelLut {
+  int off, words, qlo, qhi, cb;
+};
+
+// Copies a step table into LDS with 16-byte loads, four rounds in flight
+// (tables start on 16-byte boundaries and hold a multiple of four words).
+// All kHeadThreads threads call it; the caller puts a barrier after it.
+__device__ __forceinline__ void sel_stage_lut(const SelLut &t, unsigned *lut, int tid) {
+  const v4i *src = reinterpret_cast<const v4i *>(kGeluLut + t.off);
+  v4i *dst = reinterpret_cast<v4i *>(lut);
+  const int n4 = t.words >> 2;
+  for (int base = tid; base < n4; base += 4 * 256) {
+    v4i v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = src[min(base + r * 256, n4 - 1)];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dst[min(base + r * 256, n4 - 1)] = v[r];
+  }
+}
 
 static constexpr int kMaxCand = 196;
 
@@ -66,10 +90,14 @@ constexpr int kCandPad = kCandTiles * 16;
 // 64 bits).  Result lane l of a tile holds output channel 16 ct + l % 16 of
 // candidates 4 (l / 16) + i.  The logits (16 -> 2), the 2-way softmax and
 // the lane mean of the head slice (the head statistic) are per candidate.
+// The GELU layers with a step table for their output shift read it from
+// LDS (staged per layer: local, h1, h2) instead of evaluating ShiftGELU.
 __global__ __launch_bounds__(kHeadThreads) void k_selector_head(
     hv_selector_dev p, const int8_t *tokens, const int32_t *offsets, int batch,
     const uint8_t *pkg_in, int32_t *hs_out, int8_t *stats_out, int fast_shifts,
-    hv_selector_ckpt ck) {
+    hv_selector_ckpt ck, SelLut tl, SelLut t1, SelLut t2) {
+  static_assert(kHeadThreads == 256, "sel_stage_lut strides");
+  __shared__ __attribute__((aligned(16))) unsigned lut[kGeluLutMaxWords];
   __shared__ __attribute__((aligned(16))) int8_t wl[32 * 64];   // local_wt[h] [32][64]
   __shared__ __attribute__((aligned(16))) int8_t w1[32 * 64];   // w1t[h] [32][64]
   __shared__ __attribute__((aligned(16))) int8_t w2[16 * 32];   // w2t[h] [16][32]
@@ -107,6 +135,7 @@ __global__ __launch_bounds__(kHeadThreads) void k_selector_head(
     if (tid >= 96 && tid < 128) bl[tid - 96] = p.local_b[h * 32 + tid - 96];
     if (tid >= 160 && tid < 176) bb2[tid - 160] = p.b2[h * 16 + tid - 160];
   }
+  if (tl.off >= 0) sel_stage_lut(tl, lut, tid);
   __syncthreads();
   // int32 GELU preconditions: |acc| <= K*2^14 for the layer's K.
   const int lim64 = (1 << 30) - 1 - 64 * 16384, lim32 = (1 << 30) - 1 - 32 * 16384;
@@ -147,13 +176,22 @@ __global__ __launch_bounds__(kHeadThreads) void k_selector_head(
         }
       }
       const int j = ct * 16 + col;
+      if (fast && tl.off >= 0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        local_s[(rt * 16 + grp * 4 + i) * 32 + j] =
-            (int8_t)sel_gelu(acc[i], bl[j], fast, ra, rb, sh_in, sh_out);
+        for (int i = 0; i < 4; ++i)
+          local_s[(rt * 16 + grp * 4 + i) * 32 + j] =
+              (int8_t)gelu_table_u8(rq(acc[i] + bl[j], ra), lut, tl.cb, tl.qlo, tl.qhi);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          local_s[(rt * 16 + grp * 4 + i) * 32 + j] =
+              (int8_t)sel_gelu(acc[i], bl[j], fast, ra, rb, sh_in, sh_out);
+      }
     }
   }
   __syncthreads();
+  // score layer 1's table replaces the local layer's (barriers follow)
+  if (t1.off >= 0) sel_stage_lut(t1, lut, tid);
   // Global feature = sat8(round_div(sum_c local, C)) and the folded bias of
   // score layer 1.
   {
@@ -197,15 +235,26 @@ __global__ __launch_bounds__(kHeadThreads) void k_selector_head(
       const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, wb, v4i{0}, 0, 0, 0);
       const int j = ct * 16 + col;
       const i64 bias = bb1[j];
+      if (fast && t1.off >= 0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int v = fast ? rq(gelu_q16(rq(acc[i] + (int)bias, ra)), rb)
-                           : gelu_exact64(acc[i], bias, sh_in, sh_out);
-        h1_s[(rt * 16 + grp * 4 + i) * 32 + j] = (int8_t)v;
+        for (int i = 0; i < 4; ++i)
+          h1_s[(rt * 16 + grp * 4 + i) * 32 + j] =
+              (int8_t)gelu_table_u8(rq(acc[i] + (int)bias, ra), lut, t1.cb, t1.qlo, t1.qhi);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int v = fast ? rq(gelu_q16(rq(acc[i] + (int)bias, ra)), rb)
+                             : gelu_exact64(acc[i], bias, sh_in, sh_out);
+          h1_s[(rt * 16 + grp * 4 + i) * 32 + j] = (int8_t)v;
+        }
       }
     }
   }
   __syncthreads();
+  if (t2.off >= 0) {  // score layer 2's table
+    sel_stage_lut(t2, lut, tid);
+    __syncthreads();
+  }
   // Score layer 2.
   {
     const int sh_in = -16 - (p.h1_out_exp + p.score_w2_exp), sh_out = p.h2_out_exp + 16;
@@ -215,10 +264,17 @@ __global__ __launch_bounds__(kHeadThreads) void k_selector_head(
       const long a = *reinterpret_cast<const long *>(&h1_s[(rt * 16 + col) * 32 + grp * 8]);
       const long wb = *reinterpret_cast<const long *>(&w2[col * 32 + grp * 8]);
       const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, wb, v4i{0}, 0, 0, 0);
+      if (fast && t2.off >= 0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        h2_s[(rt * 16 + grp * 4 + i) * 16 + col] =
-            (int8_t)sel_gelu(acc[i], bb2[col], fast, ra, rb, sh_in, sh_out);
+        for (int i = 0; i < 4; ++i)
+          h2_s[(rt * 16 + grp * 4 + i) * 16 + col] =
+              (int8_t)gelu_table_u8(rq(acc[i] + bb2[col], ra), lut, t2.cb, t2.qlo, t2.qhi);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          h2_s[(rt * 16 + grp * 4 + i) * 16 + col] =
+              (int8_t)sel_gelu(acc[i], bb2[col], fast, ra, rb, sh_in, sh_out);
+      }
     }
   }
   __syncthreads();
@@ -501,8 +557,14 @@ int launch_selector(const SelectorArgs &a, hipStream_t s) {
     const int fast = in(-16 - (p.in_exp + p.local_w_exp)) && in(p.local_out_exp + 16) &&
                      in(-16 - (p.concat_out_exp + p.score_w1_exp)) && in(p.h1_out_exp + 16) &&
                      in(-16 - (p.h1_out_exp + p.score_w2_exp)) && in(p.h2_out_exp + 16);
+    auto table = [](int so) {
+      if (so < kGeluLutSoMin || so > kGeluLutSoMax) return SelLut{-1, 0, 0, 0, 0};
+      const GeluLutInfo &t = kGeluLutInfo[so - kGeluLutSoMin];
+      return SelLut{t.off, t.words, t.qlo, t.qhi, -4 * (t.qlo >> kGeluCoarseShift)};
+    };
     hv_launch(k_selector_head, dim3((a.batch * 3 + 7) / 8 * 8), dim3(kHeadThreads), 0, s, p,
-              a.tokens, a.offsets, a.batch, a.pkg_in, a.hs, a.stats, fast, a.ck);
+              a.tokens, a.offsets, a.batch, a.pkg_in, a.hs, a.stats, fast, a.ck,
+              table(p.local_out_exp + 16), table(p.h1_out_exp + 16), table(p.h2_out_exp + 16));
     if ((rc = check_hip(hipGetLastError(), "k_selector_head launch"))) return rc;
   }
   hv_launch(k_selector_keep, dim3(a.batch), dim3(256), 0, s, a.offsets, a.pkg_in,
