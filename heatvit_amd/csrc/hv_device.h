@@ -265,6 +265,34 @@ __device__ __forceinline__ unsigned gelu_table_u8(int q, const unsigned *lut, in
   return off >= __builtin_amdgcn_ubfe(w, 16, 8) ? w >> 8 : w;
 }
 
+// gelu_table_u8 of N values in stages (the N coarse reads, then the N
+// fine reads, then the selects) with scheduling barriers between them, so
+// each stage's LDS reads are in flight together (the compiler had issued
+// them eight at a time).
+template <int N>
+__device__ __forceinline__ void gelu_table_u8_n(const int (&q)[N], unsigned (&o)[N],
+                                                const unsigned *lut, int cb, int qlo, int qhi) {
+  const char *t = reinterpret_cast<const char *>(lut);
+  int c[N], w1[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    asm("v_med3_i32 %0, %1, %2, %3" : "=v"(c[j]) : "v"(q[j]), "v"(qlo), "v"(qhi));
+    int b = c[j] >> kGeluCoarseShift;
+    asm("" : "+v"(b));
+    w1[j] = *reinterpret_cast<const int *>(t + cb + b * 4);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  unsigned w[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j)
+    w[j] = *reinterpret_cast<const unsigned *>(t + (w1[j] >> 5) + (c[j] >> (w1[j] & 31)) * 4);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const unsigned off = __builtin_amdgcn_ubfe((unsigned)c[j], 0, (unsigned)w1[j]);
+    o[j] = off >= __builtin_amdgcn_ubfe(w[j], 16, 8) ? w[j] >> 8 : w[j];
+  }
+}
 // The same as a sign-extended int.
 __device__ __forceinline__ int gelu_table(int q, const unsigned *lut, int cb, int qlo, int qhi) {
   return (int)(int8_t)gelu_table_u8(q, lut, cb, qlo, qhi);

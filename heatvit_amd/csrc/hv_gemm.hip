@@ -990,10 +990,14 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
       for (int rt = 0; rt < 2; ++rt) {
         int o[16];
         if (fast) {
+          int qv[16];
+          unsigned ov[16];
 #pragma unroll
           for (int j = 0; j < 16; ++j)
-            o[j] = (int)gelu_lut(shift_nowrap<LA1>(acc[rt][j] + bs[cur][j >> 2][j & 3], r1a),
-                                 lut, qhi, g1);
+            qv[j] = shift_nowrap<LA1>(acc[rt][j] + bs[cur][j >> 2][j & 3], r1a);
+          gelu_table_u8_n<16>(qv, ov, lut, g1.lut_cb, g1.lut_qlo, qhi);
+#pragma unroll
+          for (int j = 0; j < 16; ++j) o[j] = (int)ov[j];
         } else {
 #pragma unroll
           for (int j = 0; j < 16; ++j)
