@@ -155,37 +155,71 @@ __global__ __launch_bounds__(kHeadThreads) void k_selector_head(
     const Rq ra = rq_setup(sh_in, -(1 << 23), (1 << 23) - 1), rb = rq_setup(sh_out, -128, 127);
     __syncthreads();
     const bool fast = fast_s[0];
-    for (int t = wave; t < ntiles * 2; t += 4) {
-      const int rt = t >> 1, ct = t & 1;
-      const int c = min(rt * 16 + col, C - 1);
-      const v4i a = *reinterpret_cast<const v4i *>(cand + (size_t)c * 192 + grp * 16);
-      const v4i wb = *reinterpret_cast<const v4i *>(&wl[(ct * 16 + col) * 64 + grp * 16]);
-      const v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, wb, v4i{0}, 0, 0, 0);
-      if (ct == 0) {
-        // lane mean of the candidate's 64 head lanes (selector.py:358-367)
-        int sum = 0;
+    // two tiles per round: both candidate loads in flight, then the eight
+    // table lookups staged together
+    const int nt = ntiles * 2;
+    for (int t0 = wave; t0 < nt; t0 += 8) {
+      v4i a[2], acc[2];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) sum = dot4(a[k], 0x01010101, sum);
-        sum += __shfl_xor(sum, 16);
-        sum += __shfl_xor(sum, 32);
-        if (grp == 0 && rt * 16 + col < C) {
-          const int8_t stat = (int8_t)sat_bits(round_div_pos(sum, 64), 8);
-          const int cc = rt * 16 + col;
-          stats_out[((size_t)b * kMaxCand + cc) * 3 + h] = stat;
-          if (ck.head_stats) ck.head_stats[((size_t)b * kMaxCand + cc) * 3 + h] = stat;
+      for (int u = 0; u < 2; ++u) {
+        const int tv = min(t0 + 4 * u, nt - 1);
+        const int c = min((tv >> 1) * 16 + col, C - 1);
+        a[u] = *reinterpret_cast<const v4i *>(cand + (size_t)c * 192 + grp * 16);
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int tv = min(t0 + 4 * u, nt - 1), ct = tv & 1;
+        const v4i wb = *reinterpret_cast<const v4i *>(&wl[(ct * 16 + col) * 64 + grp * 16]);
+        acc[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], wb, v4i{0}, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int t = t0 + 4 * u, rt = t >> 1, ct = t & 1;
+        if (t < nt && ct == 0) {
+          // lane mean of the candidate's 64 head lanes (selector.py:358-367)
+          int sum = 0;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) sum = dot4(a[u][k], 0x01010101, sum);
+          sum += __shfl_xor(sum, 16);
+          sum += __shfl_xor(sum, 32);
+          if (grp == 0 && rt * 16 + col < C) {
+            const int8_t stat = (int8_t)sat_bits(round_div_pos(sum, 64), 8);
+            const int cc = rt * 16 + col;
+            stats_out[((size_t)b * kMaxCand + cc) * 3 + h] = stat;
+            if (ck.head_stats) ck.head_stats[((size_t)b * kMaxCand + cc) * 3 + h] = stat;
+          }
         }
       }
-      const int j = ct * 16 + col;
       if (fast && tl.off >= 0) {
+        int qv[8];
+        unsigned ov[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          local_s[(rt * 16 + grp * 4 + i) * 32 + j] =
-              (int8_t)gelu_table_u8(rq(acc[i] + bl[j], ra), lut, tl.cb, tl.qlo, tl.qhi);
+        for (int u = 0; u < 2; ++u) {
+          const int j = ((t0 + 4 * u) & 1) * 16 + col;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) qv[4 * u + i] = rq(acc[u][i] + bl[j], ra);
+        }
+        gelu_table_u8_n<8>(qv, ov, lut, tl.cb, tl.qlo, tl.qhi);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int t = t0 + 4 * u, rt = t >> 1, j = (t & 1) * 16 + col;
+          if (t < nt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              local_s[(rt * 16 + grp * 4 + i) * 32 + j] = (int8_t)ov[4 * u + i];
+          }
+        }
       } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          local_s[(rt * 16 + grp * 4 + i) * 32 + j] =
-              (int8_t)sel_gelu(acc[i], bl[j], fast, ra, rb, sh_in, sh_out);
+        for (int u = 0; u < 2; ++u) {
+          const int t = t0 + 4 * u, rt = t >> 1, j = (t & 1) * 16 + col;
+          if (t < nt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              local_s[(rt * 16 + grp * 4 + i) * 32 + j] =
+                  (int8_t)sel_gelu(acc[u][i], bl[j], fast, ra, rb, sh_in, sh_out);
+          }
+        }
       }
     }
   }
