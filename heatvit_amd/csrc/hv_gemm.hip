@@ -784,6 +784,9 @@ int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
 //            784-byte row stride, conflict-free 16-byte reads);
 //   phase B  the FFN2 tiles (2 row x 6 column tiles, three per wavefront)
 //            with K = 768 read from LDS and the residual epilogue.
+// Optionally LayerNorm 2 of y runs in front of phase A (the normalised rows
+// pass through LDS, y is read once more as the residual) and the next
+// block's LayerNorm 1 of the output rows behind phase B (ln_rows, below).
 // The hidden activations never leave the CU.  Each workgroup stages the
 // GELU table, its loads in flight while the first rows load.
 // ---------------------------------------------------------------------------
