@@ -191,16 +191,17 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   int8_t *hidden = ck && ck->hidden ? ck->hidden : w.hidden;
   int rc;
 
-  const int8_t *ln1 = ck && ck->ln1 ? ck->ln1 : w.ln;
+  int8_t *ln1_out = ck && ck->ln1 ? ck->ln1 : w.ln;
   int8_t *ln2 = ck && ck->ln2 ? ck->ln2 : w.ln;
   if (chain.next_done) *chain.next_done = false;
-  if (chain.ln1_in && !ck) {
-    ln1 = chain.ln1_in;
-  } else {
+  // QKV reads LayerNorm 1 from the previous block's FFN kernel when it wrote
+  // it, else from this block's own LayerNorm launch.
+  const bool chained_in = chain.ln1_in && !ck;
+  const int8_t *ln1 = chained_in ? chain.ln1_in : ln1_out;
+  if (!chained_in) {
     ProfScope ps(HV_PROF_LAYERNORM, s);
-    rc = launch_layernorm(x, p.ln1_gamma, p.ln1_beta, const_cast<int8_t *>(ln1), max_rows,
-                          rows_dev, p.x_exp, p.gamma1_exp, p.beta1_exp, p.ln1_out_exp, nullptr,
-                          lw, s);
+    rc = launch_layernorm(x, p.ln1_gamma, p.ln1_beta, ln1_out, max_rows, rows_dev, p.x_exp,
+                          p.gamma1_exp, p.beta1_exp, p.ln1_out_exp, nullptr, lw, s);
     if (rc) return rc;
   }
   GemmArgs g{};
