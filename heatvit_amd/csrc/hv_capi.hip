@@ -80,8 +80,12 @@ static void prof_clear() {
 
 // ---------------------------------------------------------------- utilities
 
+// cls (optional): row 0 of each image's 197 rows in x is the CLS row,
+// align_add(cls, pos[0]) (transformer.py:130-145), written here rather than
+// by a launch of its own after the patch embedding.
 __global__ void k_init_offsets(int32_t *offsets, uint8_t *pkg, int32_t *token_counts,
-                               int32_t *warnings, int batch, int rows) {
+                               int32_t *warnings, int batch, int rows, hv_patch_dev cls,
+                               int8_t *x) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i <= batch) offsets[i] = i * rows;
   if (i < batch) {
@@ -90,12 +94,21 @@ __global__ void k_init_offsets(int32_t *offsets, uint8_t *pkg, int32_t *token_co
       for (int s = 0; s < 4; ++s) token_counts[(size_t)i * 4 + s] = rows;
     if (warnings) warnings[i] = 0;
   }
+  if (x)
+    for (int j = i; j < batch * 192; j += gridDim.x * blockDim.x) {
+      const int b = j / 192, c = j - b * 192;
+      x[(size_t)b * HV_MAX_TOKENS * 192 + c] =
+          (int8_t)align_add_i8(cls.cls[c], cls.cls_exp, cls.pos[c], cls.pos_exp, cls.tokens_exp);
+    }
 }
 
 int launch_init_offsets(int32_t *offsets, uint8_t *pkg, int32_t *token_counts,
-                        int32_t *warnings, int batch, int rows, hipStream_t s) {
-  hv_launch(k_init_offsets, dim3((batch + 256) / 256), dim3(256), 0, s, offsets, pkg,
-                     token_counts, warnings, batch, rows);
+                        int32_t *warnings, int batch, int rows, hipStream_t s,
+                        const hv_patch_dev *cls, int8_t *x) {
+  // batch + 1 offsets; with the CLS rows, batch * 192 bytes (a superset)
+  const int items = cls && x ? batch * 192 : batch + 1;
+  hv_launch(k_init_offsets, dim3((items + 255) / 256), dim3(256), 0, s, offsets, pkg,
+            token_counts, warnings, batch, rows, cls ? *cls : hv_patch_dev{}, cls ? x : nullptr);
   return check_hip(hipGetLastError(), "k_init_offsets launch");
 }
 
@@ -608,7 +621,7 @@ static int model_forward(const hv_model_dev *p, const void *images, bool float_i
   {
     ProfScope ps(HV_PROF_OTHER, s);
     rc = launch_init_offsets(w.off_a, w.pkg_a, token_counts, warnings, batch, HV_MAX_TOKENS,
-                             s);
+                             s, &p->patch, w.xa);
   }
   if (rc) return rc;
   {
@@ -617,9 +630,11 @@ static int model_forward(const hv_model_dev *p, const void *images, bool float_i
       // the FFN hidden buffer ([B*197][768]) is free until block 1's FFN
       rc = launch_image_front(static_cast<const float *>(images), batch, p->patch.image_exp,
                               w.blk.hidden, true, s);
-      if (rc == HV_OK) rc = launch_patch_embed(p->patch, w.blk.hidden, batch, w.xa, s, true);
+      if (rc == HV_OK)
+        rc = launch_patch_embed(p->patch, w.blk.hidden, batch, w.xa, s, true, false);
     } else {
-      rc = launch_patch_embed(p->patch, static_cast<const int8_t *>(images), batch, w.xa, s);
+      rc = launch_patch_embed(p->patch, static_cast<const int8_t *>(images), batch, w.xa, s,
+                              false, false);
     }
   }
   if (rc) return rc;

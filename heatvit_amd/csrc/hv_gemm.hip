@@ -1192,7 +1192,7 @@ __global__ void k_cls_rows(const int8_t *cls, const int8_t *pos, int8_t *x, int 
 }
 
 int launch_patch_embed(const hv_patch_dev &p, const int8_t *images, int batch, int8_t *x,
-                       hipStream_t s, bool patch_rows) {
+                       hipStream_t s, bool patch_rows, bool cls_rows) {
   if (batch <= 0) return HV_OK;
   GemmArgs g{};
   g.a = images;
@@ -1210,7 +1210,7 @@ int launch_patch_embed(const hv_patch_dev &p, const int8_t *images, int batch, i
   g.out_exp = p.tokens_exp;
   g.lda = patch_rows ? 768 : 0;
   int rc = launch_gemm(g, patch_rows ? A_ROWS : A_PATCH, EPI_PATCH, s);
-  if (rc) return rc;
+  if (rc || !cls_rows) return rc;
   hv_launch(k_cls_rows, dim3(batch), dim3(192), 0, s, p.cls, p.pos, x, p.cls_exp,
                      p.pos_exp, p.tokens_exp);
   return check_hip(hipGetLastError(), "k_cls_rows launch");

@@ -98,8 +98,9 @@ int launch_gelu_post(bool table, const int64_t *in, int64_t *out, int64_t n, int
 // patches of NHWC 224x224x3 images (or, with patch_rows, the patch matrix
 // [B*196][768] itself), epilogue adds the position rows, and the CLS rows
 // are written by a second small kernel.
+// cls_rows false: the CLS rows are written elsewhere (launch_init_offsets).
 int launch_patch_embed(const hv_patch_dev &p, const int8_t *images, int batch, int8_t *x,
-                       hipStream_t s, bool patch_rows = false);
+                       hipStream_t s, bool patch_rows = false, bool cls_rows = true);
 
 // Image front end: float CHW [B][3][224][224] -> int8 at input_exp, as flat
 // NHWC images or (patch_rows) as the patch matrix [B*196][768].
@@ -171,8 +172,11 @@ struct SelectorArgs {
 int launch_selector(const SelectorArgs &a, hipStream_t s);
 
 // Small utility kernels.
+// cls, x (optional): also writes the CLS row (row 0 of each image's
+// HV_MAX_TOKENS rows) of the patch embedding into x.
 int launch_init_offsets(int32_t *offsets, uint8_t *pkg, int32_t *token_counts,
-                        int32_t *warnings, int batch, int rows_per_image, hipStream_t s);
+                        int32_t *warnings, int batch, int rows_per_image, hipStream_t s,
+                        const hv_patch_dev *cls = nullptr, int8_t *x = nullptr);
 // Per-image token-count check of a caller's offsets: status[b] =
 // HV_ERR_TOKEN_COUNT unless 1 <= count <= 197 and the rows lie in
 // [0, capacity), else 0; warnings[b] = 0.  Either pointer may be NULL.
