@@ -245,11 +245,6 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   g.m_dev = rows_dev; g.m = max_rows; g.n = 192; g.k = 192; g.lda = 192; g.ldc = 192; g.ldr = 192;
   g.shift_a = p.msa_out_exp - (p.context_out_exp + p.wproj_exp);
   g.mid_exp = p.msa_out_exp; g.res_exp = p.x_exp; g.out_exp = p.ffn_x_exp;
-  {
-    ProfScope ps(HV_PROF_GEMM_PROJ, s);
-    rc = launch_gemm(g, A_ROWS, HV_EPI_RESIDUAL, s);
-  }
-  if (rc) return rc;
 
   GemmArgs g1{};
   g1.a = ln2; g1.b = p.w1_p; g1.bias = p.b1; g1.c = hidden; g1.m_dev = rows_dev;
@@ -265,20 +260,35 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   g2.mid_exp = p.ffn_out_exp; g2.res_exp = p.ffn_x_exp; g2.out_exp = p.out_exp;
   // LayerNorm 2 inside the fused FFN kernel (its rows pass through LDS)
   // when neither its output nor the hidden rows are wanted and its
-  // exponents take the int32 form.
-  Ln32 ln;
-  if (!(ck && (ck->hidden || ck->ln2)) &&
-      ln32_setup(p.ln2_gamma, p.ln2_beta, ln2, p.ffn_x_exp, p.gamma2_exp, p.beta2_exp,
-                 p.ln2_out_exp, &ln)) {
+  // exponents take the int32 form; the next block's LayerNorm 1 of z at the
+  // kernel's end when its exponents take the int32 form.
+  Ln32 ln, ln_n;
+  const bool ln2_in = !(ck && (ck->hidden || ck->ln2)) &&
+                      ln32_setup(p.ln2_gamma, p.ln2_beta, ln2, p.ffn_x_exp, p.gamma2_exp,
+                                 p.beta2_exp, p.ln2_out_exp, &ln);
+  const hv_block_dev *nx = ck ? nullptr : chain.next;
+  const bool chained = ln2_in && nx && chain.next_ln1 &&
+                       ln32_setup(nx->ln1_gamma, nx->ln1_beta, chain.next_ln1, nx->x_exp,
+                                  nx->gamma1_exp, nx->beta1_exp, nx->ln1_out_exp, &ln_n);
+  const LnPrologue fe{nullptr, ln_n, lw};
+  // Without checkpoints the projection runs in the fused FFN kernel too, y
+  // staying on the CU.
+  if (ln2_in && !ck) {
+    const LnPrologue fl{nullptr, ln, lw};
+    ProfScope ps(HV_PROF_FFN, s);
+    rc = launch_ffn(g1, g2, s, &fl, chained ? &fe : nullptr, &g);
+    if (rc != 1) {
+      if (rc == HV_OK && chained && chain.next_done) *chain.next_done = true;
+      return rc;
+    }
+  }
+  {
+    ProfScope ps(HV_PROF_GEMM_PROJ, s);
+    rc = launch_gemm(g, A_ROWS, HV_EPI_RESIDUAL, s);
+  }
+  if (rc) return rc;
+  if (ln2_in) {
     const LnPrologue fl{y, ln, lw};
-    // The next block's LayerNorm 1 of z at the kernel's end, when its
-    // exponents take the int32 form.
-    const hv_block_dev *nx = ck ? nullptr : chain.next;
-    Ln32 ln_n;
-    const bool chained = nx && chain.next_ln1 &&
-                         ln32_setup(nx->ln1_gamma, nx->ln1_beta, chain.next_ln1, nx->x_exp,
-                                    nx->gamma1_exp, nx->beta1_exp, nx->ln1_out_exp, &ln_n);
-    const LnPrologue fe{nullptr, ln_n, lw};
     ProfScope ps(HV_PROF_FFN, s);
     rc = launch_ffn(g1, g2, s, &fl, chained ? &fe : nullptr);
     if (rc != 1) {

@@ -786,7 +786,9 @@ int launch_gemm(const GemmArgs &g_in, int a_mode, int epi, hipStream_t s) {
 //            with K = 768 read from LDS and the residual epilogue.
 // Optionally LayerNorm 2 of y runs in front of phase A (the normalised rows
 // pass through LDS, y is read once more as the residual) and the next
-// block's LayerNorm 1 of the output rows behind phase B (ln_rows, below).
+// block's LayerNorm 1 of the output rows behind phase B (ln_rows, below);
+// with LayerNorm 2 inside, the attention projection that produces y can run
+// first as well (phase P: 2 x 6 tiles, K = 192; y stays on the CU).
 // The hidden activations never leave the CU.  Each workgroup stages the
 // GELU table, its loads in flight while the first rows load.
 // ---------------------------------------------------------------------------
@@ -890,13 +892,50 @@ __device__ __forceinline__ void ln_rows(const int8_t *src, int clamp, int8_t *ds
   }
 }
 
+// Epilogue of one attention-projection tile in the fused FFN: lane l's 16
+// bytes of y = align_add(x, requant(ctx Wp + bp)) (transformer.py:267-272,
+// 413-421), in the int32 form when every lane's biases allow it, else exact.
+template <bool LA, bool LB>
+__device__ __forceinline__ v4i proj_epi(const GemmArgs &gp, const v16i &acc, const v4i (&b4)[4],
+                                        v4i x4, const Rq &rpa, const Rq &rpb) {
+  int bmax = b4[0][0], bmin = bmax;
+#pragma unroll
+  for (int j = 1; j < 16; ++j) {
+    bmax = max(bmax, b4[j >> 2][j & 3]);
+    bmin = min(bmin, b4[j >> 2][j & 3]);
+  }
+  int o[16];
+  if (__all(bmax <= gp.acc_lim && bmin >= -gp.acc_lim)) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int t8 = rq_dir_nowrap<LA>(acc[j] + b4[j >> 2][j & 3], rpa);
+      const int r8 = (int)(int8_t)(x4[j >> 2] >> (8 * (j & 3)));
+      o[j] = rq_dir<LB>(r8 * (1 << gp.da) + t8 * (1 << gp.db), rpb);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int r8 = (int)(int8_t)(x4[j >> 2] >> (8 * (j & 3)));
+      o[j] = epi_exact(EPI_RES, acc[j], b4[j >> 2][j & 3], r8, gp.shift_a, gp.shift_b, gp.da,
+                       gp.db, gp.os)[0];
+    }
+  }
+  return v4i{pack4(o[0], o[1], o[2], o[3]), pack4(o[4], o[5], o[6], o[7]),
+             pack4(o[8], o[9], o[10], o[11]), pack4(o[12], o[13], o[14], o[15])};
+}
+
 // LN: LayerNorm 2 in front (fl); LNE: the next block's LayerNorm 1 of the
 // output rows behind (fe, output fe.ln.out): phase B also writes its rows to
 // LDS where the GELU table was (phase A is done with it), and the rows are
-// normalised once they are complete.
-template <int DIRS1, int DIRS2, bool LN, bool LNE>
+// normalised once they are complete.  PJ (with LN): the attention
+// projection and its residual (gp, requant directions dirsp) run first and
+// produce y, which never leaves the CU: each wavefront computes the y tiles
+// of its phase-B tiles and keeps their bytes as phase B's residual, and the
+// y rows pass through LDS to LayerNorm 2.
+template <int DIRS1, int DIRS2, bool LN, bool LNE, bool PJ>
 __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologue fl,
-                                             LnPrologue fe) {
+                                             LnPrologue fe, GemmArgs gp, int dirsp) {
+  static_assert(!PJ || LN, "the projection feeds the LayerNorm in front");
   __shared__ __attribute__((aligned(16))) int8_t hid[kFfnRows * kFfnHRow];
   // static, so its LDS address is a constant the table reads can fold
   __shared__ __attribute__((aligned(16))) unsigned lut[kGeluLutMaxWords];
@@ -940,10 +979,63 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
       for (int q = 0; q < 4; ++q)
         bi[q] = *reinterpret_cast<const v4i *>(g1.bias + ct * 32 + 16 * h + 4 * q);
     };
+    // Phase P (PJ): y tiles wave, wave + 4, wave + 8 of the 2 x 6 (phase B's
+    // tiles), K = 192 from the ctx rows; their bytes stay in yres and go to
+    // LDS (208-byte rows) for LayerNorm 2.
+    v4i yres[PJ ? 3 : 1];
+    if constexpr (PJ) {
+      const Rq rpa = rq_setup(gp.shift_a, -128, 127), rpb = rq_setup(gp.os, -128, 127);
+#pragma unroll
+      for (int ti = 0; ti < 3; ++ti) {
+        const int t = wave + 4 * ti, rt = t / 6, ct = t - rt * 6;
+        const int8_t *ap = gp.a + (size_t)min(r0 + 32 * rt + l32, M - 1) * 192 + 16 * h;
+        const int8_t *bp = gp.b + (size_t)ct * 6 * 1024 + lane * 16;
+        v4i pa[6], pw[6], b4[4];
+#pragma unroll
+        for (int kt = 0; kt < 6; ++kt) {
+          pa[kt] = *reinterpret_cast<const v4i *>(ap + kt * 32);
+          pw[kt] = *reinterpret_cast<const v4i *>(bp + kt * 1024);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          b4[q] = *reinterpret_cast<const v4i *>(gp.bias + ct * 32 + 16 * h + 4 * q);
+        const v4i x4 = *reinterpret_cast<const v4i *>(
+            gp.res + (size_t)min(r0 + 32 * rt + l32, M - 1) * 192 + ct * 32 + 16 * h);
+        v16i acc = v16i{0};
+#pragma unroll
+        for (int kt = 0; kt < 6; ++kt)
+          acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(pw[kt], pa[kt], acc, 0, 0, 0);
+        v4i yv;
+        switch (dirsp) {
+          case 0: yv = proj_epi<false, false>(gp, acc, b4, x4, rpa, rpb); break;
+          case 1: yv = proj_epi<true, false>(gp, acc, b4, x4, rpa, rpb); break;
+          case 2: yv = proj_epi<false, true>(gp, acc, b4, x4, rpa, rpb); break;
+          default: yv = proj_epi<true, true>(gp, acc, b4, x4, rpa, rpb); break;
+        }
+        yres[ti] = yv;
+        *reinterpret_cast<v4i *>(&hid[(32 * rt + l32) * kLnPrologueRow + ct * 32 + 16 * h]) = yv;
+      }
+    }
     // Phase A.  A fragments of both row tiles, all six K-steps; the weight
     // fragments and biases of column tile ci + 1 load while tile ci runs.
     v4i af[2][6];
-    if constexpr (LN) {
+    if constexpr (PJ) {
+      // y complete in LDS; LayerNorm 2 in place (each group rewrites the
+      // rows it read)
+      write_lut();
+      __syncthreads();
+      load_w1(0, bs[0]);
+      ln_rows<kLnPrologueRow, kLnPrologueRow>(hid, kFfnRows - 1, hid, kFfnRows, fl.ln, fl.lw, r0,
+                                              M - r0);
+      __syncthreads();
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int kt = 0; kt < 6; ++kt)
+          af[rt][kt] = *reinterpret_cast<const v4i *>(&hid[(32 * rt + l32) * kLnPrologueRow +
+                                                           kt * 32 + 16 * h]);
+      __syncthreads();
+    } else if constexpr (LN) {
       // the first weight tile loads while the LayerNorm runs; its rows
       // pass through hid (free until phase A writes it)
       load_w1(0, bs[0]);
@@ -1022,10 +1114,17 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
     v4i wb[3][4], bias4[1][4], res4[1][1];
     int rt, ct;
     tile_of(0, rt, ct);
-    {
+    // the tile's biases and residual bytes (PJ: the residual from yres)
+    auto operands = [&]() {
       const int arow[1] = {min(r0 + 32 * rt + l32, M - 1)};
-      epi_operands<1, 1, EPI_RES>(g2, arow, ct, h, bias4, res4);
-    }
+      if constexpr (PJ) {
+        epi_operands<1, 1, EPI_I8>(g2, arow, ct, h, bias4, res4);
+        res4[0][0] = yres[0];
+      } else {
+        epi_operands<1, 1, EPI_RES>(g2, arow, ct, h, bias4, res4);
+      }
+    };
+    operands();
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -1070,8 +1169,11 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
       if (ti + 1 < 3) {
         rt = nrt;
         ct = nct;
-        const int arow[1] = {min(r0 + 32 * rt + l32, M - 1)};
-        epi_operands<1, 1, EPI_RES>(g2, arow, ct, h, bias4, res4);
+        if constexpr (PJ) {
+          yres[0] = yres[1];
+          yres[1] = yres[2];
+        }
+        operands();
       }
     }
     if constexpr (LNE) {
@@ -1083,29 +1185,40 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
   }
 }
 
-template <int DIRS1, bool LN, bool LNE>
+template <int DIRS1, bool LN, bool LNE, bool PJ>
 static void launch_ffn_d(const GemmArgs &g1, const GemmArgs &g2, const LnPrologue &fl,
-                         const LnPrologue &fe, int dirs2, dim3 grid, size_t lds, hipStream_t s) {
+                         const LnPrologue &fe, const GemmArgs &gp, int dirsp, int dirs2, dim3 grid,
+                         size_t lds, hipStream_t s) {
+  const dim3 b(256);
   switch (dirs2) {
-    case 0: hv_launch(k_ffn<DIRS1, 0, LN, LNE>, grid, dim3(256), lds, s, g1, g2, fl, fe); break;
-    case 1: hv_launch(k_ffn<DIRS1, 1, LN, LNE>, grid, dim3(256), lds, s, g1, g2, fl, fe); break;
-    case 2: hv_launch(k_ffn<DIRS1, 2, LN, LNE>, grid, dim3(256), lds, s, g1, g2, fl, fe); break;
-    default: hv_launch(k_ffn<DIRS1, 3, LN, LNE>, grid, dim3(256), lds, s, g1, g2, fl, fe); break;
+    case 0: hv_launch(k_ffn<DIRS1, 0, LN, LNE, PJ>, grid, b, lds, s, g1, g2, fl, fe, gp, dirsp); break;
+    case 1: hv_launch(k_ffn<DIRS1, 1, LN, LNE, PJ>, grid, b, lds, s, g1, g2, fl, fe, gp, dirsp); break;
+    case 2: hv_launch(k_ffn<DIRS1, 2, LN, LNE, PJ>, grid, b, lds, s, g1, g2, fl, fe, gp, dirsp); break;
+    default: hv_launch(k_ffn<DIRS1, 3, LN, LNE, PJ>, grid, b, lds, s, g1, g2, fl, fe, gp, dirsp); break;
   }
 }
 
 // Returns HV_OK when the fused kernel was launched, 1 when the shapes or
 // exponents need the two GEMM launches instead.
 int launch_ffn(const GemmArgs &g1_in, const GemmArgs &g2_in, hipStream_t s,
-               const LnPrologue *ln, const LnPrologue *ln_next) {
+               const LnPrologue *ln, const LnPrologue *ln_next, const GemmArgs *proj) {
   GemmArgs g1 = g1_in, g2 = g2_in;
+  GemmArgs gp = proj ? *proj : GemmArgs{};
+  if (proj) {
+    if (!ln || gp.k != 192 || gp.n != 192 || gp.lda != 192 || gp.ldr != 192 || !gp.a || !gp.b ||
+        !gp.bias || !gp.res || gp.aux || gp.a_rows ||
+        (((uintptr_t)gp.a | (uintptr_t)gp.bias | (uintptr_t)gp.res) & 15))
+      return 1;
+    epilogue_limits_pub(gp, EPI_RES);
+    if (!fast_epilogue(gp, EPI_RES)) return 1;
+  }
   if (g1.k != 192 || g1.n != 768 || g2.k != 768 || g2.n != 192 || g1.lda != 192 ||
       g2.ldc != 192 || g2.ldr != 192 || !g1.bias || !g2.bias || !g2.res || g1.m <= 0)
     return 1;
   if (((uintptr_t)(ln ? nullptr : g1.a) | (uintptr_t)g1.bias | (uintptr_t)g2.bias |
        (uintptr_t)g2.c | (uintptr_t)g2.res | (uintptr_t)g2.aux) & 15)
     return 1;
-  if (ln && (!ln->x || ((uintptr_t)ln->x & 7) || ((uintptr_t)ln->ln.gamma & 7) ||
+  if (ln && ((!proj && (!ln->x || ((uintptr_t)ln->x & 7))) || ((uintptr_t)ln->ln.gamma & 7) ||
              ((uintptr_t)ln->ln.beta & 7)))
     return 1;
   if (ln_next && (!ln_next->ln.out || ((uintptr_t)ln_next->ln.out & 7) ||
@@ -1129,16 +1242,26 @@ int launch_ffn(const GemmArgs &g1_in, const GemmArgs &g2_in, hipStream_t s,
   const dim3 grid((g1.m + kFfnRows - 1) / kFfnRows);
   const int d1 = epilogue_dirs(g1, EPI_GELU) & 1, d2 = epilogue_dirs(g2, EPI_RES);
   const LnPrologue fl = ln ? *ln : LnPrologue{}, fe = ln_next ? *ln_next : LnPrologue{};
-  const int mode = (ln ? 1 : 0) | (ln_next ? 2 : 0);
-  switch (mode | (d1 ? 4 : 0)) {
-    case 0: launch_ffn_d<4, false, false>(g1, g2, fl, fe, d2, grid, lds, s); break;
-    case 1: launch_ffn_d<4, true, false>(g1, g2, fl, fe, d2, grid, lds, s); break;
-    case 2: launch_ffn_d<4, false, true>(g1, g2, fl, fe, d2, grid, lds, s); break;
-    case 3: launch_ffn_d<4, true, true>(g1, g2, fl, fe, d2, grid, lds, s); break;
-    case 4: launch_ffn_d<5, false, false>(g1, g2, fl, fe, d2, grid, lds, s); break;
-    case 5: launch_ffn_d<5, true, false>(g1, g2, fl, fe, d2, grid, lds, s); break;
-    case 6: launch_ffn_d<5, false, true>(g1, g2, fl, fe, d2, grid, lds, s); break;
-    default: launch_ffn_d<5, true, true>(g1, g2, fl, fe, d2, grid, lds, s); break;
+  const int dp = proj ? epilogue_dirs(gp, EPI_RES) : 0;
+  const int mode = (ln ? 1 : 0) | (ln_next ? 2 : 0) | (d1 ? 4 : 0);
+  if (proj) {
+    switch (mode) {
+      case 1: launch_ffn_d<4, true, false, true>(g1, g2, fl, fe, gp, dp, d2, grid, lds, s); break;
+      case 3: launch_ffn_d<4, true, true, true>(g1, g2, fl, fe, gp, dp, d2, grid, lds, s); break;
+      case 5: launch_ffn_d<5, true, false, true>(g1, g2, fl, fe, gp, dp, d2, grid, lds, s); break;
+      default: launch_ffn_d<5, true, true, true>(g1, g2, fl, fe, gp, dp, d2, grid, lds, s); break;
+    }
+    return check_hip(hipGetLastError(), "k_ffn launch");
+  }
+  switch (mode) {
+    case 0: launch_ffn_d<4, false, false, false>(g1, g2, fl, fe, gp, 0, d2, grid, lds, s); break;
+    case 1: launch_ffn_d<4, true, false, false>(g1, g2, fl, fe, gp, 0, d2, grid, lds, s); break;
+    case 2: launch_ffn_d<4, false, true, false>(g1, g2, fl, fe, gp, 0, d2, grid, lds, s); break;
+    case 3: launch_ffn_d<4, true, true, false>(g1, g2, fl, fe, gp, 0, d2, grid, lds, s); break;
+    case 4: launch_ffn_d<5, false, false, false>(g1, g2, fl, fe, gp, 0, d2, grid, lds, s); break;
+    case 5: launch_ffn_d<5, true, false, false>(g1, g2, fl, fe, gp, 0, d2, grid, lds, s); break;
+    case 6: launch_ffn_d<5, false, true, false>(g1, g2, fl, fe, gp, 0, d2, grid, lds, s); break;
+    default: launch_ffn_d<5, true, true, false>(g1, g2, fl, fe, gp, 0, d2, grid, lds, s); break;
   }
   return check_hip(hipGetLastError(), "k_ffn launch");
 }

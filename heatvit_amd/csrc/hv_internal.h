@@ -78,14 +78,20 @@ int launch_gemm(const GemmArgs &g, int a_mode, int epilogue, hipStream_t s);
 // ln32_setup, whose output pointer is unused), g1.a unused.  ln_next
 // (optional): a LayerNorm of the output rows (the next block's LayerNorm 1)
 // runs at the kernel's end and writes ln_next->ln.out (row stride 192;
-// ln_next->x unused).  Negative variances reach the lw of each.
+// ln_next->x unused).  Negative variances reach the lw of each.  proj
+// (optional, with ln): the residual GEMM in front of the LayerNorm
+// (attention projection: a = ctx rows, res = x, K = N = 192) runs in the
+// same kernel and its output rows y feed the LayerNorm and g2's residual
+// on the CU: ln->x and g2.res unused, proj->c not written, proj->aux must
+// be NULL.
 struct LnPrologue {
   const int8_t *x;
   Ln32 ln;
   LnWarn lw;
 };
 int launch_ffn(const GemmArgs &g1, const GemmArgs &g2, hipStream_t s,
-               const LnPrologue *ln = nullptr, const LnPrologue *ln_next = nullptr);
+               const LnPrologue *ln = nullptr, const LnPrologue *ln_next = nullptr,
+               const GemmArgs *proj = nullptr);
 // Fills acc_lim / narrow_ok / da / db / os of the int32 epilogue paths.
 void epilogue_limits_pub(GemmArgs &g, int epilogue);
 

@@ -113,28 +113,32 @@ def _block_launches(xs, bp, checkpoints):
 
 
 def test_block_ln2_inside_fused_ffn_vs_oracle(oracle):
-    """Without checkpoints LayerNorm 2 runs inside the fused FFN kernel (its
-    rows pass through LDS): one LayerNorm launch per block (LN1) and one FFN
-    launch.  With checkpoints LN2 has its own launch, which writes the ln2
-    checkpoint, and FFN1 / FFN2 run as two GEMMs (the hidden checkpoint).
-    Both match the oracle over ragged images (partial 64-row blocks)."""
+    """Without checkpoints the attention projection and LayerNorm 2 run
+    inside the fused FFN kernel (y and the LN2 rows pass through LDS): one
+    LayerNorm launch per block (LN1), one FFN launch and no projection
+    launch.  With checkpoints the projection and LN2 have launches of their
+    own, which write the y and ln2 checkpoints, and FFN1 / FFN2 run as two
+    GEMMs (the hidden checkpoint).  Both match the oracle over ragged images
+    (partial 64-row blocks)."""
     _, bp = synth.block_workload()
     xs = _ragged_batch(np.random.default_rng(21))
     zs, n = _block_launches(xs, bp, False)
-    assert n["layernorm"] == 1 and n["ffn"] == 1, n
+    assert n["layernorm"] == 1 and n["ffn"] == 1 and n["gemm_proj"] == 0, n
     assert n["gemm_ffn1"] == 0 and n["gemm_ffn2"] == 0, n
     (zs_ck, cks), n_ck = _block_launches(xs, bp, True)
-    assert n_ck["layernorm"] == 2 and n_ck["ffn"] == 0, n_ck
+    assert n_ck["layernorm"] == 2 and n_ck["ffn"] == 0 and n_ck["gemm_proj"] == 1, n_ck
     for i, x in enumerate(xs):
         z, ck = oracle.transformer_block(x, bp, checkpoints=True)
         assert np.array_equal(zs[i], z), (i, len(x))
         assert np.array_equal(zs_ck[i], z), (i, len(x))
         assert np.array_equal(cks[i]["ln2"], ck["ln2"]), (i, len(x))
+        assert np.array_equal(cks[i]["y"], ck["y"]), (i, len(x))
 
 
 def test_block_wide_biases_all_gemms_vs_oracle(oracle):
     """Biases beyond the int32 epilogue bounds in all four GEMMs send their
-    tiles to the exact 64-bit forms."""
+    tiles to the exact 64-bit forms (the projection's inside the fused FFN
+    kernel, as the block runs without checkpoints)."""
     import dataclasses
     from heatvit_amd.transformer import transformer_block_batch
     _, bp = synth.block_workload()
@@ -361,7 +365,43 @@ def test_model_layernorm_fallbacks_vs_oracle(oracle):
         L.hv_profile_enable(0)
     n = dict(zip(_lib.PROF_CLASSES, n.tolist()))
     # blocks 1, 4, 7, 10 and the final one; block 2's LN1, block 5's LN2, block 6's LN1
-    assert n["layernorm"] == 5 + 3 and n["ffn"] == 12, n
+    # block 5's projection runs as its own launch too (it feeds LayerNorm 2)
+    assert n["layernorm"] == 5 + 3 and n["ffn"] == 12 and n["gemm_proj"] == 1, n
+    logits, counts, status, warnings = oracle.model_infer_batch(imgs, p)
+    assert not status.any()
+    assert np.array_equal(r.logits, logits)
+    assert np.array_equal(r.token_counts, counts)
+    assert np.array_equal(r.warnings, warnings)
+
+
+def test_model_projection_outside_ffn_kernel_vs_oracle(oracle):
+    """A block whose residual align-add after the attention projection needs
+    the exact epilogue (the projection's output 22 binary places below x,
+    beyond the int32 form's 21) runs the projection as a launch of its own
+    and its FFN kernel reads y from memory, still with LayerNorm 2 inside;
+    the other blocks keep the projection in their FFN kernels.  Logits,
+    token counts and warnings match the oracle."""
+    import dataclasses
+    from heatvit_amd import _lib
+    from heatvit_amd.model import HeatViTModel
+    imgs, params = synth.pruned_workload(6)
+    blocks = list(params.blocks)
+    m7 = blocks[7].mhsa
+    blocks[7] = dataclasses.replace(
+        blocks[7], mhsa=dataclasses.replace(m7, msa_out_scale_exp=m7.x_scale_exp - 22))
+    p = dataclasses.replace(params, blocks=tuple(blocks))
+    L = _lib.lib()
+    L.hv_profile_enable(1)
+    try:
+        r = HeatViTModel().infer_batch(imgs, p)
+        ms = np.zeros(len(_lib.PROF_CLASSES), np.float32)
+        n = np.zeros(len(_lib.PROF_CLASSES), np.int32)
+        _lib.check(L.hv_profile_read(ms.ctypes.data, n.ctypes.data, len(ms)), "profile")
+    finally:
+        L.hv_profile_enable(0)
+    n = dict(zip(_lib.PROF_CLASSES, n.tolist()))
+    assert n["gemm_proj"] == 1 and n["ffn"] == 12, n
+    assert n["layernorm"] == 2 + len(params.selectors), n
     logits, counts, status, warnings = oracle.model_infer_batch(imgs, p)
     assert not status.any()
     assert np.array_equal(r.logits, logits)
