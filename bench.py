@@ -60,6 +60,8 @@ def class_work(counts, params, batch):
     figures: QKV 2*192*576, proj 2*192*192, FFN1 2*192*768, FFN2 2*768*192
     ops per token; attention 2*384*N^2 per image; patch 2*768*192 per
     patch; head 2*192*1000 per image; selector 2*13938 per candidate.  The
+    attention kernel computes its head's Q, K and V itself (the LayerNorm 1
+    rows in, the context rows out: 384 B per token, with the QKV ops).  The
     fused FFN kernel runs the attention projection and its residual (the
     context rows and x in once; y stays on the CU), LayerNorm 2, FFN1,
     FFN2 and writes the block output and, when the next block follows
@@ -86,7 +88,9 @@ def class_work(counts, params, batch):
         ops["gemm_proj"] += 2 * 192 * 192 * t
         ops["gemm_ffn1"] += 2 * 192 * 768 * t
         ops["gemm_ffn2"] += 2 * 768 * 192 * t
-        ops["attention"] += int((2 * 384 * n * n).sum())
+        # attention with each head's Q, K, V from its own GEMM: LayerNorm 1
+        # rows in, context rows out
+        ops["attention"] += 2 * 192 * 576 * t + int((2 * 384 * n * n).sum())
         hbm["gemm_qkv"] += (192 + 576) * t
         hbm["gemm_proj"] += (192 + 192 + 192) * t
         hbm["gemm_ffn1"] += (192 + 768) * t
@@ -95,7 +99,7 @@ def class_work(counts, params, batch):
         # LayerNorm 1) out
         ops["ffn"] += (2 * 192 * 192 + 2 * 2 * 192 * 768) * t
         hbm["ffn"] += (192 + 192 + 192 + (192 if chained else 0)) * t
-        hbm["attention"] += (576 + 192) * t
+        hbm["attention"] += (192 + 192) * t
         if stage_first:
             hbm["layernorm"] += 2 * 192 * t
     for s in range(len(params.selectors)):
@@ -226,7 +230,8 @@ def config_lines(args, L):
     n = 197
     ops = {"gemm_qkv": 2 * 192 * 576 * n, "gemm_proj": 2 * 192 * 192 * n,
            "gemm_ffn1": 2 * 192 * 768 * n, "gemm_ffn2": 2 * 768 * 192 * n,
-           "ffn": (2 * 192 * 192 + 2 * 2 * 192 * 768) * n, "attention": 2 * 384 * n * n}
+           "ffn": (2 * 192 * 192 + 2 * 2 * 192 * 768) * n,
+           "attention": 2 * 192 * 576 * n + 2 * 384 * n * n}
     hbm = {"layernorm": 2 * 2 * 192 * n}
     out["c0_block_b1"] = _summary(_class_ms(L, block, args.steps), ops, hbm, 1, ms,
                                   bool(np.array_equal(z.cpu().numpy(), want)), cpu_s)

@@ -221,13 +221,23 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   g.a = ln1; g.b = p.wqkv_p; g.bias = p.bqkv; g.c = qkv; g.m_dev = rows_dev;
   g.m = max_rows; g.n = 576; g.k = 192; g.lda = 192; g.ldc = 576;
   g.shift_a = p.qkv_out_exp - (p.ln1_out_exp + p.wqkv_exp);
-  {
+  // Without checkpoints the attention kernel computes each head's Q, K and
+  // V itself when their requant takes the int32 form: qkv never reaches
+  // memory.
+  epilogue_limits_pub(g, HV_EPI_I8);
+  const bool fuse_qkv = !ck && g.narrow_ok && g.shift_a >= -30 && g.shift_a <= 30 &&
+                        !(((uintptr_t)ln1 | (uintptr_t)p.wqkv_p | (uintptr_t)p.bqkv) & 15);
+  if (!fuse_qkv) {
     ProfScope ps(HV_PROF_GEMM_QKV, s);
     rc = launch_gemm(g, A_ROWS, HV_EPI_I8, s);
+    if (rc) return rc;
   }
-  if (rc) return rc;
 
   AttnArgs a{};
+  if (fuse_qkv) {
+    a.ln1 = ln1; a.wqkv = p.wqkv_p; a.bqkv = p.bqkv;
+    a.qkv_shift = g.shift_a; a.qkv_acc_lim = g.acc_lim;
+  }
   a.qkv = qkv; a.offsets = offsets; a.ctx = ctx; a.batch = batch; a.rows_cap = max_rows;
   a.score = ck ? ck->score : nullptr;
   a.prob = ck ? ck->prob : nullptr;

@@ -148,6 +148,15 @@ struct AttnArgs {
   int q16_mode, q16_s, q16_rnd;  // int32 fast path for the score -> Q8.16 conversion
   int ctx_fast, ctx_rnd;         // int32 context requant (shift in [1, 30])
   int rows_cap;                  // rows of qkv / ctx; images outside are skipped
+  // Fused QKV (ln1 non-NULL): each head's Q, K and V come from the kernel's
+  // own GEMM over the LayerNorm 1 rows (row stride 192, the same row
+  // offsets), qkv unused.  wqkv mfma32-packed [192][576]; the int8 requant
+  // by qkv_shift in [-30, 30] (left: qkv_shift <= 0) takes the int32 form
+  // for columns with |bias| <= qkv_acc_lim, the exact one otherwise.
+  const int8_t *ln1;
+  const int8_t *wqkv;
+  const int32_t *bqkv;
+  int qkv_shift, qkv_acc_lim;
 };
 int launch_attention(const AttnArgs &a, hipStream_t s);
 

@@ -330,13 +330,107 @@ __device__ __noinline__ int attn_ctx_general(int v, int ctx_shift) {
   return (int)requant_shift(v, ctx_shift, 8);
 }
 
+// int8 requant of one fused-QKV tile (gemm_writeback, gemm.py:117-139):
+// lane l's 16 outputs, the int32 form when every lane's biases allow it.
+template <bool LA>
+__device__ __forceinline__ v4i qkv_epi(const AttnArgs &g, const v16i &acc, const v4i (&b4)[4],
+                                       const Rq &rq) {
+  int bmax = b4[0][0], bmin = bmax;
+#pragma unroll
+  for (int j = 1; j < 16; ++j) {
+    bmax = max(bmax, b4[j >> 2][j & 3]);
+    bmin = min(bmin, b4[j >> 2][j & 3]);
+  }
+  int o[16];
+  if (__all(bmax <= g.qkv_acc_lim && bmin >= -g.qkv_acc_lim)) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) o[j] = rq_dir_nowrap<LA>(acc[j] + b4[j >> 2][j & 3], rq);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      o[j] = (int)requant_shift((i64)acc[j] + b4[j >> 2][j & 3], g.qkv_shift, 8);
+  }
+  v4i w;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    w[q] = (int)((unsigned)(o[4 * q] & 0xFF) | ((unsigned)(o[4 * q + 1] & 0xFF) << 8) |
+                 ((unsigned)(o[4 * q + 2] & 0xFF) << 16) | ((unsigned)o[4 * q + 3] << 24));
+  return w;
+}
+
+// Q, K and V of head h over the image's N rows (the fused QKV GEMM and its
+// requant, transformer.py:211-227, split per head as qkv_unpack does,
+// layout.py:92-131) into LDS: Q and K as rows (Qs, Ks), V transposed in
+// the P V key order (Vt).  Units of one row tile of 32 and one of Q, K, V
+// (its two column tiles of 32), unit u = p * nrt + rt on wavefront u % 4,
+// which loads the weight fragments once per p.  Rows from N up
+// to the 64-key chunk end are stored as zero (the padded keys); Q and K
+// rows past the key tiles are not stored.
+template <bool LA>
+__device__ __forceinline__ void qkv_head(const AttnArgs &g, int8_t *Qs, int8_t *Ks, int8_t *Vt,
+                                         int row0, int N, int h, int wave, int lane) {
+  const int l32 = lane & 31, hh = lane >> 5;
+  const int nrt = 2 * ((N + 63) >> 6), rows_k = ((N + 15) >> 4) * 16;
+  const Rq rq = rq_setup(g.qkv_shift, -128, 127);
+#pragma unroll 1
+  for (int p = 0; p < 3; ++p) {
+    // this wavefront's units of p: u = p * nrt + rt with u % 4 == wave
+    const int rt0 = (wave - p * nrt) & 3;
+    if (rt0 >= nrt) continue;
+    v4i w[2][6];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int ctg = p * 6 + h * 2 + c;  // 32-column tile of the 576
+#pragma unroll
+      for (int kt = 0; kt < 6; ++kt)
+        w[c][kt] = *reinterpret_cast<const v4i *>(g.wqkv + (size_t)(ctg * 6 + kt) * 1024 +
+                                                  lane * 16);
+    }
+#pragma unroll 1
+  for (int rt = rt0; rt < nrt; rt += 4) {
+    const int r = rt * 32 + l32;
+    const int8_t *ap = g.ln1 + (size_t)(row0 + min(r, N - 1)) * 192 + 16 * hh;
+    v4i a[6];
+#pragma unroll
+    for (int kt = 0; kt < 6; ++kt) a[kt] = *reinterpret_cast<const v4i *>(ap + kt * 32);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int ctg = p * 6 + h * 2 + c;
+      v4i b4[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        b4[q] = *reinterpret_cast<const v4i *>(g.bqkv + ctg * 32 + 16 * hh + 4 * q);
+      v16i acc = v16i{0};
+#pragma unroll
+      for (int kt = 0; kt < 6; ++kt)
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[c][kt], a[kt], acc, 0, 0, 0);
+      v4i o = qkv_epi<LA>(g, acc, b4, rq);
+      if (r >= N) o = v4i{0};
+      const int ch = c * 32 + 16 * hh;  // channel within the head
+      if (p == 0) {
+        if (r < rows_k) *reinterpret_cast<v4i *>(&Qs[r * kKStride + ch]) = o;
+      } else if (p == 1) {
+        if (r < rows_k) *reinterpret_cast<v4i *>(&Ks[r * kKStride + ch]) = o;
+      } else {
+        const int pos = vt_pos(r);
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          Vt[(ch + i) * kVStride + pos] = (int8_t)(o[i >> 2] >> (8 * (i & 3)));
+      }
+      __builtin_amdgcn_sched_barrier(0);  // one column tile's registers at a time
+    }
+  }
+  }
+}
+
 // The query tiles of one wavefront for an image of NT key tiles (N in
 // (16 (NT - 1), 16 NT]): straight-line code per tile count, so the score
 // MFMAs issue back to back and only the last tile masks padded keys.
-template <int MODE, bool CKPT, int NT>
+// FQ: the queries come from Qs in LDS (fused QKV), else from qkv.
+template <int MODE, bool CKPT, int NT, bool FQ>
 __device__ __forceinline__ void attn_tiles(const AttnArgs &g, const int8_t *Ks, const int8_t *Vt,
-                                           const int *vsum, const int8_t *qkv, int b, int h, int N,
-                                           int row0, int wave, int lane) {
+                                           const int *vsum, const int8_t *qkv, const int8_t *Qs,
+                                           int b, int h, int N, int row0, int wave, int lane) {
   constexpr int NC = (NT + 3) / 4;  // PV chunks of 64 keys
   const int ql = lane & 15, grp = lane >> 4;
   const int kvalid = N - 16 * (NT - 1) - 4 * grp;  // valid keys i < kvalid in the last tile
@@ -346,7 +440,9 @@ __device__ __forceinline__ void attn_tiles(const AttnArgs &g, const int8_t *Ks, 
   for (int qt = (wave + blockIdx.x) & 3; qt < NT; qt += 4) {
     const int q = qt * 16 + ql;  // this lane's query
     v4i qb = v4i{0};
-    if (q < N) qb = *reinterpret_cast<const v4i *>(qkv + (size_t)q * 576 + h * 64 + grp * 16);
+    if (q < N)
+      qb = FQ ? *reinterpret_cast<const v4i *>(&Qs[q * kKStride + grp * 16])
+              : *reinterpret_cast<const v4i *>(qkv + (size_t)q * 576 + h * 64 + grp * 16);
     // S^T tiles: lane holds keys 16 kt + 4 grp + i of query ql.
     v4i st[NT];
 #pragma unroll
@@ -436,12 +532,14 @@ __device__ __forceinline__ void attn_tiles(const AttnArgs &g, const int8_t *Ks, 
 }
 
 // At most 168 VGPRs (three workgroups per CU): the 768 items of a 256-image
-// batch then run in one round.
-template <int MODE, bool CKPT>
+// batch then run in one round.  FQ: fused QKV (qkv_head), FQL its requant
+// shifting left.
+template <int MODE, bool CKPT, bool FQ, bool FQL>
 __global__ __launch_bounds__(256, 3) void k_attention(AttnArgs g) {
   __shared__ __attribute__((aligned(16))) int8_t Ks[kMaxKeys * kKStride];
   __shared__ __attribute__((aligned(16))) int8_t Vt[64 * kVStride];
   __shared__ __attribute__((aligned(16))) int vsum[64];  // 128 * sum_k V[k][d]
+  __shared__ __attribute__((aligned(16))) int8_t Qs[FQ ? kMaxKeys * kKStride : 16];
 
   // The grid is a multiple of 8 and workgroups go round-robin over the 8
   // XCDs, so XCD x runs logical items [x*T8, (x+1)*T8): the three heads of
@@ -458,8 +556,11 @@ __global__ __launch_bounds__(256, 3) void k_attention(AttnArgs g) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n16 = (N + 15) >> 4;  // key / query tiles
   const int n64 = (N + 63) >> 6;  // PV chunks of 64 keys
-  const int8_t *qkv = g.qkv + (size_t)row0 * 576;
+  const int8_t *qkv = FQ ? nullptr : g.qkv + (size_t)row0 * 576;
 
+  if constexpr (FQ) {
+    qkv_head<FQL>(g, Qs, Ks, Vt, row0, N, h, wave, lane);
+  } else {
   for (int i = tid; i < n16 * 16 * 4; i += 256) {
     const int r = i >> 2, c = (i & 3) * 16;
     v4i v = v4i{0};
@@ -487,6 +588,7 @@ __global__ __launch_bounds__(256, 3) void k_attention(AttnArgs g) {
         *reinterpret_cast<unsigned *>(&Vt[(dg * 16 + dq * 4 + e) * kVStride + pos]) = col;
       }
   }
+  }
   __syncthreads();
   // The probabilities enter P V as the signed bytes P - 128: P V =
   // (P - 128) V + 128 sum_k V[k], one MFMA per tile instead of two.  The
@@ -501,7 +603,8 @@ __global__ __launch_bounds__(256, 3) void k_attention(AttnArgs g) {
 
   switch (n16) {
 #define HV_ATTN_CASE(n) \
-    case n: attn_tiles<MODE, CKPT, n>(g, Ks, Vt, vsum, qkv, b, h, N, row0, wave, lane); break;
+    case n: attn_tiles<MODE, CKPT, n, FQ>(g, Ks, Vt, vsum, qkv, Qs, b, h, N, row0, wave, lane); \
+      break;
     HV_ATTN_CASE(1) HV_ATTN_CASE(2) HV_ATTN_CASE(3) HV_ATTN_CASE(4) HV_ATTN_CASE(5)
     HV_ATTN_CASE(6) HV_ATTN_CASE(7) HV_ATTN_CASE(8) HV_ATTN_CASE(9) HV_ATTN_CASE(10)
     HV_ATTN_CASE(11) HV_ATTN_CASE(12) HV_ATTN_CASE(13)
@@ -536,12 +639,29 @@ int launch_attention(const AttnArgs &a_in, hipStream_t s) {
   a.ctx_rnd = a.ctx_fast ? 1 << (a.ctx_shift - 1) : 0;
   const bool ck = a.score || a.prob;
   const dim3 grid((a.batch * 3 + 7) / 8 * 8), block(256);
-  if (a.q16_mode == 0 && !ck) hv_launch((k_attention<0, false>), grid, block, 0, s, a);
-  else if (a.q16_mode == 0) hv_launch((k_attention<0, true>), grid, block, 0, s, a);
-  else if (a.q16_mode == 1 && !ck) hv_launch((k_attention<1, false>), grid, block, 0, s, a);
-  else if (a.q16_mode == 1) hv_launch((k_attention<1, true>), grid, block, 0, s, a);
-  else if (!ck) hv_launch((k_attention<2, false>), grid, block, 0, s, a);
-  else hv_launch((k_attention<2, true>), grid, block, 0, s, a);
+  if (a.ln1) {
+    // fused QKV: no checkpoints, the int32-form shift range
+    if (ck || !a.wqkv || !a.bqkv || a.qkv_shift < -30 || a.qkv_shift > 30 ||
+        (((uintptr_t)a.ln1 | (uintptr_t)a.wqkv | (uintptr_t)a.bqkv) & 15))
+      return fail(HV_EVALUE, HV_ERR_DIMENSION, "attention: fused QKV arguments");
+    const bool left = a.qkv_shift <= 0;
+    auto go = [&](auto k) { hv_launch(k, grid, block, 0, s, a); };
+    switch (a.q16_mode * 2 + (left ? 1 : 0)) {
+      case 0: go(k_attention<0, false, true, false>); break;
+      case 1: go(k_attention<0, false, true, true>); break;
+      case 2: go(k_attention<1, false, true, false>); break;
+      case 3: go(k_attention<1, false, true, true>); break;
+      case 4: go(k_attention<2, false, true, false>); break;
+      default: go(k_attention<2, false, true, true>); break;
+    }
+    return check_hip(hipGetLastError(), "k_attention launch");
+  }
+  if (a.q16_mode == 0 && !ck) hv_launch((k_attention<0, false, false, false>), grid, block, 0, s, a);
+  else if (a.q16_mode == 0) hv_launch((k_attention<0, true, false, false>), grid, block, 0, s, a);
+  else if (a.q16_mode == 1 && !ck) hv_launch((k_attention<1, false, false, false>), grid, block, 0, s, a);
+  else if (a.q16_mode == 1) hv_launch((k_attention<1, true, false, false>), grid, block, 0, s, a);
+  else if (!ck) hv_launch((k_attention<2, false, false, false>), grid, block, 0, s, a);
+  else hv_launch((k_attention<2, true, false, false>), grid, block, 0, s, a);
   return check_hip(hipGetLastError(), "k_attention launch");
 }
 

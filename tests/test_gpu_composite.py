@@ -125,14 +125,17 @@ def test_block_ln2_inside_fused_ffn_vs_oracle(oracle):
     zs, n = _block_launches(xs, bp, False)
     assert n["layernorm"] == 1 and n["ffn"] == 1 and n["gemm_proj"] == 0, n
     assert n["gemm_ffn1"] == 0 and n["gemm_ffn2"] == 0, n
+    assert n["gemm_qkv"] == 0 and n["attention"] == 1, n  # QKV inside the attention kernel
     (zs_ck, cks), n_ck = _block_launches(xs, bp, True)
     assert n_ck["layernorm"] == 2 and n_ck["ffn"] == 0 and n_ck["gemm_proj"] == 1, n_ck
+    assert n_ck["gemm_qkv"] == 1, n_ck
     for i, x in enumerate(xs):
         z, ck = oracle.transformer_block(x, bp, checkpoints=True)
         assert np.array_equal(zs[i], z), (i, len(x))
         assert np.array_equal(zs_ck[i], z), (i, len(x))
         assert np.array_equal(cks[i]["ln2"], ck["ln2"]), (i, len(x))
         assert np.array_equal(cks[i]["y"], ck["y"]), (i, len(x))
+        assert np.array_equal(cks[i]["fused_qkv"], ck["fused_qkv"]), (i, len(x))
 
 
 def test_block_wide_biases_all_gemms_vs_oracle(oracle):
@@ -374,21 +377,26 @@ def test_model_layernorm_fallbacks_vs_oracle(oracle):
     assert np.array_equal(r.warnings, warnings)
 
 
-def test_model_projection_outside_ffn_kernel_vs_oracle(oracle):
+def test_model_projection_and_qkv_outside_fused_kernels_vs_oracle(oracle):
     """A block whose residual align-add after the attention projection needs
     the exact epilogue (the projection's output 22 binary places below x,
     beyond the int32 form's 21) runs the projection as a launch of its own
     and its FFN kernel reads y from memory, still with LayerNorm 2 inside;
-    the other blocks keep the projection in their FFN kernels.  Logits,
-    token counts and warnings match the oracle."""
+    a block whose QKV requant shifts left by 10 (no int32 bias bound left)
+    runs the QKV GEMM as a launch of its own and its attention kernel reads
+    Q, K, V from memory.  The other blocks keep the projection in their FFN
+    kernels and the QKV GEMM in their attention kernels.  Logits, token
+    counts and warnings match the oracle."""
     import dataclasses
     from heatvit_amd import _lib
     from heatvit_amd.model import HeatViTModel
     imgs, params = synth.pruned_workload(6)
     blocks = list(params.blocks)
-    m7 = blocks[7].mhsa
+    m7, m9 = blocks[7].mhsa, blocks[9].mhsa
     blocks[7] = dataclasses.replace(
         blocks[7], mhsa=dataclasses.replace(m7, msa_out_scale_exp=m7.x_scale_exp - 22))
+    blocks[9] = dataclasses.replace(blocks[9], mhsa=dataclasses.replace(
+        m9, qkv_out_scale_exp=m9.ln1_out_scale_exp + m9.wqkv_scale_exp - 10))
     p = dataclasses.replace(params, blocks=tuple(blocks))
     L = _lib.lib()
     L.hv_profile_enable(1)
@@ -401,6 +409,7 @@ def test_model_projection_outside_ffn_kernel_vs_oracle(oracle):
         L.hv_profile_enable(0)
     n = dict(zip(_lib.PROF_CLASSES, n.tolist()))
     assert n["gemm_proj"] == 1 and n["ffn"] == 12, n
+    assert n["gemm_qkv"] == 1 and n["attention"] == 12, n
     assert n["layernorm"] == 2 + len(params.selectors), n
     logits, counts, status, warnings = oracle.model_infer_batch(imgs, p)
     assert not status.any()
