@@ -189,6 +189,9 @@ struct LnChain {
   bool *next_done;
 };
 
+// Images per batch from which the attention kernel runs the QKV GEMM.
+static constexpr int kFusedQkvMinBatch = 32;
+
 // transformer_block (transformer.py:401-431) on rows [0, offsets[batch]):
 // LN1, QKV, attention, proj + residual, LN2, FFN1 + GELU, FFN2 + residual.
 // warnings (optional, [B]) receive the LayerNorms' negative-variance bit.
@@ -223,9 +226,12 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   g.shift_a = p.qkv_out_exp - (p.ln1_out_exp + p.wqkv_exp);
   // Without checkpoints the attention kernel computes each head's Q, K and
   // V itself when their requant takes the int32 form: qkv never reaches
-  // memory.
+  // memory.  Small batches keep the separate GEMM: with a few workgroups
+  // per head the in-kernel GEMM would run on a few CUs in series with the
+  // attention (one image: 0.63 ms → 0.67 ms per forward).
   epilogue_limits_pub(g, HV_EPI_I8);
-  const bool fuse_qkv = !ck && g.narrow_ok && g.shift_a >= -30 && g.shift_a <= 30 &&
+  const bool fuse_qkv = !ck && batch >= kFusedQkvMinBatch && g.narrow_ok && g.shift_a >= -30 &&
+                        g.shift_a <= 30 &&
                         !(((uintptr_t)ln1 | (uintptr_t)p.wqkv_p | (uintptr_t)p.bqkv) & 15);
   if (!fuse_qkv) {
     ProfScope ps(HV_PROF_GEMM_QKV, s);

@@ -73,8 +73,9 @@ def test_fused_ffn_wide_biases_and_ragged_rows_vs_oracle(oracle, wide):
 
 
 # Ragged token counts of a pruned stage: partial 32-row tiles and 64-row
-# FFN blocks, images of one and two key tiles, many small images.
-RAGGED_LENS = [1, 2, 16, 17, 31, 32, 33, 63, 64, 65, 100, 128, 129, 150, 197] + [3] * 16
+# FFN blocks, images of one and two key tiles, many small images; 32 images,
+# so the attention kernel runs the QKV GEMM.
+RAGGED_LENS = [1, 2, 16, 17, 31, 32, 33, 48, 63, 64, 65, 100, 128, 129, 150, 197] + [3] * 16
 
 
 def _ragged_batch(rng, lens=RAGGED_LENS):
@@ -113,19 +114,24 @@ def _block_launches(xs, bp, checkpoints):
 
 
 def test_block_ln2_inside_fused_ffn_vs_oracle(oracle):
-    """Without checkpoints the attention projection and LayerNorm 2 run
-    inside the fused FFN kernel (y and the LN2 rows pass through LDS): one
-    LayerNorm launch per block (LN1), one FFN launch and no projection
-    launch.  With checkpoints the projection and LN2 have launches of their
-    own, which write the y and ln2 checkpoints, and FFN1 / FFN2 run as two
-    GEMMs (the hidden checkpoint).  Both match the oracle over ragged images
-    (partial 64-row blocks)."""
+    """Without checkpoints the QKV GEMM runs inside the attention kernel (32
+    images or more) and the attention projection and LayerNorm 2 inside the
+    fused FFN kernel (y and the LN2 rows pass through LDS): one LayerNorm
+    launch per block (LN1), one attention and one FFN launch.  A batch of 8
+    keeps the QKV launch.  With checkpoints QKV, the projection and LN2 have
+    launches of their own, which write the fused_qkv, y and ln2 checkpoints,
+    and FFN1 / FFN2 run as two GEMMs (the hidden checkpoint).  All match the
+    oracle over ragged images (partial 32-row tiles and 64-row blocks)."""
     _, bp = synth.block_workload()
     xs = _ragged_batch(np.random.default_rng(21))
     zs, n = _block_launches(xs, bp, False)
     assert n["layernorm"] == 1 and n["ffn"] == 1 and n["gemm_proj"] == 0, n
     assert n["gemm_ffn1"] == 0 and n["gemm_ffn2"] == 0, n
-    assert n["gemm_qkv"] == 0 and n["attention"] == 1, n  # QKV inside the attention kernel
+    assert n["gemm_qkv"] == 0 and n["attention"] == 1, n
+    zs8, n8 = _block_launches(xs[8:16], bp, False)
+    assert n8["gemm_qkv"] == 1 and n8["attention"] == 1 and n8["ffn"] == 1, n8
+    for i, x in enumerate(xs[8:16]):
+        assert np.array_equal(zs8[i], zs[8 + i]), i
     (zs_ck, cks), n_ck = _block_launches(xs, bp, True)
     assert n_ck["layernorm"] == 2 and n_ck["ffn"] == 0 and n_ck["gemm_proj"] == 1, n_ck
     assert n_ck["gemm_qkv"] == 1, n_ck
@@ -390,7 +396,7 @@ def test_model_projection_and_qkv_outside_fused_kernels_vs_oracle(oracle):
     import dataclasses
     from heatvit_amd import _lib
     from heatvit_amd.model import HeatViTModel
-    imgs, params = synth.pruned_workload(6)
+    imgs, params = synth.pruned_workload(32)
     blocks = list(params.blocks)
     m7, m9 = blocks[7].mhsa, blocks[9].mhsa
     blocks[7] = dataclasses.replace(
