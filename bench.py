@@ -65,10 +65,10 @@ def class_work(counts, params, batch):
     fused FFN kernel runs the attention projection and its residual (the
     context rows and x in once; y stays on the CU), LayerNorm 2, FFN1,
     FFN2 and writes the block output and, when the next block follows
-    without a selector in between, that block's LayerNorm 1: 576 B per
-    token plus 192 B for those blocks; the LayerNorm class is then each
-    stage's first LayerNorm 1 and the final one.  Only the classes a run
-    launches are reported."""
+    without a selector in between, that block's LayerNorm 1 (block 12: the
+    final LayerNorm): 576 B per token plus 192 B for those blocks; the
+    LayerNorm class is then each stage's first LayerNorm 1.  Only the
+    classes a run launches are reported."""
     counts = np.asarray(counts, np.int64)
     stage_of_block = []
     s = 0
@@ -82,7 +82,7 @@ def class_work(counts, params, batch):
     for b, st in enumerate(stage_of_block, start=1):
         n = counts[:, st]
         t = int(n.sum())
-        chained = b < 12 and (b + 1) not in params.selector_blocks
+        chained = b == 12 or (b + 1) not in params.selector_blocks
         stage_first = b == 1 or b in params.selector_blocks
         ops["gemm_qkv"] += 2 * 192 * 576 * t
         ops["gemm_proj"] += 2 * 192 * 192 * t
@@ -109,7 +109,6 @@ def class_work(counts, params, batch):
     ops["patch"] = 2 * 768 * 192 * 196 * batch
     hbm["patch"] = 150528 * batch + 197 * 192 * batch
     ops["head"] = 2 * 192 * 1000 * batch
-    hbm["layernorm"] += 2 * 192 * int(counts[:, len(params.selectors)].sum())
     hbm["head"] = 192 * batch + 4000 * batch
     return ops, hbm
 

@@ -668,6 +668,16 @@ static int model_forward(const hv_model_dev *p, const void *images, bool float_i
 
   int sel = 0;
   const int8_t *ln1_ready = nullptr;  // this block's LayerNorm 1, from the previous FFN
+  // The final LayerNorm (model.py:102-106) as the "next LayerNorm" of block
+  // 12's FFN kernel: the same fields in the layout the chain reads.
+  hv_block_dev fin{};
+  fin.ln1_gamma = p->final_gamma;
+  fin.ln1_beta = p->final_beta;
+  fin.x_exp = p->blocks[11].out_exp;
+  fin.gamma1_exp = p->final_gamma_exp;
+  fin.beta1_exp = p->final_beta_exp;
+  fin.ln1_out_exp = p->final_ln_out_exp;
+  bool final_done = false;
   for (int blk = 1; blk <= 12; ++blk) {
     if (sel < p->n_selectors && p->selector_blocks[sel] == blk) {
       SelectorArgs a{};
@@ -688,28 +698,32 @@ static int model_forward(const hv_model_dev *p, const void *images, bool float_i
       ++sel;
       if (ckpt && (rc = launch_copy_ckpt(w.xa, w.off_a, batch, ckpt, ckpt_rows, sel, s))) return rc;
     }
-    // The next block's LayerNorm 1 inside this block's FFN kernel, unless a
-    // selector changes the rows in between.
+    // The next block's LayerNorm 1 (after block 12 the final LayerNorm)
+    // inside this block's FFN kernel, unless a selector changes the rows in
+    // between.
     const bool chain_next =
-        blk < 12 && !(sel < p->n_selectors && p->selector_blocks[sel] == blk + 1);
+        blk == 12 || !(sel < p->n_selectors && p->selector_blocks[sel] == blk + 1);
     bool next_done = false;
-    const LnChain chain{ln1_ready, chain_next ? &p->blocks[blk] : nullptr, w.blk.ln, &next_done};
+    const LnChain chain{ln1_ready, chain_next ? (blk < 12 ? &p->blocks[blk] : &fin) : nullptr,
+                        w.blk.ln, &next_done};
     if ((rc = block_forward(p->blocks[blk - 1], w.xa, w.off_a, batch, max_rows, w.xb, nullptr,
                             warnings, w.blk, s, chain)))
       return rc;
     ln1_ready = next_done ? w.blk.ln : nullptr;
+    if (blk == 12) final_done = next_done;
     std::swap(w.xa, w.xb);
     if (ckpt && (rc = launch_copy_ckpt(w.xa, w.off_a, batch, ckpt, ckpt_rows, 3 + blk, s))) return rc;
   }
-  // Final LayerNorm over every row (model.py:102-106), head on CLS rows.
-  {
+  // Final LayerNorm over every row (model.py:102-106) unless block 12's FFN
+  // kernel wrote it, head on CLS rows.
+  if (!final_done) {
     ProfScope ps(HV_PROF_LAYERNORM, s);
     rc = launch_layernorm(w.xa, p->final_gamma, p->final_beta, w.blk.ln, max_rows,
                           w.off_a + batch, p->blocks[11].out_exp, p->final_gamma_exp,
                           p->final_beta_exp, p->final_ln_out_exp, nullptr,
                           LnWarn{w.off_a, batch, warnings}, s);
+    if (rc) return rc;
   }
-  if (rc) return rc;
   if (ckpt && (rc = launch_copy_ckpt(w.blk.ln, w.off_a, batch, ckpt, ckpt_rows, 16, s))) return rc;
   GemmArgs g{};
   g.a = w.blk.ln; g.a_rows = w.off_a; g.b = p->head_w_p; g.bias = p->head_b; g.c = logits;

@@ -316,9 +316,9 @@ def test_pipeline_slots_match_engine():
 @pytest.mark.parametrize("pruned", [True, False])
 def test_model_chains_layernorm1_through_ffn_kernels(oracle, pruned):
     """Each block's FFN kernel also writes the next block's LayerNorm 1 unless
-    a selector changes the rows in between, so the LayerNorm launches are
-    block 1's, one after each selector and the final one; logits, token
-    counts and warnings match the oracle."""
+    a selector changes the rows in between, and block 12's the final
+    LayerNorm, so the LayerNorm launches are block 1's and one after each
+    selector; logits, token counts and warnings match the oracle."""
     from heatvit_amd import _lib
     from heatvit_amd.model import HeatViTModel
     imgs, params = synth.pruned_workload(6)
@@ -335,7 +335,7 @@ def test_model_chains_layernorm1_through_ffn_kernels(oracle, pruned):
     finally:
         L.hv_profile_enable(0)
     n = dict(zip(_lib.PROF_CLASSES, n.tolist()))
-    assert n["layernorm"] == 2 + len(params.selectors) and n["ffn"] == 12, n
+    assert n["layernorm"] == 1 + len(params.selectors) and n["ffn"] == 12, n
     logits, counts, status, warnings = oracle.model_infer_batch(imgs, params)
     assert not status.any()
     assert np.array_equal(r.logits, logits)
@@ -348,8 +348,9 @@ def test_model_layernorm_fallbacks_vs_oracle(oracle):
     """Blocks whose LayerNorm leaves the int32 form (beta 17 binary places
     below gamma, so gamma no longer sits at the common exponent): block 2's
     LayerNorm 1 then runs as a launch of the general kernel (block 1's FFN
-    kernel does not write it) and block 5's LayerNorm 2 runs outside its FFN
-    kernel, which then writes no LayerNorm 1 for block 6 either; the other
+    kernel does not write it), block 5's LayerNorm 2 runs outside its FFN
+    kernel, which then writes no LayerNorm 1 for block 6 either, and the
+    final LayerNorm, so changed, runs as a launch after block 12; the other
     blocks stay fused.  The LayerNorm launch count follows, and logits,
     token counts and warnings match the oracle."""
     import dataclasses
@@ -362,7 +363,8 @@ def test_model_layernorm_fallbacks_vs_oracle(oracle):
         blocks[1], mhsa=dataclasses.replace(m1, beta1_scale_exp=m1.gamma1_scale_exp - 17))
     blocks[4] = dataclasses.replace(
         blocks[4], ffn=dataclasses.replace(f4, beta2_scale_exp=f4.gamma2_scale_exp - 17))
-    p = dataclasses.replace(params, blocks=tuple(blocks))
+    p = dataclasses.replace(params, blocks=tuple(blocks),
+                            final_beta_scale_exp=params.final_gamma_scale_exp - 17)
     L = _lib.lib()
     L.hv_profile_enable(1)
     try:
@@ -416,7 +418,7 @@ def test_model_projection_and_qkv_outside_fused_kernels_vs_oracle(oracle):
     n = dict(zip(_lib.PROF_CLASSES, n.tolist()))
     assert n["gemm_proj"] == 1 and n["ffn"] == 12, n
     assert n["gemm_qkv"] == 1 and n["attention"] == 12, n
-    assert n["layernorm"] == 2 + len(params.selectors), n
+    assert n["layernorm"] == 1 + len(params.selectors), n
     logits, counts, status, warnings = oracle.model_infer_batch(imgs, p)
     assert not status.any()
     assert np.array_equal(r.logits, logits)
