@@ -387,39 +387,39 @@ __device__ __forceinline__ void qkv_head(const AttnArgs &g, int8_t *Qs, int8_t *
                                                   lane * 16);
     }
 #pragma unroll 1
-  for (int rt = rt0; rt < nrt; rt += 4) {
-    const int r = rt * 32 + l32;
-    const int8_t *ap = g.ln1 + (size_t)(row0 + min(r, N - 1)) * 192 + 16 * hh;
-    v4i a[6];
+    for (int rt = rt0; rt < nrt; rt += 4) {
+      const int r = rt * 32 + l32;
+      const int8_t *ap = g.ln1 + (size_t)(row0 + min(r, N - 1)) * 192 + 16 * hh;
+      v4i a[6];
 #pragma unroll
-    for (int kt = 0; kt < 6; ++kt) a[kt] = *reinterpret_cast<const v4i *>(ap + kt * 32);
+      for (int kt = 0; kt < 6; ++kt) a[kt] = *reinterpret_cast<const v4i *>(ap + kt * 32);
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int ctg = p * 6 + h * 2 + c;
-      v4i b4[4];
+      for (int c = 0; c < 2; ++c) {
+        const int ctg = p * 6 + h * 2 + c;
+        v4i b4[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        b4[q] = *reinterpret_cast<const v4i *>(g.bqkv + ctg * 32 + 16 * hh + 4 * q);
-      v16i acc = v16i{0};
+        for (int q = 0; q < 4; ++q)
+          b4[q] = *reinterpret_cast<const v4i *>(g.bqkv + ctg * 32 + 16 * hh + 4 * q);
+        v16i acc = v16i{0};
 #pragma unroll
-      for (int kt = 0; kt < 6; ++kt)
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[c][kt], a[kt], acc, 0, 0, 0);
-      v4i o = qkv_epi<LA>(g, acc, b4, rq);
-      if (r >= N) o = v4i{0};
-      const int ch = c * 32 + 16 * hh;  // channel within the head
-      if (p == 0) {
-        if (r < rows_k) *reinterpret_cast<v4i *>(&Qs[r * kKStride + ch]) = o;
-      } else if (p == 1) {
-        if (r < rows_k) *reinterpret_cast<v4i *>(&Ks[r * kKStride + ch]) = o;
-      } else {
-        const int pos = vt_pos(r);
+        for (int kt = 0; kt < 6; ++kt)
+          acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[c][kt], a[kt], acc, 0, 0, 0);
+        v4i o = qkv_epi<LA>(g, acc, b4, rq);
+        if (r >= N) o = v4i{0};
+        const int ch = c * 32 + 16 * hh;  // channel within the head
+        if (p == 0) {
+          if (r < rows_k) *reinterpret_cast<v4i *>(&Qs[r * kKStride + ch]) = o;
+        } else if (p == 1) {
+          if (r < rows_k) *reinterpret_cast<v4i *>(&Ks[r * kKStride + ch]) = o;
+        } else {
+          const int pos = vt_pos(r);
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          Vt[(ch + i) * kVStride + pos] = (int8_t)(o[i >> 2] >> (8 * (i & 3)));
+          for (int i = 0; i < 16; ++i)
+            Vt[(ch + i) * kVStride + pos] = (int8_t)(o[i >> 2] >> (8 * (i & 3)));
+        }
+        __builtin_amdgcn_sched_barrier(0);  // one column tile's registers at a time
       }
-      __builtin_amdgcn_sched_barrier(0);  // one column tile's registers at a time
     }
-  }
   }
 }
 
