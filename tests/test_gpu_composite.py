@@ -144,6 +144,50 @@ def test_block_ln2_inside_fused_ffn_vs_oracle(oracle):
         assert np.array_equal(cks[i]["fused_qkv"], ck["fused_qkv"]), (i, len(x))
 
 
+@pytest.mark.parametrize("msa_exp,ffn_x_exp,dirs", [(-7, -11, 0), (-13, -12, 1), (-7, -12, 2),
+                                                    (-11, -12, 3)])
+def test_block_projection_requant_directions_in_ffn_kernel_vs_oracle(oracle, msa_exp,
+                                                                     ffn_x_exp, dirs):
+    """The projection inside the fused FFN kernel with each pair of requant
+    directions (bit 0: the product's requant shifts left, msa_out at or
+    below context_out + wproj; bit 1: the residual align-add's output shift
+    is not positive), over 32 ragged images without checkpoints: no
+    projection launch, and z equal to the oracle's."""
+    import dataclasses
+    _, bp = synth.block_workload()
+    m, f = bp.mhsa, bp.ffn
+    shift_a = msa_exp - (m.context_out_scale_exp + m.wproj_scale_exp)
+    os_ = ffn_x_exp - min(m.x_scale_exp, msa_exp)
+    assert (shift_a <= 0) + 2 * (os_ <= 0) == dirs
+    bp = dataclasses.replace(bp, mhsa=dataclasses.replace(m, msa_out_scale_exp=msa_exp),
+                             ffn=dataclasses.replace(f, x_scale_exp=ffn_x_exp))
+    xs = _ragged_batch(np.random.default_rng(40 + dirs))
+    zs, n = _block_launches(xs, bp, False)
+    assert n["gemm_proj"] == 0 and n["ffn"] == 1 and n["layernorm"] == 1, n
+    for i, x in enumerate(xs):
+        z, _ = oracle.transformer_block(x, bp, checkpoints=False)
+        assert np.array_equal(zs[i], z), (i, len(x))
+
+
+@pytest.mark.parametrize("qkv_exp,score_exp", [(-9, -21), (-4, -11), (-9, -7), (-19, -30)])
+def test_block_attention_with_qkv_in_kernel_exponents_vs_oracle(oracle, qkv_exp, score_exp):
+    """The QKV GEMM inside the attention kernel over 32 ragged images without
+    checkpoints, under the score paths of the int32 Q8.16 conversion (a
+    right shift, a plain saturation, the general two-step form) and a QKV
+    requant that shifts left (the last case): no QKV launch, z equal to the
+    oracle's."""
+    import dataclasses
+    _, bp = synth.block_workload()
+    bp = dataclasses.replace(bp, mhsa=dataclasses.replace(
+        bp.mhsa, qkv_out_scale_exp=qkv_exp, score_scale_exp=score_exp))
+    xs = _ragged_batch(np.random.default_rng(60 - qkv_exp))
+    zs, n = _block_launches(xs, bp, False)
+    assert n["gemm_qkv"] == 0 and n["attention"] == 1, n
+    for i, x in enumerate(xs):
+        z, _ = oracle.transformer_block(x, bp, checkpoints=False)
+        assert np.array_equal(zs[i], z), (i, len(x))
+
+
 def test_block_wide_biases_all_gemms_vs_oracle(oracle):
     """Biases beyond the int32 epilogue bounds in all four GEMMs send their
     tiles to the exact 64-bit forms (the projection's inside the fused FFN
