@@ -330,6 +330,12 @@ __device__ __noinline__ int attn_ctx_general(int v, int ctx_shift) {
   return (int)requant_shift(v, ctx_shift, 8);
 }
 
+// Exact int8 requant of acc + bias (64-bit), out of line: the fused QKV's
+// form for biases beyond the int32 bound.
+__device__ __noinline__ int attn_requant8(int acc, int bias, int shift) {
+  return (int)requant_shift((i64)acc + bias, shift, 8);
+}
+
 // int8 requant of one fused-QKV tile (gemm_writeback, gemm.py:117-139):
 // lane l's 16 outputs, the int32 form when every lane's biases allow it.
 template <bool LA>
@@ -347,8 +353,7 @@ __device__ __forceinline__ v4i qkv_epi(const AttnArgs &g, const v16i &acc, const
     for (int j = 0; j < 16; ++j) o[j] = rq_dir_nowrap<LA>(acc[j] + b4[j >> 2][j & 3], rq);
   } else {
 #pragma unroll
-    for (int j = 0; j < 16; ++j)
-      o[j] = (int)requant_shift((i64)acc[j] + b4[j >> 2][j & 3], g.qkv_shift, 8);
+    for (int j = 0; j < 16; ++j) o[j] = attn_requant8(acc[j], b4[j >> 2][j & 3], g.qkv_shift);
   }
   v4i w;
 #pragma unroll
@@ -361,7 +366,10 @@ __device__ __forceinline__ v4i qkv_epi(const AttnArgs &g, const v16i &acc, const
 // Q, K and V of head h over the image's N rows (the fused QKV GEMM and its
 // requant, transformer.py:211-227, split per head as qkv_unpack does,
 // layout.py:92-131) into LDS: Q and K as rows (Qs, Ks), V transposed in
-// the P V key order (Vt).  Units of one row tile of 32 and one of Q, K, V
+// the P V key order (Vt).  V takes the product with the operands swapped:
+// each lane then holds one channel (the weight packing's channel of its
+// column) over four runs of four consecutive keys, and each run is one
+// dword of Vt.  Units of one row tile of 32 and one of Q, K, V
 // (its two column tiles of 32), unit u = p * nrt + rt on wavefront u % 4,
 // which loads the weight fragments once per p.  Rows from N up
 // to the 64-key chunk end are stored as zero (the padded keys); Q and K
@@ -393,6 +401,37 @@ __device__ __forceinline__ void qkv_head(const AttnArgs &g, int8_t *Qs, int8_t *
       v4i a[6];
 #pragma unroll
       for (int kt = 0; kt < 6; ++kt) a[kt] = *reinterpret_cast<const v4i *>(ap + kt * 32);
+      if (p == 2) {
+        // channel of this lane's column under the weight packing
+        const int pj = 16 * ((l32 >> 2) & 1) + 4 * (l32 >> 3) + (l32 & 3);
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const int bias = g.bqkv[(p * 6 + h * 2 + c) * 32 + pj];
+          v16i acc = v16i{0};
+#pragma unroll
+          for (int kt = 0; kt < 6; ++kt)
+            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[kt], w[c][kt], acc, 0, 0, 0);
+          if (__all(bias <= g.qkv_acc_lim && bias >= -g.qkv_acc_lim)) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) acc[j] = rq_dir_nowrap<LA>(acc[j] + bias, rq);
+          } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) acc[j] = attn_requant8(acc[j], bias, g.qkv_shift);
+          }
+          int8_t *vrow = Vt + (c * 32 + pj) * kVStride;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int t0 = rt * 32 + 8 * k + 4 * hh;  // keys t0 .. t0 + 3
+            unsigned wd = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              wd |= (t0 + i < N ? (unsigned)(acc[4 * k + i] & 0xFF) : 0u) << (8 * i);
+            *reinterpret_cast<unsigned *>(vrow + vt_pos(t0)) = wd;
+          }
+          __builtin_amdgcn_sched_barrier(0);  // one column tile's registers at a time
+        }
+        continue;
+      }
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const int ctg = p * 6 + h * 2 + c;
@@ -407,16 +446,7 @@ __device__ __forceinline__ void qkv_head(const AttnArgs &g, int8_t *Qs, int8_t *
         v4i o = qkv_epi<LA>(g, acc, b4, rq);
         if (r >= N) o = v4i{0};
         const int ch = c * 32 + 16 * hh;  // channel within the head
-        if (p == 0) {
-          if (r < rows_k) *reinterpret_cast<v4i *>(&Qs[r * kKStride + ch]) = o;
-        } else if (p == 1) {
-          if (r < rows_k) *reinterpret_cast<v4i *>(&Ks[r * kKStride + ch]) = o;
-        } else {
-          const int pos = vt_pos(r);
-#pragma unroll
-          for (int i = 0; i < 16; ++i)
-            Vt[(ch + i) * kVStride + pos] = (int8_t)(o[i >> 2] >> (8 * (i & 3)));
-        }
+        if (r < rows_k) *reinterpret_cast<v4i *>(&(p == 0 ? Qs : Ks)[r * kKStride + ch]) = o;
         __builtin_amdgcn_sched_barrier(0);  // one column tile's registers at a time
       }
     }
