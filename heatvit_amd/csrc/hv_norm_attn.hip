@@ -370,20 +370,23 @@ __device__ __forceinline__ v4i qkv_epi(const AttnArgs &g, const v16i &acc, const
 // each lane then holds one channel (the weight packing's channel of its
 // column) over four runs of four consecutive keys, and each run is one
 // dword of Vt.  Units of one row tile of 32 and one of Q, K, V
-// (its two column tiles of 32), unit u = p * nrt + rt on wavefront u % 4,
-// which loads the weight fragments once per p.  Rows from N up
-// to the 64-key chunk end are stored as zero (the padded keys); Q and K
-// rows past the key tiles are not stored.
+// (its two column tiles of 32): Q and K over the row tiles that hold key
+// tiles, V over the 64-key chunks; the units are numbered Q, K, V in turn
+// and unit u runs on wavefront u % 4, which loads the weight fragments once
+// per group.  Rows from N up to the 64-key chunk end are stored as zero
+// (the padded keys); Q and K rows past the key tiles are not stored.
 template <bool LA>
 __device__ __forceinline__ void qkv_head(const AttnArgs &g, int8_t *Qs, int8_t *Ks, int8_t *Vt,
                                          int row0, int N, int h, int wave, int lane) {
   const int l32 = lane & 31, hh = lane >> 5;
-  const int nrt = 2 * ((N + 63) >> 6), rows_k = ((N + 15) >> 4) * 16;
+  const int rows_k = ((N + 15) >> 4) * 16;
+  const int nqk = (rows_k + 31) >> 5, nv = 2 * ((N + 63) >> 6);  // row tiles per group
   const Rq rq = rq_setup(g.qkv_shift, -128, 127);
 #pragma unroll 1
   for (int p = 0; p < 3; ++p) {
-    // this wavefront's units of p: u = p * nrt + rt with u % 4 == wave
-    const int rt0 = (wave - p * nrt) & 3;
+    // this wavefront's units of group p: u = p * nqk + rt with u % 4 == wave
+    const int nrt = p < 2 ? nqk : nv;
+    const int rt0 = (wave - p * nqk) & 3;
     if (rt0 >= nrt) continue;
     v4i w[2][6];
 #pragma unroll
