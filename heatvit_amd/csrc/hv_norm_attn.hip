@@ -371,7 +371,7 @@ __device__ __forceinline__ v4i qkv_epi(const AttnArgs &g, const v16i &acc, const
 // column) over four runs of four consecutive keys, and each run is one
 // dword of Vt.  Units of one row tile of 32 and one of Q, K, V
 // (its two column tiles of 32): Q and K over the row tiles that hold key
-// tiles, V over the 64-key chunks; the units are numbered Q, K, V in turn
+// tiles, V over those that hold keys; the units are numbered Q, K, V in turn
 // and unit u runs on wavefront u % 4, which loads the weight fragments once
 // per group.  Rows from N up to the 64-key chunk end are stored as zero
 // (the padded keys); Q and K rows past the key tiles are not stored.
@@ -380,7 +380,7 @@ __device__ __forceinline__ void qkv_head(const AttnArgs &g, int8_t *Qs, int8_t *
                                          int row0, int N, int h, int wave, int lane) {
   const int l32 = lane & 31, hh = lane >> 5;
   const int rows_k = ((N + 15) >> 4) * 16;
-  const int nqk = (rows_k + 31) >> 5, nv = 2 * ((N + 63) >> 6);  // row tiles per group
+  const int nqk = (rows_k + 31) >> 5, nv = (N + 31) >> 5;  // row tiles per group
   const Rq rq = rq_setup(g.qkv_shift, -128, 127);
 #pragma unroll 1
   for (int p = 0; p < 3; ++p) {
@@ -454,6 +454,11 @@ __device__ __forceinline__ void qkv_head(const AttnArgs &g, int8_t *Qs, int8_t *
       }
     }
   }
+  // keys of the last 64-key chunk past the V tiles: zero (four keys of one
+  // channel per dword)
+  const int kz = nv * 32, runs = (((N + 63) >> 6) * 64 - kz) >> 2;
+  for (int i = threadIdx.x; i < runs * 64; i += blockDim.x)
+    *reinterpret_cast<unsigned *>(Vt + (i & 63) * kVStride + vt_pos(kz + 4 * (i >> 6))) = 0u;
 }
 
 // The query tiles of one wavefront for an image of NT key tiles (N in
