@@ -349,9 +349,9 @@ def main():
                          "kernel for scaling HBM counters in a profiler run)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one MI355X: this build runs the whole batch on a single GPU "
-              "(images are independent; see DESIGN.md for how the path would shard). "
-              "Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one MI355X: the whole batch runs on a single GPU (images are "
+              "independent, so more GPUs would each take a share of the batch in a process of "
+              "their own). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if args.hw_queues:
         # before anything initialises HIP (torch and the library load below)
