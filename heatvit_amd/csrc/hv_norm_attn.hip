@@ -369,7 +369,9 @@ __device__ __forceinline__ v4i qkv_epi(const AttnArgs &g, const v16i &acc, const
 // the P V key order (Vt).  V takes the product with the operands swapped:
 // each lane then holds one channel (the weight packing's channel of its
 // column) over four runs of four consecutive keys, and each run is one
-// dword of Vt.  Units of one row tile of 32 and one of Q, K, V
+// dword of Vt, and adds its keys' sum to the channel's 128 sum_k V[k]
+// in vsum (LDS atomics; vsum zeroed before).  Units of one row tile of 32
+// and one of Q, K, V
 // (its two column tiles of 32): Q and K over the row tiles that hold key
 // tiles, V over those that hold keys; the units are numbered Q, K, V in turn
 // and unit u runs on wavefront u % 4, which loads the weight fragments once
@@ -377,7 +379,7 @@ __device__ __forceinline__ v4i qkv_epi(const AttnArgs &g, const v16i &acc, const
 // (the padded keys); Q and K rows past the key tiles are not stored.
 template <bool LA>
 __device__ __forceinline__ void qkv_head(const AttnArgs &g, int8_t *Qs, int8_t *Ks, int8_t *Vt,
-                                         int row0, int N, int h, int wave, int lane) {
+                                         int *vsum, int row0, int N, int h, int wave, int lane) {
   const int l32 = lane & 31, hh = lane >> 5;
   const int rows_k = ((N + 15) >> 4) * 16;
   const int nqk = (rows_k + 31) >> 5, nv = (N + 31) >> 5;  // row tiles per group
@@ -422,15 +424,20 @@ __device__ __forceinline__ void qkv_head(const AttnArgs &g, int8_t *Qs, int8_t *
             for (int j = 0; j < 16; ++j) acc[j] = attn_requant8(acc[j], bias, g.qkv_shift);
           }
           int8_t *vrow = Vt + (c * 32 + pj) * kVStride;
+          int vs = 0;
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
             const int t0 = rt * 32 + 8 * k + 4 * hh;  // keys t0 .. t0 + 3
             unsigned wd = 0;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-              wd |= (t0 + i < N ? (unsigned)(acc[4 * k + i] & 0xFF) : 0u) << (8 * i);
+            for (int i = 0; i < 4; ++i) {
+              const int v = t0 + i < N ? acc[4 * k + i] : 0;
+              vs += v;
+              wd |= (unsigned)(v & 0xFF) << (8 * i);
+            }
             *reinterpret_cast<unsigned *>(vrow + vt_pos(t0)) = wd;
           }
+          atomicAdd(&vsum[c * 32 + pj], vs * 128);
           __builtin_amdgcn_sched_barrier(0);  // one column tile's registers at a time
         }
         continue;
@@ -597,7 +604,9 @@ __global__ __launch_bounds__(256, 3) void k_attention(AttnArgs g) {
   const int8_t *qkv = FQ ? nullptr : g.qkv + (size_t)row0 * 576;
 
   if constexpr (FQ) {
-    qkv_head<FQL>(g, Qs, Ks, Vt, row0, N, h, wave, lane);
+    if (tid < 64) vsum[tid] = 0;
+    __syncthreads();
+    qkv_head<FQL>(g, Qs, Ks, Vt, vsum, row0, N, h, wave, lane);
   } else {
   for (int i = tid; i < n16 * 16 * 4; i += 256) {
     const int r = i >> 2, c = (i & 3) * 16;
@@ -630,14 +639,18 @@ __global__ __launch_bounds__(256, 3) void k_attention(AttnArgs g) {
   __syncthreads();
   // The probabilities enter P V as the signed bytes P - 128: P V =
   // (P - 128) V + 128 sum_k V[k], one MFMA per tile instead of two.  The
-  // per-channel sums run over the zero-padded keys too.
-  if (tid < 64) {
-    const int *row = reinterpret_cast<const int *>(&Vt[tid * kVStride]);
-    int sv = 0;
-    for (int w = 0; w < n64 * 16; ++w) sv = __builtin_amdgcn_sdot4(row[w], 0x01010101, sv, false);
-    vsum[tid] = sv * 128;
+  // per-channel sums run over the zero-padded keys too (with FQ qkv_head
+  // has added them up).
+  if constexpr (!FQ) {
+    if (tid < 64) {
+      const int *row = reinterpret_cast<const int *>(&Vt[tid * kVStride]);
+      int sv = 0;
+      for (int w = 0; w < n64 * 16; ++w)
+        sv = __builtin_amdgcn_sdot4(row[w], 0x01010101, sv, false);
+      vsum[tid] = sv * 128;
+    }
+    __syncthreads();
   }
-  __syncthreads();
 
   switch (n16) {
 #define HV_ATTN_CASE(n) \
