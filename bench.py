@@ -61,9 +61,11 @@ def class_work(counts, params, batch):
     ops per token; attention 2*384*N^2 per image; patch 2*768*192 per
     patch; head 2*192*1000 per image; selector 2*13938 per candidate.  The
     attention kernel computes its head's Q, K and V itself (the LayerNorm 1
-    rows in, the context rows out: 384 B per token, with the QKV ops).  The
-    fused FFN kernel runs the attention projection and its residual (the
-    context rows and x in once; y stays on the CU), LayerNorm 2, FFN1,
+    rows in, the context rows out: 384 B per token, with the QKV ops); where
+    the QKV GEMM runs as its own launch instead (fewer than 32 images),
+    `launched_work` moves those ops back to it.  The fused FFN kernel runs
+    the attention projection and its residual (the context rows and x in
+    once; y stays on the CU), LayerNorm 2, FFN1,
     FFN2 and writes the block output and, when the next block follows
     without a selector in between, that block's LayerNorm 1 (block 12: the
     final LayerNorm): 576 B per token plus 192 B for those blocks; the
@@ -113,6 +115,20 @@ def class_work(counts, params, batch):
     return ops, hbm
 
 
+def launched_work(ops, hbm, launched):
+    """The per-class work of the classes a run launched.  When the QKV GEMM
+    ran as its own launch, the attention kernel read the fused QKV rows
+    (576 B per token) instead of computing them: its QKV ops belong to the
+    GEMM class only, and its bytes are 768 B per token (QKV rows in, context
+    out) instead of 384."""
+    ops, hbm = dict(ops), dict(hbm)
+    if "gemm_qkv" in launched and ops.get("attention"):
+        ops["attention"] -= ops["gemm_qkv"]
+        hbm["attention"] = hbm["attention"] * 2
+    return ({n: v for n, v in ops.items() if n in launched},
+            {n: v for n, v in hbm.items() if n in launched})
+
+
 def oracle_model(images, params, threads):
     """The CPU oracle over a batch: (logits, token counts, status, seconds)."""
     from oracle import oracle
@@ -141,6 +157,25 @@ def roof(ops, nbytes, ms):
              "mfma_frac": round(tops / MI355X_INT8_TOPS, 4)}
     r["ops_per_byte"] = round(intensity, 1) if nbytes else None
     return r
+
+
+def reference_cpu():
+    """The reference's own golden model (verification/heatvit_ref,
+    HeatViTModel.infer) on the 32 images of the pruned workload, timed when
+    the fixture tests/golden/pruned.json was written: one image per process,
+    eight processes on the eight cores of the development container.  Not
+    measured on the GPU box's host, so it is labelled and kept apart from
+    cpu_baseline."""
+    f = ROOT / "tests" / "golden" / "pruned.json"
+    if not f.exists():
+        return None
+    secs = json.loads(f.read_text())["golden_seconds"]
+    per_image = float(np.mean(secs))
+    return {"seconds_per_image": round(per_image, 2),
+            "images_per_s": round(8 / per_image, 4), "cores": 8, "same_box": False,
+            "sample": f"golden model HeatViTModel.infer on {len(secs)} pruned images "
+                      "(197->88->45->32), one per process in an 8-process pool on the "
+                      "8-core development container, from tests/golden/pruned.json"}
 
 
 def _sync_time(fn, warmup, steps):
@@ -175,6 +210,7 @@ GEMM_CLASSES = ("patch", "gemm_qkv", "attention", "gemm_proj", "gemm_ffn1", "gem
 def _summary(cls_ms, ops, hbm, batch, ms, exact, cpu_s):
     # classes the run launched (the fused FFN's work also has entries under
     # the separate FFN1 / FFN2 GEMMs, which then do not launch)
+    ops, hbm = launched_work(ops, hbm, cls_ms)
     gemm_ms = sum(cls_ms.get(n, 0.0) for n in GEMM_CLASSES)
     gemm_ops = sum(ops.get(n, 0) for n in GEMM_CLASSES if n in cls_ms)
     line = {"images_per_s": round(batch / (ms * 1e-3), 1), "ms_per_forward": round(ms, 4),
@@ -231,7 +267,9 @@ def config_lines(args, L):
            "gemm_ffn1": 2 * 192 * 768 * n, "gemm_ffn2": 2 * 768 * 192 * n,
            "ffn": (2 * 192 * 192 + 2 * 2 * 192 * 768) * n,
            "attention": 2 * 192 * 576 * n + 2 * 384 * n * n}
-    hbm = {"layernorm": 2 * 2 * 192 * n}
+    # one LayerNorm launch (LayerNorm 1; LayerNorm 2 runs inside the fused
+    # FFN kernel)
+    hbm = {"layernorm": 2 * 192 * n, "attention": 384 * n}
     out["c0_block_b1"] = _summary(_class_ms(L, block, args.steps), ops, hbm, 1, ms,
                                   bool(np.array_equal(z.cpu().numpy(), want)), cpu_s)
 
@@ -344,6 +382,9 @@ def main():
                     help="skip the float-image front-end measurement")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the per-config lines and the standalone softmax")
+    ap.add_argument("--sustained-seconds", type=float, default=2.5,
+                    help="length of the sustained pipelined run reported beside `value` "
+                         "(0 skips it)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run three 64 MiB device-to-device copies (the reference "
                          "kernel for scaling HBM counters in a profiler run)")
@@ -404,6 +445,23 @@ def main():
         wall_ms = latency_ms
     value = args.batch / (wall_ms / 1e3)
 
+    # Sustained: the same pipelined forwards back to back for a few seconds,
+    # so clocks reach steady state; reported beside `value`, never as it.
+    sustained = None
+    if args.sustained_seconds > 0:
+        spipe = Pipeline(eng.model, args.batch, depth=max(args.streams, 1)) \
+            if args.streams > 1 else None
+        step = spipe.submit if spipe else eng.forward
+        per = max(1, int(args.sustained_seconds * 1e3 / max(wall_ms, 1e-3)))
+        s_ms = timed(step, per)
+        sustained = {"value": round(args.batch / (s_ms / 1e3), 1), "ms_per_step": round(s_ms, 4),
+                     "steps": per, "seconds": round(per * s_ms / 1e3, 2),
+                     "batches_in_flight": max(args.streams, 1)}
+        if spipe:
+            sustained["logits_equal"] = all(bool(torch.equal(e.logits[:args.batch], ref_logits))
+                                            for e in spipe.engines)
+            del spipe
+
     # Second pass over the same steps; every kernel carries start/stop HIP
     # events recorded by its dispatch (kept out of the timed region above).
     L = _lib.lib()
@@ -414,7 +472,8 @@ def main():
     launches = np.zeros(len(_lib.PROF_CLASSES), np.int32)
     _lib.check(L.hv_profile_read(ms.ctypes.data, launches.ctypes.data, len(ms)), "profile")
     L.hv_profile_enable(0)
-    ops, hbm = class_work(counts, params, args.batch)
+    ops, hbm = launched_work(*class_work(counts, params, args.batch),
+                             {n for i, n in enumerate(_lib.PROF_CLASSES) if launches[i]})
     per_class = {}
     for i, name in enumerate(_lib.PROF_CLASSES):
         if launches[i] == 0:
@@ -565,6 +624,8 @@ def main():
         "configs": configs,
         "softmax_standalone": softmax,
         "cpu_baseline": cpu,
+        "reference_cpu": reference_cpu(),
+        "sustained": sustained,
     }
     print(json.dumps(line))
     if not line["bit_exact"] or (configs and not all(c["bit_exact"] for c in configs.values())):

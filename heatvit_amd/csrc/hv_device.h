@@ -454,11 +454,18 @@ __host__ __device__ __forceinline__ LnRow ln_row_consts(int sx, int sxx, int s, 
   return r;
 }
 
+// v sign-extended from bit 23.  The limbs a0, a1, a2 already are signed
+// 24-bit values; restating it where they are used lets the compiler emit
+// v_mad_i32_i24 for the limb products even when the row constants arrive
+// through a cross-lane shuffle (it otherwise picks v_mad_u64_u32 and
+// v_mul_lo_u32, which issue at a quarter of the rate).
+__host__ __device__ __forceinline__ int i24(int v) { return (int)((unsigned)v << 8) >> 8; }
+
 // norm_q16 of one element (sat24 included).
 __host__ __device__ __forceinline__ int ln_norm(int x, const LnRow &r) {
-  const int u0 = x * r.a0 + r.c0 - (x <= r.xt ? 1 : 0);
-  const int u1 = x * r.a1 + r.c1 + (u0 >> 24);
-  const int v = x * r.a2 + r.c2 + (u1 >> 24);
+  const int u0 = x * i24(r.a0) + r.c0 - (x <= r.xt ? 1 : 0);
+  const int u1 = x * i24(r.a1) + r.c1 + (u0 >> 24);
+  const int v = x * i24(r.a2) + r.c2 + (u1 >> 24);
   return v < -(1 << 23) ? -(1 << 23) : (v > (1 << 23) - 1 ? (1 << 23) - 1 : v);
 }
 

@@ -99,3 +99,55 @@ def test_calibration_targets_recorded():
     assert abs(cal["selector"]["kept_fraction"] - 0.45) < 0.01
     means = [np.mean(c) for c in cal["pruned"]["calibration_token_counts"]]
     assert [round(m) for m in means] == list(synth.TOKEN_TARGETS)
+
+
+def _abi_kind(t):
+    """ctypes argtype reduced to what the C ABI sees: any pointer is a pointer."""
+    if t is ctypes.c_void_p or (isinstance(t, type) and issubclass(t, ctypes._Pointer)):
+        return "ptr"
+    return ctypes.sizeof(t), t.__name__.replace("c_int32", "c_int")
+
+
+def test_integration_example_matches_binding():
+    """The ctypes example of INTEGRATION.md declares the argtypes that
+    heatvit_amd._lib declares, and its call passes as many arguments as
+    include/heatvit_hip.h's prototype has."""
+    from heatvit_amd import _lib
+
+    text = (ROOT / "INTEGRATION.md").read_text()
+    block = text.split("### ctypes binding", 1)[1].split("```python", 1)[1].split("```", 1)[0]
+    stmts = re.findall(r"^(lib\.hv_\w+\.(?:argtypes|restype) = (?:.*\\\n)*.*)$", block, re.M)
+    assert any("hv_model_forward.argtypes" in s for s in stmts)
+
+    class Fn:
+        pass
+
+    class Lib:
+        def __getattr__(self, name):
+            f = Fn()
+            setattr(self, name, f)
+            return f
+
+    doc, ref = Lib(), Lib()
+    for s in stmts:
+        exec(s, {"ctypes": ctypes, "lib": doc})
+    _lib._declare(ref)
+    for name, fn in vars(doc).items():
+        want = getattr(ref, name)
+        if hasattr(fn, "argtypes"):
+            assert [_abi_kind(t) for t in fn.argtypes] == \
+                [_abi_kind(t) for t in want.argtypes], name
+        if hasattr(fn, "restype"):
+            assert fn.restype is want.restype, name
+
+    header = (ROOT / "include" / "heatvit_hip.h").read_text()
+    proto = re.search(r"int hv_model_forward\(([^)]*)\);", header).group(1)
+    n_params = len(proto.split(","))
+    assert n_params == len(doc.hv_model_forward.argtypes)
+    call = re.search(r"lib\.hv_model_forward\((.*?)\)\n", block, re.S).group(1)
+    depth, args = 0, 1
+    for ch in call:
+        depth += ch == "("
+        depth -= ch == ")"
+        args += ch == "," and depth == 0
+    assert args == n_params
