@@ -83,9 +83,33 @@ static void prof_clear() {
 // cls (optional): row 0 of each image's 197 rows in x is the CLS row,
 // align_add(cls, pos[0]) (transformer.py:130-145), written here rather than
 // by a launch of its own after the patch embedding.
+// The model's GEMM bias tensors whose largest |bias| the first kernel of a
+// forward writes (GemmArgs::bias_max): entry 4 * block + t for t = 0 bqkv,
+// 1 bproj, 2 b1, 3 b2.
+struct BiasJobs {
+  const int32_t *p[48];
+  unsigned *out;
+};
+__device__ constexpr int kBiasCount[4] = {576, 192, 768, 192};
+
 __global__ void k_init_offsets(int32_t *offsets, uint8_t *pkg, int32_t *token_counts,
                                int32_t *warnings, int batch, int rows, hv_patch_dev cls,
-                               int8_t *x) {
+                               int8_t *x, BiasJobs bj, int init_blocks) {
+  if ((int)blockIdx.x >= init_blocks) {  // uniform: one bias tensor per workgroup
+    __shared__ unsigned red[4];
+    const int j = blockIdx.x - init_blocks, n = kBiasCount[j & 3];
+    unsigned m = 0;
+    for (int k = threadIdx.x; k < n; k += blockDim.x) {
+      const int b = bj.p[j][k];
+      m = max(m, b < 0 ? 0u - (unsigned)b : (unsigned)b);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = max(m, (unsigned)__shfl_xor((int)m, off));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) bj.out[j] = max(max(red[0], red[1]), max(red[2], red[3]));
+    return;
+  }
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i <= batch) offsets[i] = i * rows;
   if (i < batch) {
@@ -104,11 +128,26 @@ __global__ void k_init_offsets(int32_t *offsets, uint8_t *pkg, int32_t *token_co
 
 int launch_init_offsets(int32_t *offsets, uint8_t *pkg, int32_t *token_counts,
                         int32_t *warnings, int batch, int rows, hipStream_t s,
-                        const hv_patch_dev *cls, int8_t *x) {
-  // batch + 1 offsets; with the CLS rows, batch * 192 bytes (a superset)
+                        const hv_patch_dev *cls, int8_t *x, const hv_block_dev *blocks,
+                        unsigned *bias_max) {
+  // batch + 1 offsets; with the CLS rows, batch * 192 bytes (a superset);
+  // with blocks, 48 more workgroups for the bias bounds
   const int items = cls && x ? batch * 192 : batch + 1;
-  hv_launch(k_init_offsets, dim3((items + 255) / 256), dim3(256), 0, s, offsets, pkg,
-            token_counts, warnings, batch, rows, cls ? *cls : hv_patch_dev{}, cls ? x : nullptr);
+  const int init_blocks = (items + 255) / 256;
+  BiasJobs bj{};
+  const bool bias = blocks && bias_max;
+  if (bias) {
+    for (int i = 0; i < 12; ++i) {
+      bj.p[4 * i] = blocks[i].bqkv;
+      bj.p[4 * i + 1] = blocks[i].bproj;
+      bj.p[4 * i + 2] = blocks[i].b1;
+      bj.p[4 * i + 3] = blocks[i].b2;
+    }
+    bj.out = bias_max;
+  }
+  hv_launch(k_init_offsets, dim3(init_blocks + (bias ? 48 : 0)), dim3(256), 0, s, offsets, pkg,
+            token_counts, warnings, batch, rows, cls ? *cls : hv_patch_dev{}, cls ? x : nullptr,
+            bj, init_blocks);
   return check_hip(hipGetLastError(), "k_init_offsets launch");
 }
 
@@ -195,10 +234,11 @@ static constexpr int kFusedQkvMinBatch = 32;
 // transformer_block (transformer.py:401-431) on rows [0, offsets[batch]):
 // LN1, QKV, attention, proj + residual, LN2, FFN1 + GELU, FFN2 + residual.
 // warnings (optional, [B]) receive the LayerNorms' negative-variance bit.
+// bias_max (optional, device): the largest |bias| of bqkv, bproj, b1 and b2.
 static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *offsets,
                          int batch, int max_rows, int8_t *z, const hv_block_ckpt *ck,
                          int32_t *warnings, const BlockWs &w, hipStream_t s,
-                         const LnChain &chain = LnChain{}) {
+                         const LnChain &chain = LnChain{}, const unsigned *bias_max = nullptr) {
   const int32_t *rows_dev = offsets + batch;
   const LnWarn lw{offsets, batch, warnings};
   int8_t *qkv = ck && ck->fused_qkv ? ck->fused_qkv : w.qkv;
@@ -222,6 +262,7 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   }
   GemmArgs g{};
   g.a = ln1; g.b = p.wqkv_p; g.bias = p.bqkv; g.c = qkv; g.m_dev = rows_dev;
+  g.bias_max = bias_max;
   g.m = max_rows; g.n = 576; g.k = 192; g.lda = 192; g.ldc = 576;
   g.shift_a = p.qkv_out_exp - (p.ln1_out_exp + p.wqkv_exp);
   // Without checkpoints the attention kernel computes each head's Q, K and
@@ -242,7 +283,7 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   AttnArgs a{};
   if (fuse_qkv) {
     a.ln1 = ln1; a.wqkv = p.wqkv_p; a.bqkv = p.bqkv;
-    a.qkv_shift = g.shift_a; a.qkv_acc_lim = g.acc_lim;
+    a.qkv_shift = g.shift_a; a.qkv_acc_lim = g.acc_lim; a.bqkv_max = bias_max;
   }
   a.qkv = qkv; a.offsets = offsets; a.ctx = ctx; a.batch = batch; a.rows_cap = max_rows;
   a.score = ck ? ck->score : nullptr;
@@ -258,17 +299,20 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
 
   g = GemmArgs{};
   g.a = ctx; g.b = p.wproj_p; g.bias = p.bproj; g.c = y; g.res = x; g.aux = ck ? ck->msa : nullptr;
+  g.bias_max = bias_max ? bias_max + 1 : nullptr;
   g.m_dev = rows_dev; g.m = max_rows; g.n = 192; g.k = 192; g.lda = 192; g.ldc = 192; g.ldr = 192;
   g.shift_a = p.msa_out_exp - (p.context_out_exp + p.wproj_exp);
   g.mid_exp = p.msa_out_exp; g.res_exp = p.x_exp; g.out_exp = p.ffn_x_exp;
 
   GemmArgs g1{};
   g1.a = ln2; g1.b = p.w1_p; g1.bias = p.b1; g1.c = hidden; g1.m_dev = rows_dev;
+  g1.bias_max = bias_max ? bias_max + 2 : nullptr;
   g1.m = max_rows; g1.n = 768; g1.k = 192; g1.lda = 192; g1.ldc = 768;
   g1.shift_a = -16 - (p.ln2_out_exp + p.w1_exp);
   g1.shift_b = p.hidden_out_exp + 16;
   GemmArgs g2{};
   g2.a = hidden; g2.b = p.w2_p; g2.bias = p.b2; g2.c = z; g2.res = y;
+  g2.bias_max = bias_max ? bias_max + 3 : nullptr;
   g2.aux = ck ? ck->ffn_out : nullptr;
   g2.m_dev = rows_dev; g2.m = max_rows; g2.n = 192; g2.k = 768; g2.lda = 768; g2.ldc = 192;
   g2.ldr = 192;
@@ -592,6 +636,7 @@ struct ModelWs {
   BlockWs blk;
   int32_t *off_a, *off_b, *fused, *kept, *state;
   uint8_t *pkg_a, *pkg_b;
+  unsigned *bias_max;  // [12][4], k_init_offsets
   SelectorWs sel;
 };
 
@@ -608,6 +653,7 @@ static ModelWs carve_model(Carve &cv, int batch) {
   w.state = cv.take<int32_t>((size_t)batch * 3 * 5);
   w.pkg_a = cv.take<uint8_t>(batch);
   w.pkg_b = cv.take<uint8_t>(batch);
+  w.bias_max = cv.take<unsigned>(48);
   w.sel = carve_selector(cv, batch);
   return w;
 }
@@ -647,7 +693,7 @@ static int model_forward(const hv_model_dev *p, const void *images, bool float_i
   {
     ProfScope ps(HV_PROF_OTHER, s);
     rc = launch_init_offsets(w.off_a, w.pkg_a, token_counts, warnings, batch, HV_MAX_TOKENS,
-                             s, &p->patch, w.xa);
+                             s, &p->patch, w.xa, p->blocks, w.bias_max);
   }
   if (rc) return rc;
   {
@@ -707,7 +753,7 @@ static int model_forward(const hv_model_dev *p, const void *images, bool float_i
     const LnChain chain{ln1_ready, chain_next ? (blk < 12 ? &p->blocks[blk] : &fin) : nullptr,
                         w.blk.ln, &next_done};
     if ((rc = block_forward(p->blocks[blk - 1], w.xa, w.off_a, batch, max_rows, w.xb, nullptr,
-                            warnings, w.blk, s, chain)))
+                            warnings, w.blk, s, chain, w.bias_max + 4 * (blk - 1))))
       return rc;
     ln1_ready = next_done ? w.blk.ln : nullptr;
     if (blk == 12) final_done = next_done;

@@ -336,6 +336,35 @@ __host__ __device__ __forceinline__ unsigned softmax_exp_nx(unsigned nx) {
   return (((mul_u24(23495u, square) + 32768u) >> 16) + 22544u) >> z;
 }
 
+// The same exponential from t = max(x_tilde, -17 * 45426) in seven 32/64-bit
+// multiply-adds and shifts.  z16 = floor(-t / 45426) + 16 is the high word
+// of -t * 94549 + 16 * 2^32 (94549 = ceil(2^32 / 45426)); the quotient this
+// gives is one too large at 16 arguments just below a multiple of 45426,
+// where s then is 88671 instead of 43245 and the result is the same, so the
+// function equals the reference's exponential for every t (an exhaustive
+// check over all 772,243 arguments pins it).  X = 23495 * square + 2^15 +
+// 22544 * 2^16 < 2^33 holds the polynomial as X >> 16, and one 64-bit shift
+// by z16 applies both the >> 16 and the >> z.
+__host__ __device__ __forceinline__ unsigned softmax_exp_t(int t) {
+  const unsigned z16 = (unsigned)((u64)((i64)t * -94549ll + (16ll << 32)) >> 32);
+  const unsigned s = mul_u24(z16, 45426u) + (unsigned)(88670 - 16 * 45426) + (unsigned)t;
+  const unsigned square = (unsigned)(((u64)s * s + 32768u) >> 16);
+  const u64 x = (u64)square * 23495u + (32768u + (22544ull << 16));
+  return (unsigned)(x >> z16);
+}
+
+// The attention's UQ0.8 probability minus 128 (the signed P - 128 operand
+// of the P.V product): p = min(rsa(rsa(e * recip, 16), 8), 255), whose
+// first rounding's discarded bits cannot carry past a multiple of 2^8, so p
+// = min((e * recip + 2^15 + 2^23) >> 24, 255).  With r256 = recip * 2^8 the
+// high word of e * r256 + (2^15 + 2^23) * 2^8 - 128 * 2^32 is p - 128
+// before the clamp (e, recip < 2^17).
+__host__ __device__ __forceinline__ int softmax_prob_m128(unsigned e, unsigned r256) {
+  const i64 v = (i64)e * (i64)r256 + (((32768ll + (1ll << 23)) << 8) - (128ll << 32));
+  const int p = (int)(v >> 32);
+  return p < 127 ? p : 127;
+}
+
 // round_div(2^32, sum) for a row sum that includes exp(0) = 65554, so
 // 65554 <= sum < 2^32 and the result is below 2^17 (nonlinear.py:119):
 // float estimate, exact correction on the remainder.

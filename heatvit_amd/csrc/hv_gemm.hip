@@ -189,22 +189,22 @@ __device__ __forceinline__ void epi_tile(const GemmArgs &g, const v16i (&acc)[MT
   // scalar registers the clamp cannot be a single med3
   int qhi = g.lut_qhi;
   if constexpr (EPI == EPI_GELU && (DIRS & 4)) asm("" : "+v"(qhi));
+  const bool all_narrow = FAST && tensor_narrow(g.bias_max, g.acc_lim);
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int c0 = (ct0 + nt) * 32 + 16 * h;
-    bool narrow = FAST;
-    if (FAST) {
-      // |b| <= acc_lim for the lane's 16 biases, from their range
+    // Uniform per wavefront: the int32 form only when every lane qualifies
+    // (the whole tensor, or a vote over the lanes' 16 biases each).
+    bool fast = all_narrow;
+    if (FAST && !all_narrow) {
       int bmax = bias4[nt][0][0], bmin = bmax;
 #pragma unroll
       for (int j = 1; j < 16; ++j) {
         bmax = max(bmax, bias4[nt][j >> 2][j & 3]);
         bmin = min(bmin, bias4[nt][j >> 2][j & 3]);
       }
-      narrow = bmax <= g.acc_lim && bmin >= -g.acc_lim;
+      fast = __all(bmax <= g.acc_lim && bmin >= -g.acc_lim);
     }
-    // Uniform per wavefront: the int32 form only when every lane qualifies.
-    const bool fast = FAST && __all(narrow);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int row = r0 + mt * 32 + l32;
@@ -897,15 +897,19 @@ __device__ __forceinline__ void ln_rows(const int8_t *src, int clamp, int8_t *ds
 // 413-421), in the int32 form when every lane's biases allow it, else exact.
 template <bool LA, bool LB>
 __device__ __forceinline__ v4i proj_epi(const GemmArgs &gp, const v16i &acc, const v4i (&b4)[4],
-                                        v4i x4, const Rq &rpa, const Rq &rpb) {
-  int bmax = b4[0][0], bmin = bmax;
+                                        v4i x4, const Rq &rpa, const Rq &rpb, bool all_narrow) {
+  bool fast = all_narrow;
+  if (!all_narrow) {
+    int bmax = b4[0][0], bmin = bmax;
 #pragma unroll
-  for (int j = 1; j < 16; ++j) {
-    bmax = max(bmax, b4[j >> 2][j & 3]);
-    bmin = min(bmin, b4[j >> 2][j & 3]);
+    for (int j = 1; j < 16; ++j) {
+      bmax = max(bmax, b4[j >> 2][j & 3]);
+      bmin = min(bmin, b4[j >> 2][j & 3]);
+    }
+    fast = __all(bmax <= gp.acc_lim && bmin >= -gp.acc_lim);
   }
   int o[16];
-  if (__all(bmax <= gp.acc_lim && bmin >= -gp.acc_lim)) {
+  if (fast) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int t8 = rq_dir_nowrap<LA>(acc[j] + b4[j >> 2][j & 3], rpa);
@@ -961,6 +965,7 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
   const Rq r1a = rq_setup(g1.shift_a, -(1 << 23), (1 << 23) - 1);
   const Rq r2a = rq_setup(g2.shift_a, -128, 127), r2b = rq_setup(g2.os, -128, 127);
   constexpr bool LA1 = DIRS1 & 1;
+  const bool all1 = tensor_narrow(g1.bias_max, g1.acc_lim);
   int qhi = g1.lut_qhi;
   asm("" : "+v"(qhi));  // the table clamp as one med3 (both bounds in VGPRs)
 
@@ -985,6 +990,7 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
     v4i yres[PJ ? 3 : 1];
     if constexpr (PJ) {
       const Rq rpa = rq_setup(gp.shift_a, -128, 127), rpb = rq_setup(gp.os, -128, 127);
+      const bool allp = tensor_narrow(gp.bias_max, gp.acc_lim);
 #pragma unroll
       for (int ti = 0; ti < 3; ++ti) {
         const int t = wave + 4 * ti, rt = t / 6, ct = t - rt * 6;
@@ -1007,10 +1013,10 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
           acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(pw[kt], pa[kt], acc, 0, 0, 0);
         v4i yv;
         switch (dirsp) {
-          case 0: yv = proj_epi<false, false>(gp, acc, b4, x4, rpa, rpb); break;
-          case 1: yv = proj_epi<true, false>(gp, acc, b4, x4, rpa, rpb); break;
-          case 2: yv = proj_epi<false, true>(gp, acc, b4, x4, rpa, rpb); break;
-          default: yv = proj_epi<true, true>(gp, acc, b4, x4, rpa, rpb); break;
+          case 0: yv = proj_epi<false, false>(gp, acc, b4, x4, rpa, rpb, allp); break;
+          case 1: yv = proj_epi<true, false>(gp, acc, b4, x4, rpa, rpb, allp); break;
+          case 2: yv = proj_epi<false, true>(gp, acc, b4, x4, rpa, rpb, allp); break;
+          default: yv = proj_epi<true, true>(gp, acc, b4, x4, rpa, rpb, allp); break;
         }
         yres[ti] = yv;
         *reinterpret_cast<v4i *>(&hid[(32 * rt + l32) * kLnPrologueRow + ct * 32 + 16 * h]) = yv;
@@ -1074,13 +1080,16 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
           acc[rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[kt], af[rt][kt], acc[rt], 0, 0, 0);
       }
       if (ci + 1 < 6) load_w1(ci + 1, bs[cur ^ 1]);
-      int bmax = bs[cur][0][0], bmin = bmax;
+      bool fast = all1;
+      if (!all1) {
+        int bmax = bs[cur][0][0], bmin = bmax;
 #pragma unroll
-      for (int j = 1; j < 16; ++j) {
-        bmax = max(bmax, bs[cur][j >> 2][j & 3]);
-        bmin = min(bmin, bs[cur][j >> 2][j & 3]);
+        for (int j = 1; j < 16; ++j) {
+          bmax = max(bmax, bs[cur][j >> 2][j & 3]);
+          bmin = min(bmin, bs[cur][j >> 2][j & 3]);
+        }
+        fast = __all(bmax <= g1.acc_lim && bmin >= -g1.acc_lim);
       }
-      const bool fast = __all(bmax <= g1.acc_lim && bmin >= -g1.acc_lim);
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
         int o[16];

@@ -58,6 +58,10 @@ struct GemmArgs {
   // Filled by launch_gemm: int32 epilogue preconditions.
   int acc_lim;     // a column takes the int32 path when |bias| <= acc_lim
   int narrow_ok;   // acc_lim > 0
+  // Optional device word: the largest |bias| of the whole bias tensor (as
+  // unsigned).  When it is at most acc_lim every column takes the int32
+  // path and the kernels skip their per-tile bias vote.
+  const unsigned *bias_max;
   int da, db, os;  // residual / patch align-add shifts
   int vec_out;     // c (and aux) allow 16-byte row stores
   int vec_res;     // res (or pos) allow 16-byte row loads
@@ -157,7 +161,14 @@ struct AttnArgs {
   const int8_t *wqkv;
   const int32_t *bqkv;
   int qkv_shift, qkv_acc_lim;
+  const unsigned *bqkv_max;  // optional: largest |bias| of bqkv (GemmArgs::bias_max)
 };
+
+// Whether a tensor-wide bias bound (GemmArgs::bias_max) puts every column on
+// the int32 path: a uniform scalar load and compare.
+__device__ __forceinline__ bool tensor_narrow(const unsigned *bias_max, int acc_lim) {
+  return bias_max && acc_lim > 0 && *bias_max <= (unsigned)acc_lim;
+}
 int launch_attention(const AttnArgs &a, hipStream_t s);
 
 int launch_softmax_rows(const int32_t *x, const int32_t *offsets, int rows, uint8_t *att,
@@ -188,10 +199,13 @@ int launch_selector(const SelectorArgs &a, hipStream_t s);
 
 // Small utility kernels.
 // cls, x (optional): also writes the CLS row (row 0 of each image's
-// HV_MAX_TOKENS rows) of the patch embedding into x.
+// HV_MAX_TOKENS rows) of the patch embedding into x.  blocks, bias_max
+// (optional): also writes the largest |bias| of each block's bqkv, bproj,
+// b1 and b2 to bias_max[4 * block + t] (GemmArgs::bias_max).
 int launch_init_offsets(int32_t *offsets, uint8_t *pkg, int32_t *token_counts,
                         int32_t *warnings, int batch, int rows_per_image, hipStream_t s,
-                        const hv_patch_dev *cls = nullptr, int8_t *x = nullptr);
+                        const hv_patch_dev *cls = nullptr, int8_t *x = nullptr,
+                        const hv_block_dev *blocks = nullptr, unsigned *bias_max = nullptr);
 // Per-image token-count check of a caller's offsets: status[b] =
 // HV_ERR_TOKEN_COUNT unless 1 <= count <= 197 and the rows lie in
 // [0, capacity), else 0; warnings[b] = 0.  Either pointer may be NULL.

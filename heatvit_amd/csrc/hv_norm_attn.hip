@@ -340,15 +340,19 @@ __device__ __noinline__ int attn_requant8(int acc, int bias, int shift) {
 // lane l's 16 outputs, the int32 form when every lane's biases allow it.
 template <bool LA>
 __device__ __forceinline__ v4i qkv_epi(const AttnArgs &g, const v16i &acc, const v4i (&b4)[4],
-                                       const Rq &rq) {
-  int bmax = b4[0][0], bmin = bmax;
+                                       const Rq &rq, bool all_narrow) {
+  bool fast = all_narrow;
+  if (!all_narrow) {
+    int bmax = b4[0][0], bmin = bmax;
 #pragma unroll
-  for (int j = 1; j < 16; ++j) {
-    bmax = max(bmax, b4[j >> 2][j & 3]);
-    bmin = min(bmin, b4[j >> 2][j & 3]);
+    for (int j = 1; j < 16; ++j) {
+      bmax = max(bmax, b4[j >> 2][j & 3]);
+      bmin = min(bmin, b4[j >> 2][j & 3]);
+    }
+    fast = __all(bmax <= g.qkv_acc_lim && bmin >= -g.qkv_acc_lim);
   }
   int o[16];
-  if (__all(bmax <= g.qkv_acc_lim && bmin >= -g.qkv_acc_lim)) {
+  if (fast) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) o[j] = rq_dir_nowrap<LA>(acc[j] + b4[j >> 2][j & 3], rq);
   } else {
@@ -384,6 +388,7 @@ __device__ __forceinline__ void qkv_head(const AttnArgs &g, int8_t *Qs, int8_t *
   const int rows_k = ((N + 15) >> 4) * 16;
   const int nqk = (rows_k + 31) >> 5, nv = (N + 31) >> 5;  // row tiles per group
   const Rq rq = rq_setup(g.qkv_shift, -128, 127);
+  const bool all_narrow = tensor_narrow(g.bqkv_max, g.qkv_acc_lim);
 #pragma unroll 1
   for (int p = 0; p < 3; ++p) {
     // this wavefront's units of group p: u = p * nqk + rt with u % 4 == wave
@@ -416,7 +421,7 @@ __device__ __forceinline__ void qkv_head(const AttnArgs &g, int8_t *Qs, int8_t *
 #pragma unroll
           for (int kt = 0; kt < 6; ++kt)
             acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[kt], w[c][kt], acc, 0, 0, 0);
-          if (__all(bias <= g.qkv_acc_lim && bias >= -g.qkv_acc_lim)) {
+          if (all_narrow || __all(bias <= g.qkv_acc_lim && bias >= -g.qkv_acc_lim)) {
 #pragma unroll
             for (int j = 0; j < 16; ++j) acc[j] = rq_dir_nowrap<LA>(acc[j] + bias, rq);
           } else {
@@ -453,7 +458,7 @@ __device__ __forceinline__ void qkv_head(const AttnArgs &g, int8_t *Qs, int8_t *
 #pragma unroll
         for (int kt = 0; kt < 6; ++kt)
           acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[c][kt], a[kt], acc, 0, 0, 0);
-        v4i o = qkv_epi<LA>(g, acc, b4, rq);
+        v4i o = qkv_epi<LA>(g, acc, b4, rq, all_narrow);
         if (r >= N) o = v4i{0};
         const int ch = c * 32 + 16 * hh;  // channel within the head
         if (r < rows_k) *reinterpret_cast<v4i *>(&(p == 0 ? Qs : Ks)[r * kKStride + ch]) = o;
@@ -518,35 +523,36 @@ __device__ __forceinline__ void attn_tiles(const AttnArgs &g, const int8_t *Ks, 
     for (int kt = 0; kt < NT; ++kt) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const unsigned e = softmax_exp_nx((unsigned)(mx - st[kt][i]));
+        const unsigned e = softmax_exp_t(max(st[kt][i] - mx, -17 * 45426));
         st[kt][i] = (int)e;
         sum += e;
       }
     }
     sum += __shfl_xor(sum, 16);
     sum += __shfl_xor(sum, 32);
-    const unsigned recip = softmax_recip24(sum);  // sum <= 197 * 65554 < 2^24
+    const unsigned r256 = softmax_recip24(sum) << 8;  // sum <= 197 * 65554 < 2^24
     v4i pk[NC];
 #pragma unroll
     for (int kc = 0; kc < NC; ++kc) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int kt = kc * 4 + t;
-        unsigned w = 0;
+        unsigned w = 0x80808080u;  // keys past the tiles: P = 0
         if (kt < NT) {
+          // the bytes P - 128 (softmax_prob_m128), packed by byte permutes
+          unsigned pm[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            // min(rsa(rsa(e * recip, 16), 8), 255) with one rounding: the
-            // first rounding's discarded bits cannot carry past a multiple
-            // of 2^8, so it equals (e * recip + 2^15 + 2^23) >> 24.
-            const u64 pr = (u64)(unsigned)st[kt][i] * recip + (32768u + (1u << 23));
-            const unsigned p = min((unsigned)(pr >> 24), 255u);
-            w |= p << (8 * i);
+            pm[i] = (unsigned)softmax_prob_m128((unsigned)st[kt][i], r256);
             if (CKPT && g.prob && q < N && kt * 16 + 4 * grp + i < N)
-              g.prob[(((size_t)b * 3 + h) * 197 + q) * 197 + kt * 16 + 4 * grp + i] = (uint8_t)p;
+              g.prob[(((size_t)b * 3 + h) * 197 + q) * 197 + kt * 16 + 4 * grp + i] =
+                  (uint8_t)(pm[i] + 128);
           }
+          w = __builtin_amdgcn_perm(__builtin_amdgcn_perm(pm[3], pm[2], 0x0c0c0400u),
+                                    __builtin_amdgcn_perm(pm[1], pm[0], 0x0c0c0400u),
+                                    0x05040100u);
         }
-        pk[kc][t] = (int)(w ^ 0x80808080u);  // bytes P - 128
+        pk[kc][t] = (int)w;
         // keeps the scheduler from hoisting every tile's 64-bit products
         // at once (register pressure, spills)
         __builtin_amdgcn_sched_barrier(0);

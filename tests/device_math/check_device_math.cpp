@@ -88,6 +88,22 @@ static long check_exp_nx() {
   return bad;
 }
 
+// softmax_exp_t(max(x, -17 * 45426)) against the oracle's exp of x for
+// every x in [-2^25, 0] (all 772,243 clamped arguments and beyond) and a
+// million larger magnitudes.
+static long check_exp_t() {
+  long bad = 0;
+  auto one = [&](int x) {
+    const int t = x > -17 * 45426 ? x : -17 * 45426;
+    if ((long long)softmax_exp_t(t) != hvo_softmax_exp(x))
+      if (++bad < 5) std::printf("softmax_exp_t mismatch at %d\n", x);
+  };
+  for (int x = -(1 << 25); x <= 0; ++x) one(x);
+  std::mt19937_64 rng(11);
+  for (int i = 0; i < 1000000; ++i) one(-(int)(rng() % 2147483647u));
+  return bad;
+}
+
 static long check_softmax(int rows) {
   std::mt19937_64 rng(3);
   int32_t x[256], ref_sel[256];
@@ -113,7 +129,9 @@ static long check_softmax(int rows) {
       // attention narrowing in one rounding, as the attention kernel does it
       const unsigned long long pr = (unsigned long long)e[i] * recip + 32768u + (1u << 23);
       const unsigned p1 = (unsigned)(pr >> 24) > 255u ? 255u : (unsigned)(pr >> 24);
-      if (prob_u8(ratio) != ref_att[i] || p1 != ref_att[i] ||
+      // and as the signed P - 128 operand from one multiply-add
+      const int pm = softmax_prob_m128(e[i], recip << 8);
+      if (prob_u8(ratio) != ref_att[i] || p1 != ref_att[i] || pm + 128 != (int)ref_att[i] ||
           (int)(ratio > 65536u ? 65536u : ratio) != ref_sel[i])
         if (++bad < 5) std::printf("softmax mismatch row %d col %d\n", it, i);
     }
@@ -168,7 +186,7 @@ static long check_layernorm(int rows) {
 int main(int argc, char **argv) {
   const int rows = argc > 1 ? std::atoi(argv[1]) : 100000;
   const long g = check_gelu(),
-             s = check_softmax(rows) + check_recip24() + check_exp() + check_exp_nx(),
+             s = check_softmax(rows) + check_recip24() + check_exp() + check_exp_nx() + check_exp_t(),
              l = check_layernorm(rows);
   std::printf("gelu_bad=%ld softmax_bad=%ld layernorm_bad=%ld\n", g, s, l);
   return (g || s || l) ? 1 : 0;
