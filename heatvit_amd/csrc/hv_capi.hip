@@ -503,14 +503,12 @@ int hv_block_forward(const hv_block_dev *p, const int8_t *x, const int32_t *offs
 }
 
 struct SelectorWs {
-  int32_t *hs;
-  int8_t *stats;
+  int8_t *pkg_rows;
 };
 
 static SelectorWs carve_selector(Carve &cv, int batch) {
   SelectorWs w;
-  w.hs = cv.take<int32_t>((size_t)batch * 3 * 196);
-  w.stats = cv.take<int8_t>((size_t)batch * 196 * 3);
+  w.pkg_rows = cv.take<int8_t>((size_t)batch * 192);
   return w;
 }
 
@@ -535,8 +533,7 @@ int hv_selector_forward(const hv_selector_dev *p, const int8_t *tokens, const in
   const SelectorWs w = carve_selector(cv, batch);
   if (!cv.ok || !workspace) return fail(HV_EVALUE, HV_ERR_ADDRESS, "selector: workspace too small");
   SelectorArgs a{};
-  a.hs = w.hs;
-  a.stats = w.stats;
+  a.pkg_rows = w.pkg_rows;
   a.p = p; a.tokens = tokens; a.offsets = offsets; a.pkg_in = pkg_in; a.batch = batch;
   a.out_tokens = out_tokens; a.out_offsets = out_offsets; a.pkg_out = pkg_out; a.fused = fused;
   a.kept_index = kept_index; a.state = state;
@@ -551,7 +548,7 @@ namespace hv {
 // HV_SELECTOR_NOALLOC_MAX_BATCH images.  Host code never uses the array's
 // name as an address: each device's copy is found once with
 // hipGetSymbolAddress (with that device current) and kept per device.
-static constexpr size_t kNoAllocScratchBytes = 3 * 1024 * 1024;
+static constexpr size_t kNoAllocScratchBytes = 256 * 1024;
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 static constexpr int kMaxDevices = 64;
 static void *g_scratch_ptr[kMaxDevices];
@@ -588,7 +585,7 @@ int hv_selector_forward_noalloc(const hv_selector_dev *p, const int8_t *tokens,
     return fail(HV_EVALUE, HV_ERR_DIMENSION,
                 "selector noalloc: batch %d exceeds the fixed scratch's %d images", batch,
                 HV_SELECTOR_NOALLOC_MAX_BATCH);
-  static_assert(kNoAllocScratchBytes >= (size_t)HV_SELECTOR_NOALLOC_MAX_BATCH * 196 * 3 * 5 + 512,
+  static_assert(kNoAllocScratchBytes >= (size_t)HV_SELECTOR_NOALLOC_MAX_BATCH * 192 + 256,
                 "scratch holds the selector workspace of the largest batch");
   if (batch <= 0) return hv_selector_forward(p, tokens, offsets, pkg_in, batch, out_tokens,
                                              out_offsets, pkg_out, fused, kept_index, state, ck,
@@ -731,7 +728,7 @@ static int model_forward(const hv_model_dev *p, const void *images, bool float_i
       a.tokens = w.xa; a.offsets = w.off_a; a.pkg_in = w.pkg_a; a.batch = batch;
       a.out_tokens = w.xb; a.out_offsets = w.off_b; a.pkg_out = w.pkg_b;
       a.fused = w.fused; a.kept_index = w.kept; a.state = st + (size_t)sel * batch * 5;
-      a.hs = w.sel.hs; a.stats = w.sel.stats;
+      a.pkg_rows = w.sel.pkg_rows;
       a.token_counts = token_counts; a.stage = sel + 1; a.img_warn = warnings;
       {
         ProfScope ps(HV_PROF_SELECTOR, s);

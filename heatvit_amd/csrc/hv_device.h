@@ -82,6 +82,19 @@ __host__ __device__ __forceinline__ i64 round_div_pos(i64 num, i64 den) {
   return num < 0 ? -(i64)q : (i64)q;
 }
 
+// round_div_pos for |num| < 2^52 and 0 < den < 2^52 from one double
+// quotient: num and den are exact in double, and when num / den is not an
+// integer its distance to the next integer (at least 1 / den) exceeds the
+// quotient's rounding error (at most num / den * 2^-53 < 1 / den), so the
+// truncated double quotient is floor(num / den); the remainder test rounds.
+__host__ __device__ __forceinline__ i64 round_div_pos_d(i64 num, i64 den) {
+  const u64 mag = num < 0 ? (u64)(-num) : (u64)num;
+  u64 q = (u64)((double)mag / (double)den);
+  const u64 r = mag - q * (u64)den;
+  if (2 * r >= (u64)den) q += 1;
+  return num < 0 ? -(i64)q : (i64)q;
+}
+
 // _align_add_requant (transformer.py:96-101): both operands int8.  The
 // aligned sum needs more than 64 bits only when the exponents differ by
 // more than 54; that case takes the 128-bit route.

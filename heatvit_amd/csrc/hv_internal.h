@@ -188,8 +188,7 @@ struct SelectorArgs {
   int32_t *fused;       // [B][196]
   int32_t *kept_index;  // [B][196]
   int32_t *state;       // [B][5]
-  int32_t *hs;          // workspace [B][3][196] head scores (selector forward)
-  int8_t *stats;        // workspace [B][196][3] head statistics
+  int8_t *pkg_rows;     // workspace [B][192]: package rows (selector forward)
   int32_t *token_counts;  // optional [B][4] column `stage`
   int stage;
   int32_t *img_warn;      // optional [B]: the state's warning bits are ORed in

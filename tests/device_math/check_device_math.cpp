@@ -104,6 +104,24 @@ static long check_exp_t() {
   return bad;
 }
 
+// round_div_pos_d (one double quotient) against round_div_pos over random
+// operands of every magnitude below 2^52, the selector's ranges included.
+static long check_round_div_d() {
+  std::mt19937_64 rng(12);
+  long bad = 0;
+  for (int i = 0; i < 4000000; ++i) {
+    const int nb = 1 + (int)(rng() % 52), db = 1 + (int)(rng() % 52);
+    long long num = (long long)(rng() & ((1ull << nb) - 1));
+    long long den = (long long)(rng() & ((1ull << db) - 1));
+    if (den == 0) den = 1;
+    if (i % 5 == 0) num = den * (long long)(rng() % 1000) + (long long)(den / 2);  // ties
+    if (rng() & 1) num = -num;
+    if (round_div_pos_d(num, den) != round_div_pos(num, den))
+      if (++bad < 5) std::printf("round_div_pos_d mismatch %lld / %lld\n", num, den);
+  }
+  return bad;
+}
+
 static long check_softmax(int rows) {
   std::mt19937_64 rng(3);
   int32_t x[256], ref_sel[256];
@@ -187,7 +205,7 @@ int main(int argc, char **argv) {
   const int rows = argc > 1 ? std::atoi(argv[1]) : 100000;
   const long g = check_gelu(),
              s = check_softmax(rows) + check_recip24() + check_exp() + check_exp_nx() + check_exp_t(),
-             l = check_layernorm(rows);
+             l = check_layernorm(rows) + check_round_div_d();
   std::printf("gelu_bad=%ld softmax_bad=%ld layernorm_bad=%ld\n", g, s, l);
   return (g || s || l) ? 1 : 0;
 }

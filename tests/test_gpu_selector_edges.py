@@ -119,3 +119,36 @@ def test_finalize_rejects_out_of_range_scores(oracle, bad):
         assert st[i, 0] == wst.token_count
         assert np.array_equal(out[o[i]:o[i + 1]], want), i
         assert np.array_equal(kept.cpu().numpy()[i, :st[i, 2]], want_kept), i
+
+
+def test_selector_1024_images_vs_oracle(oracle):
+    """hv_selector_forward over 1,024 ragged token sets (2 to 197 tokens,
+    every eighth with an incoming package, some near the keep threshold's
+    edges) against the oracle: every image's output offset sums the counts
+    of all images before it, so every image's rows must land at the right
+    place."""
+    from heatvit_amd.selector import token_selector_batch
+    tokens, sp = synth.selector_workload()
+    rng = np.random.default_rng(1024)
+    sets, flags = [], []
+    for i in range(1024):
+        n = int(rng.integers(2, 198)) if i % 5 else 197
+        f = i % 8 == 3 and n >= 3
+        base = tokens[i % len(tokens)]
+        t = base[:n].copy()
+        if i % 3 == 1:  # fresh rows so images differ beyond the 64 base sets
+            t[1:] = rng.integers(-128, 128, (n - 1, 192), dtype=np.int16).astype(np.int8)
+        sets.append(t)
+        flags.append(f)
+    print("selector 1024 images", flush=True)
+    res = token_selector_batch(sets, flags, sp)
+    kept_total = 0
+    for i, (t, f) in enumerate(zip(sets, flags)):
+        want = oracle.token_selector(t, f, sp, checkpoints=False)
+        r = res[i]
+        assert r.token_count == want["token_count"], i
+        assert np.array_equal(r.tokens, want["tokens"]), i
+        assert np.array_equal(r.kept_index, want["kept_index"]), i
+        assert r.warnings == want["warnings"], i
+        kept_total += r.kept_normal_count
+    assert 0 < kept_total < sum(len(t) - 1 for t in sets)
