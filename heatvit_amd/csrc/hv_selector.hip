@@ -1,7 +1,7 @@
 // hv_selector.hip -- token selector (selector.token_selector,
 // selector.py:503-563) over a ragged batch.
 //
-// k_selector_image, one 512-thread workgroup per image (XCD-major): the
+// k_selector_image, one 1024-thread workgroup per image (XCD-major): the
 //   three heads' local MLP + head statistic (:253, :358), candidate mean
 //   (:273), concat + 64->32->16->2 score MLP + 2-way selector softmax
 //   (:292, :307, :338) as int8 MFMAs over tiles of 16 candidates, every
@@ -120,40 +120,41 @@ __device__ __forceinline__ void state_invalid(int32_t *st) {
   st[0] = -1; st[1] = 0; st[2] = 0; st[3] = 0; st[4] = 0;
 }
 
-// Head fuse of one candidate (selector.py:370-418): head-weight MLP (3->3
-// GELU, 3->3 PLAN) on the head statistics stats[0..2] and the weighted mean
-// of the head scores hs[0], hs[kMaxCand], hs[2 * kMaxCand]; *warn is set
-// when the weights sum to zero (plain mean then).
-__device__ int fuse_candidate(const hv_selector_dev &p, const int8_t *stats, const int32_t *hs,
-                              int32_t *weights_out, bool *warn) {
+// Head fuse (selector.py:370-418), in three steps over one thread per
+// candidate and head-weight unit: the head-weight MLP's GELU layer on the
+// head statistics (3 -> 3), its PLAN layer (3 -> 3), and the weighted mean
+// of the head scores (plain mean, and the warning, when the weights sum to
+// zero).  The biases are any int32 and the reference adds them in int64
+// (gemm.py:118-119): the three products (|sum| < 2^16) are summed in 32
+// bits and the bias added in 64; the empty asm keeps the compiler from
+// folding bias and products into one 32-bit dot-product accumulation, which
+// wraps for biases near the int32 limits.
+__device__ __forceinline__ int fuse_hidden(const hv_selector_dev &p, const int8_t *stats, int j) {
   const int a_in = -16 - (p.stats_out_exp + p.hw_w1_exp), a_out = p.hw_hidden_out_exp + 16;
+  int dot = 0;
+#pragma unroll
+  for (int k = 0; k < 3; ++k) dot += (int)stats[k] * (int)p.hw_w1t[j * 3 + k];
+  asm volatile("" : "+v"(dot));
+  return gelu_post((i64)p.hw_b1[j] + dot, a_in, a_out);
+}
+
+__device__ __forceinline__ int fuse_weight(const hv_selector_dev &p, const int *hid, int j) {
   const int b_sh = -16 - (p.hw_hidden_out_exp + p.hw_w2_exp);
-  int hid[3];
+  int dot = 0;
 #pragma unroll
-  for (int j = 0; j < 3; ++j) {
-    // The bias is any int32 and the reference adds it in int64
-    // (gemm.py:118-119): the three products (|sum| < 2^16) are summed in
-    // 32 bits and the bias added in 64.  The empty asm keeps the compiler
-    // from folding bias and products into one 32-bit dot-product
-    // accumulation, which wraps for biases near the int32 limits.
-    int dot = 0;
-#pragma unroll
-    for (int k = 0; k < 3; ++k) dot += (int)stats[k] * (int)p.hw_w1t[j * 3 + k];
-    asm volatile("" : "+v"(dot));
-    hid[j] = gelu_post((i64)p.hw_b1[j] + dot, a_in, a_out);
-  }
+  for (int k = 0; k < 3; ++k) dot += hid[k] * (int)p.hw_w2t[j * 3 + k];
+  asm volatile("" : "+v"(dot));
+  return sat_q016(plan_sigmoid((int)requant_shift((i64)p.hw_b2[j] + dot, b_sh, 24)));
+}
+
+// hs[0], hs[kMaxCand], hs[2 * kMaxCand]: the candidate's head scores; w[0..2]
+// its head weights.
+__device__ __forceinline__ int fuse_mean(const int32_t *hs, const int *w, bool *warn) {
   i64 num = 0, den = 0;
 #pragma unroll
   for (int j = 0; j < 3; ++j) {
-    int dot = 0;
-#pragma unroll
-    for (int k = 0; k < 3; ++k) dot += hid[k] * (int)p.hw_w2t[j * 3 + k];
-    asm volatile("" : "+v"(dot));
-    const i64 acc = (i64)p.hw_b2[j] + dot;
-    const int w = sat_q016(plan_sigmoid((int)requant_shift(acc, b_sh, 24)));
-    if (weights_out) weights_out[j] = w;
-    num += (i64)hs[j * kMaxCand] * w;
-    den += w;
+    num += (i64)hs[j * kMaxCand] * w[j];
+    den += w[j];
   }
   *warn = den == 0;
   if (den == 0) {
@@ -170,20 +171,22 @@ __device__ int fuse_candidate(const hv_selector_dev &p, const int8_t *stats, con
 // 32768) in input order, ki[kept .. 196) = -1, and the state {token_count,
 // package_present, kept, pruned, warnings}; bad (any thread) marks the
 // image invalid (state token count -1).  Returns the kept count, or -1 when
-// the image is invalid.
+// the image is invalid; *den_out receives the sum of the partitioned
+// candidates' scores (the package's divisor).
 template <int NT>
 __device__ __forceinline__ int keep_list(int C, int pkg, int fc, bool warn, bool bad, int32_t *ki,
-                                         int32_t *st) {
+                                         int32_t *st, i64 *den_out = nullptr) {
   constexpr int NWAVE = NT / 64;
-  __shared__ int w_kept[NWAVE], w_flags[NWAVE];
-  __shared__ i64 w_den[NWAVE];
+  __shared__ int w_kept[NWAVE], w_flags[NWAVE], w_den[NWAVE];
   const int c = threadIdx.x, lane = c & 63, wave = c >> 6;
   const int n_norm = C - pkg;
   const bool is_norm = c < n_norm;
   const bool keep = is_norm && fc >= 32768;
   const bool part = (is_norm && !keep) || (pkg && c == C - 1);
   const u64 mask = __ballot(keep);
-  i64 d = part ? fc : 0;
+  // valid scores are at most 65536, so a wavefront's sum fits 32 bits (an
+  // invalid image is rejected below before the sum is used)
+  int d = part ? fc : 0;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) d += __shfl_xor(d, off);
   const int flags = (__ballot(warn) != 0 ? 1 : 0) | (__ballot(bad) != 0 ? 2 : 0);
@@ -206,6 +209,7 @@ __device__ __forceinline__ int keep_list(int C, int pkg, int fc, bool warn, bool
     if (c == 0) state_invalid(st);
     return -1;
   }
+  if (den_out) *den_out = den;
   if (keep) ki[before] = c;
   if (c >= kept && c < kMaxCand) ki[c] = -1;
   if (c == 0) {
@@ -225,46 +229,39 @@ __device__ __forceinline__ int keep_list(int C, int pkg, int fc, bool warn, bool
 // Package token of one image (selector.py:470-500): dst[ch] = sat8(
 // round_div(sum_c w_c x_c[ch], sum_c w_c)) over the pruned normals and the
 // incoming package with w_c = fused score, or their plain mean (w_c = 1,
-// divisor n_part) when those scores sum to zero.  |num| <= 196 * 65536 *
+// divisor n_part) when those scores sum to zero (den: the scores' sum, from
+// keep_list).  |num| <= 196 * 65536 *
 // 128 < 2^31.  Thread c holds candidate c's fused score fv; thread (channel
-// group of 16, candidate group g) accumulates candidates g, g + 21, ... (its
-// candidate rows loaded at once, weight 0 for kept ones) and part_sum
-// ([21][192] ints) sums the groups.  Every thread of the NT-thread
-// workgroup calls it; cand points at candidate 0's row (16-byte aligned
-// rows, RS bytes apart, in memory or LDS).
-template <int NT, int RS>
+// group of 16, candidate group g < G) accumulates candidates g, g + G, ...
+// (its candidate rows loaded at once, weight 0 for kept ones) and part_sum
+// ([G][192] ints) sums the groups.  Every thread of the NT-thread workgroup
+// calls it; cand points at candidate 0's row (16-byte aligned rows, RS
+// bytes apart, in memory or LDS).
+template <int NT, int RS, int G>
 __device__ __forceinline__ void package_row(const int8_t *cand, int C, int pkg, int kept, int fv,
-                                            int8_t *dst, int *wgt, int *part_sum) {
-  constexpr int NWAVE = NT / 64, kSteps = (kMaxCand + 20) / 21;
-  __shared__ i64 den_part[NWAVE];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+                                            i64 den, int8_t *dst, int *wgt, int *part_sum) {
+  constexpr int kSteps = (kMaxCand + G - 1) / G;
+  static_assert(12 * G <= NT, "one thread per channel group and candidate group");
+  const int tid = threadIdx.x;
   const int cg = tid / 12, chg = tid - cg * 12;
   v4i xv[kSteps];
-  if (tid < 12 * 21) {
+  if (tid < 12 * G) {
     const int8_t *cp = cand + chg * 16;
 #pragma unroll
     for (int j = 0; j < kSteps; ++j)
-      xv[j] = *reinterpret_cast<const v4i *>(cp + (size_t)min(cg + 21 * j, C - 1) * RS);
+      xv[j] = *reinterpret_cast<const v4i *>(cp + (size_t)min(cg + G * j, C - 1) * RS);
   }
   const int n_norm = C - pkg;
   const bool part = tid < C && ((tid < n_norm && fv < 32768) || (pkg && tid == C - 1));
-  i64 d = part ? fv : 0;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) d += __shfl_xor(d, off);
-  if (lane == 0) den_part[wave] = d;
-  __syncthreads();
-  i64 den = 0;
-#pragma unroll
-  for (int w = 0; w < NWAVE; ++w) den += den_part[w];
   if (tid < C) wgt[tid] = part ? (den == 0 ? 1 : fv) : 0;
   __syncthreads();
-  if (tid < 12 * 21) {
+  if (tid < 12 * G) {
     int acc[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc[j] = 0;
 #pragma unroll
     for (int j = 0; j < kSteps; ++j) {
-      const int c = cg + 21 * j;
+      const int c = cg + G * j;
       const int w = c < C ? wgt[c] : 0;
 #pragma unroll
       for (int k = 0; k < 16; ++k) acc[k] += w * (int)(int8_t)(xv[j][k >> 2] >> (8 * (k & 3)));
@@ -277,12 +274,18 @@ __device__ __forceinline__ void package_row(const int8_t *cand, int C, int pkg, 
   if (tid < 192) {
     int num = 0;
 #pragma unroll
-    for (int g = 0; g < 21; ++g) num += part_sum[g * 192 + tid];
+    for (int g = 0; g < G; ++g) num += part_sum[g * 192 + tid];
     dst[tid] = (int8_t)sat_bits(round_div_pos_d(num, den == 0 ? n_part : den), 8);
   }
 }
 
-constexpr int kImgThreads = 512, kXsRow = 208;
+constexpr int kImgThreads = 1024, kXsRow = 208;
+
+// The low bytes of four words as one word (byte permutes).
+__device__ __forceinline__ unsigned pack_lo4(unsigned a, unsigned b, unsigned c, unsigned d) {
+  return __builtin_amdgcn_perm(__builtin_amdgcn_perm(d, c, 0x0c0c0400u),
+                               __builtin_amdgcn_perm(b, a, 0x0c0c0400u), 0x05040100u);
+}
 
 // One workgroup per image (XCD-major).  Per layer, the (head, tile) units of
 // the three heads run over the eight wavefronts; the layer's GELU step table
@@ -292,8 +295,9 @@ constexpr int kImgThreads = 512, kXsRow = 208;
 //   h2    = GELU(h1 . W2 + b2)                       16x16x32, 1 column tile
 // where b1' = b1 + global . W1[32:64] (the global feature is the same for
 // every candidate, so the concat's second half is a per-head bias, exact in
-// 64 bits).  Result lane l of a tile holds output channel 16 ct + l % 16 of
-// candidates 4 (l / 16) + i.  Logits (16 -> 2), the 2-way softmax and the
+// 64 bits).  With the weights as the MFMA's first operand, result lane l of
+// a tile holds output channels 16 ct + 4 (l / 16) + i of candidate l % 16,
+// stored as one word.  Logits (16 -> 2), the 2-way softmax and the
 // lane mean of the head slice (the head statistic) are per candidate; the
 // head fuse, the keep list and the package token follow in the same
 // workgroup.  The package row goes to pkg_rows[b] for k_selector_compact.
@@ -310,23 +314,22 @@ __global__ __launch_bounds__(kImgThreads) void k_selector_image(
   __shared__ int w3[3][8];                                         // w3t[h] [2][16] as words
   __shared__ int bl[3][32], bb2[3][16];
   __shared__ i64 bb1[3][32];                                       // b1 + global . W1[32:64]
-  // local [3][208][32], then h2 [3][208][16]; h1 [3][208][32], then the
-  // package's partial sums [21][192] ints
+  // local [3][208][32], then h2 [3][208][16]; h1 [3][208][32]
   __shared__ __attribute__((aligned(16))) int8_t act_a[3 * kCandPad * 32];
   __shared__ __attribute__((aligned(16))) int8_t act_b[3 * kCandPad * 32];
   __shared__ int hs_s[3 * kMaxCand];                               // head scores [h][c]
   __shared__ int8_t st_s[kMaxCand * 3];                            // head statistics [c][h]
-  __shared__ int part[5][96];
+  __shared__ int part[10][96];
   __shared__ int glob_s[3][32];
   __shared__ int fast_s[3][3];
   __shared__ int wgt[kMaxCand];
   // the image's candidate rows, 208-byte stride (conflict-free 16-byte
   // fragment reads of 16 consecutive rows)
   __shared__ __attribute__((aligned(16))) int8_t xs[kMaxCand * kXsRow];
-  static_assert(21 * 192 * 4 <= (int)sizeof(act_b), "package sums fit the h1 buffer");
 
   const int b = xcd_image(batch);
   if (b < 0) return;  // uniform: before any barrier
+  constexpr int NW = NT / 64;  // wavefronts; each takes two units per round, NW apart
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, col = lane & 15, grp = lane >> 4;
   const int row0 = offsets[b], N = offsets[b + 1] - row0, C = N - 1;
   const int pkg = pkg_in ? (pkg_in[b] ? 1 : 0) : 0;
@@ -389,15 +392,15 @@ __global__ __launch_bounds__(kImgThreads) void k_selector_image(
     const Rq ra = rq_setup(sh_in, -(1 << 23), (1 << 23) - 1), rb = rq_setup(sh_out, -128, 127);
     __syncthreads();
     const int nt2 = ntiles * 2, nu = 3 * nt2;
-    for (int u0 = wave; u0 < nu; u0 += 16) {
+    for (int u0 = wave; u0 < nu; u0 += 2 * NW) {
       int hh[2], tv[2];
       bool valid[2], fast[2];
       v4i a[2], acc[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const int uu = min(u0 + 8 * u, nu - 1);
-        valid[u] = u0 + 8 * u < nu;
-        hh[u] = uu / nt2;
+        const int uu = min(u0 + NW * u, nu - 1);
+        valid[u] = u0 + NW * u < nu;
+        hh[u] = (uu >= nt2 ? 1 : 0) + (uu >= 2 * nt2 ? 1 : 0);  // uu / nt2 (< 3)
         tv[u] = uu - hh[u] * nt2;
         fast[u] = fast_s[hh[u]][0];
         const int c = min((tv[u] >> 1) * 16 + col, C - 1);
@@ -407,7 +410,9 @@ __global__ __launch_bounds__(kImgThreads) void k_selector_image(
       for (int u = 0; u < 2; ++u) {
         const v4i wb =
             *reinterpret_cast<const v4i *>(&wl[hh[u]][((tv[u] & 1) * 16 + col) * 64 + grp * 16]);
-        acc[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], wb, v4i{0}, 0, 0, 0);
+        // weights as the first operand: lane (col, grp) gets output channels
+        // 16 ct + 4 grp + i of candidate 16 rt + col, stored as one word
+        acc[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wb, a[u], v4i{0}, 0, 0, 0);
       }
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
@@ -431,34 +436,33 @@ __global__ __launch_bounds__(kImgThreads) void k_selector_image(
         unsigned ov[8];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          const int j = (tv[u] & 1) * 16 + col;
+          const int jb = (tv[u] & 1) * 16 + 4 * grp;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) qv[4 * u + i] = rq(acc[u][i] + bl[hh[u]][j], ra);
+          for (int i = 0; i < 4; ++i) qv[4 * u + i] = rq(acc[u][i] + bl[hh[u]][jb + i], ra);
         }
         gelu_table_u8_n<8>(qv, ov, lut, tl.cb, tl.qlo, tl.qhi);
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          const int rt = tv[u] >> 1, j = (tv[u] & 1) * 16 + col;
-          if (valid[u]) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              act_a[(hh[u] * kCandPad + rt * 16 + grp * 4 + i) * 32 + j] = (int8_t)ov[4 * u + i];
-          }
+          const int rt = tv[u] >> 1, jb = (tv[u] & 1) * 16 + 4 * grp;
+          if (valid[u])
+            *reinterpret_cast<unsigned *>(&act_a[(hh[u] * kCandPad + rt * 16 + col) * 32 + jb]) =
+                pack_lo4(ov[4 * u], ov[4 * u + 1], ov[4 * u + 2], ov[4 * u + 3]);
         }
       } else {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          const int rt = tv[u] >> 1, j = (tv[u] & 1) * 16 + col;
+          const int rt = tv[u] >> 1, jb = (tv[u] & 1) * 16 + 4 * grp;
           if (valid[u]) {
+            unsigned o[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int v = fast[u] && tl.off >= 0
-                                ? (int)(int8_t)gelu_table_u8(rq(acc[u][i] + bl[hh[u]][j], ra),
-                                                             lut, tl.cb, tl.qlo, tl.qhi)
-                                : sel_gelu(acc[u][i], bl[hh[u]][j], fast[u], ra, rb, sh_in,
-                                           sh_out);
-              act_a[(hh[u] * kCandPad + rt * 16 + grp * 4 + i) * 32 + j] = (int8_t)v;
-            }
+            for (int i = 0; i < 4; ++i)
+              o[i] = (unsigned)(fast[u] && tl.off >= 0
+                                    ? (int)gelu_table_u8(rq(acc[u][i] + bl[hh[u]][jb + i], ra),
+                                                         lut, tl.cb, tl.qlo, tl.qhi)
+                                    : sel_gelu(acc[u][i], bl[hh[u]][jb + i], fast[u], ra, rb,
+                                               sh_in, sh_out));
+            *reinterpret_cast<unsigned *>(&act_a[(hh[u] * kCandPad + rt * 16 + col) * 32 + jb]) =
+                pack_lo4(o[0], o[1], o[2], o[3]);
           }
         }
       }
@@ -469,10 +473,10 @@ __global__ __launch_bounds__(kImgThreads) void k_selector_image(
   if (t1.off >= 0) lut_store<NT>(t1, lv, lut, tid);
   // Global features = sat8(round_div(sum_c local, C)) per head and channel,
   // five partial sums each; the local checkpoint before act_a is reused.
-  if (tid < 5 * 96) {
+  if (tid < 10 * 96) {
     const int prt = tid / 96, hc = tid - prt * 96, h = hc >> 5, ch = hc & 31;
     int sacc = 0;
-    for (int c = prt; c < C; c += 5) sacc += act_a[(h * kCandPad + c) * 32 + ch];
+    for (int c = prt; c < C; c += 10) sacc += act_a[(h * kCandPad + c) * 32 + ch];
     part[prt][hc] = sacc;
   }
   if (ck.local)
@@ -483,7 +487,9 @@ __global__ __launch_bounds__(kImgThreads) void k_selector_image(
     }
   __syncthreads();
   if (tid < 96) {
-    const int sacc = part[0][tid] + part[1][tid] + part[2][tid] + part[3][tid] + part[4][tid];
+    int sacc = 0;
+#pragma unroll
+    for (int q = 0; q < 10; ++q) sacc += part[q][tid];
     const int gv = (int)sat_bits(round_div_pos_d(sacc, C), 8);
     glob_s[tid >> 5][tid & 31] = gv;
     if (ck.global) ck.global[((size_t)b * 3 + (tid >> 5)) * 32 + (tid & 31)] = (int8_t)gv;
@@ -513,15 +519,15 @@ __global__ __launch_bounds__(kImgThreads) void k_selector_image(
     __syncthreads();
     if (t2.off >= 0) lut_load<NT>(t2, lv, tid);  // score layer 2's table
     const int nt2 = ntiles * 2, nu = 3 * nt2;
-    for (int u0 = wave; u0 < nu; u0 += 16) {
+    for (int u0 = wave; u0 < nu; u0 += 2 * NW) {
       int hh[2], tv[2];
       bool valid[2], fast[2];
       v4i acc[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const int uu = min(u0 + 8 * u, nu - 1);
-        valid[u] = u0 + 8 * u < nu;
-        hh[u] = uu / nt2;
+        const int uu = min(u0 + NW * u, nu - 1);
+        valid[u] = u0 + NW * u < nu;
+        hh[u] = (uu >= nt2 ? 1 : 0) + (uu >= 2 * nt2 ? 1 : 0);  // uu / nt2 (< 3)
         tv[u] = uu - hh[u] * nt2;
         fast[u] = fast_s[hh[u]][1];
         const int rt = tv[u] >> 1, ct = tv[u] & 1;
@@ -529,44 +535,45 @@ __global__ __launch_bounds__(kImgThreads) void k_selector_image(
             &act_a[(hh[u] * kCandPad + rt * 16 + col) * 32 + grp * 8]);
         const long wb =
             *reinterpret_cast<const long *>(&w1[hh[u]][(ct * 16 + col) * 64 + grp * 8]);
-        acc[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, wb, v4i{0}, 0, 0, 0);
+        // weights first: four channels of one candidate per lane
+        acc[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(wb, a, v4i{0}, 0, 0, 0);
       }
       if (fast[0] && fast[1] && t1.off >= 0) {
         int qv[8];
         unsigned ov[8];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          const int bias = (int)bb1[hh[u]][(tv[u] & 1) * 16 + col];
+          const int jb = (tv[u] & 1) * 16 + 4 * grp;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) qv[4 * u + i] = rq(acc[u][i] + bias, ra);
+          for (int i = 0; i < 4; ++i) qv[4 * u + i] = rq(acc[u][i] + (int)bb1[hh[u]][jb + i], ra);
         }
         gelu_table_u8_n<8>(qv, ov, lut, t1.cb, t1.qlo, t1.qhi);
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          int8_t *dst = &act_b[(hh[u] * kCandPad + (tv[u] >> 1) * 16 + grp * 4) * 32 +
-                               (tv[u] & 1) * 16 + col];
-          if (valid[u]) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) dst[i * 32] = (int8_t)ov[4 * u + i];
-          }
+          const int jb = (tv[u] & 1) * 16 + 4 * grp;
+          if (valid[u])
+            *reinterpret_cast<unsigned *>(
+                &act_b[(hh[u] * kCandPad + (tv[u] >> 1) * 16 + col) * 32 + jb]) =
+                pack_lo4(ov[4 * u], ov[4 * u + 1], ov[4 * u + 2], ov[4 * u + 3]);
         }
       } else {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          const i64 bias = bb1[hh[u]][(tv[u] & 1) * 16 + col];
-          int8_t *dst = &act_b[(hh[u] * kCandPad + (tv[u] >> 1) * 16 + grp * 4) * 32 +
-                               (tv[u] & 1) * 16 + col];
+          const int jb = (tv[u] & 1) * 16 + 4 * grp;
           if (valid[u]) {
+            unsigned o[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const int v =
-                  fast[u] && t1.off >= 0
-                      ? (int)(int8_t)gelu_table_u8(rq(acc[u][i] + (int)bias, ra), lut, t1.cb,
-                                                   t1.qlo, t1.qhi)
-                  : fast[u] ? rq(gelu_q16(rq(acc[u][i] + (int)bias, ra)), rb)
-                            : gelu_exact64(acc[u][i], bias, sh_in, sh_out);
-              dst[i * 32] = (int8_t)v;
+              const i64 bias = bb1[hh[u]][jb + i];
+              o[i] = (unsigned)(fast[u] && t1.off >= 0
+                                    ? (int)gelu_table_u8(rq(acc[u][i] + (int)bias, ra), lut,
+                                                         t1.cb, t1.qlo, t1.qhi)
+                                : fast[u] ? rq(gelu_q16(rq(acc[u][i] + (int)bias, ra)), rb)
+                                          : gelu_exact64(acc[u][i], bias, sh_in, sh_out));
             }
+            *reinterpret_cast<unsigned *>(
+                &act_b[(hh[u] * kCandPad + (tv[u] >> 1) * 16 + col) * 32 + jb]) =
+                pack_lo4(o[0], o[1], o[2], o[3]);
           }
         }
       }
@@ -583,21 +590,21 @@ __global__ __launch_bounds__(kImgThreads) void k_selector_image(
     const int sh_in = -16 - (p.h1_out_exp + p.score_w2_exp), sh_out = p.h2_out_exp + 16;
     const Rq ra = rq_setup(sh_in, -(1 << 23), (1 << 23) - 1), rb = rq_setup(sh_out, -128, 127);
     const int nu = 3 * ntiles;
-    for (int u0 = wave; u0 < nu; u0 += 16) {
+    for (int u0 = wave; u0 < nu; u0 += 2 * NW) {
       int hh[2], rt[2];
       bool valid[2], fast[2];
       v4i acc[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const int uu = min(u0 + 8 * u, nu - 1);
-        valid[u] = u0 + 8 * u < nu;
-        hh[u] = uu / ntiles;
+        const int uu = min(u0 + NW * u, nu - 1);
+        valid[u] = u0 + NW * u < nu;
+        hh[u] = (uu >= ntiles ? 1 : 0) + (uu >= 2 * ntiles ? 1 : 0);  // uu / ntiles (< 3)
         rt[u] = uu - hh[u] * ntiles;
         fast[u] = fast_s[hh[u]][2];
         const long a = *reinterpret_cast<const long *>(
             &act_b[(hh[u] * kCandPad + rt[u] * 16 + col) * 32 + grp * 8]);
         const long wb = *reinterpret_cast<const long *>(&w2[hh[u]][col * 32 + grp * 8]);
-        acc[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, wb, v4i{0}, 0, 0, 0);
+        acc[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(wb, a, v4i{0}, 0, 0, 0);
       }
       if (fast[0] && fast[1] && t2.off >= 0) {
         int qv[8];
@@ -605,30 +612,30 @@ __global__ __launch_bounds__(kImgThreads) void k_selector_image(
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) qv[4 * u + i] = rq(acc[u][i] + bb2[hh[u]][col], ra);
+          for (int i = 0; i < 4; ++i) qv[4 * u + i] = rq(acc[u][i] + bb2[hh[u]][4 * grp + i], ra);
         gelu_table_u8_n<8>(qv, ov, lut, t2.cb, t2.qlo, t2.qhi);
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          int8_t *dst = &act_a[(hh[u] * kCandPad + rt[u] * 16 + grp * 4) * 16 + col];
-          if (valid[u]) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) dst[i * 16] = (int8_t)ov[4 * u + i];
-          }
-        }
+        for (int u = 0; u < 2; ++u)
+          if (valid[u])
+            *reinterpret_cast<unsigned *>(
+                &act_a[(hh[u] * kCandPad + rt[u] * 16 + col) * 16 + 4 * grp]) =
+                pack_lo4(ov[4 * u], ov[4 * u + 1], ov[4 * u + 2], ov[4 * u + 3]);
       } else {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          int8_t *dst = &act_a[(hh[u] * kCandPad + rt[u] * 16 + grp * 4) * 16 + col];
           if (valid[u]) {
+            unsigned o[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const int v = fast[u] && t2.off >= 0
-                                ? (int)(int8_t)gelu_table_u8(rq(acc[u][i] + bb2[hh[u]][col], ra),
-                                                             lut, t2.cb, t2.qlo, t2.qhi)
-                                : sel_gelu(acc[u][i], bb2[hh[u]][col], fast[u], ra, rb, sh_in,
-                                           sh_out);
-              dst[i * 16] = (int8_t)v;
+              const int bias = bb2[hh[u]][4 * grp + i];
+              o[i] = (unsigned)(fast[u] && t2.off >= 0
+                                    ? (int)gelu_table_u8(rq(acc[u][i] + bias, ra), lut, t2.cb,
+                                                         t2.qlo, t2.qhi)
+                                    : sel_gelu(acc[u][i], bias, fast[u], ra, rb, sh_in, sh_out));
             }
+            *reinterpret_cast<unsigned *>(
+                &act_a[(hh[u] * kCandPad + rt[u] * 16 + col) * 16 + 4 * grp]) =
+                pack_lo4(o[0], o[1], o[2], o[3]);
           }
         }
       }
@@ -662,21 +669,34 @@ __global__ __launch_bounds__(kImgThreads) void k_selector_image(
     }
   }
   __syncthreads();
-  // Head fuse (thread c < C), keep list and state.
+  // Head fuse: thread j * C + c takes head-weight unit j of candidate c
+  // (hidden and weight layers, through LDS: the h1 buffer is free), then
+  // thread c < C the mean; keep list and state.
+  int *hid_s = reinterpret_cast<int *>(act_b), *hw_s = hid_s + 3 * kMaxCand;
+  const int fj = (tid >= C ? 1 : 0) + (tid >= 2 * C ? 1 : 0), fcand = tid - fj * C;
+  if (tid < 3 * C) hid_s[fcand * 3 + fj] = fuse_hidden(p, &st_s[fcand * 3], fj);
+  __syncthreads();
+  if (tid < 3 * C) {
+    const int w = fuse_weight(p, &hid_s[fcand * 3], fj);
+    hw_s[fcand * 3 + fj] = w;
+    if (ck.head_weights) ck.head_weights[((size_t)b * kMaxCand + fcand) * 3 + fj] = w;
+  }
+  __syncthreads();
   int fc = 0;
   bool warn = false;
   if (tid < C) {
-    fc = fuse_candidate(p, &st_s[tid * 3], &hs_s[tid],
-                        ck.head_weights ? ck.head_weights + ((size_t)b * kMaxCand + tid) * 3
-                                        : nullptr,
-                        &warn);
+    fc = fuse_mean(&hs_s[tid], &hw_s[tid * 3], &warn);
     fused_out[(size_t)b * kMaxCand + tid] = fc;
   }
-  const int kept = keep_list<NT>(C, pkg, fc, warn, false, kept_index + (size_t)b * kMaxCand, st);
+  i64 den = 0;
+  const int kept =
+      keep_list<NT>(C, pkg, fc, warn, false, kept_index + (size_t)b * kMaxCand, st, &den);
   if (tid == 0 && img_warn) img_warn[b] |= st[4];
   if (kept < 0 || C - kept == 0) return;  // uniform; no package row
-  package_row<NT, kXsRow>(xs, C, pkg, kept, fc, pkg_rows + (size_t)b * 192, wgt,
-                          reinterpret_cast<int *>(act_b));
+  // (the step table's LDS is free: its last reader was score layer 2)
+  static_assert(36 * 192 <= kGeluLutMaxWords, "package sums fit the table's LDS");
+  package_row<NT, kXsRow, 36>(xs, C, pkg, kept, fc, den, pkg_rows + (size_t)b * 192, wgt,
+                              reinterpret_cast<int *>(lut));
 }
 
 // finalize_tokens from given fused scores (hv_selector_finalize): the keep
@@ -769,9 +789,18 @@ __global__ __launch_bounds__(256) void k_selector_compact(
           reinterpret_cast<const v4i *>(pkg_rows + (size_t)b * 192)[tid];
     return;
   }
+  // the partitioned candidates' score sum (finalize's scores are checked
+  // to lie in [0, 65536], so a wavefront's sum fits 32 bits)
   const int fv = tid < C ? fused[(size_t)b * kMaxCand + tid] : 0;
-  package_row<256, 192>(tokens + (size_t)(row0 + 1) * 192, C, pkg, kept, fv, prow, wgt,
-                        part_sum);
+  const bool part = tid < C && ((tid < C - pkg && fv < 32768) || (pkg && tid == C - 1));
+  int d = part ? fv : 0;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) d += __shfl_xor(d, off);
+  if (lane == 0) red[wave] = d;
+  __syncthreads();
+  const i64 den = (i64)red[0] + red[1] + red[2] + red[3];
+  package_row<256, 192, 21>(tokens + (size_t)(row0 + 1) * 192, C, pkg, kept, fv, den, prow, wgt,
+                            part_sum);
 }
 
 int launch_selector(const SelectorArgs &a, hipStream_t s) {
