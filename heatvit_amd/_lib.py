@@ -22,6 +22,7 @@ GELU_TABLE_SO = range(3, 13)
 HV_EPI_I8, HV_EPI_I32, HV_EPI_GELU, HV_EPI_RESIDUAL = 0, 1, 2, 3
 HV_A_ROWS, HV_A_GATHER, HV_A_UNSIGNED = 0, 1, 4
 HV_SELECTOR_NOALLOC_MAX_BATCH = 1024
+HV_FWD_PIPELINED = 1
 ABI_VERSION = 5
 PROF_CLASSES = ("patch", "layernorm", "gemm_qkv", "attention", "gemm_proj", "gemm_ffn1",
                 "gemm_ffn2", "selector", "head", "other", "ffn")
@@ -157,6 +158,9 @@ def _declare(L):
     L.hv_model_forward.argtypes = [C.POINTER(ModelDev), _vp, C.c_int, _vp, _vp, _vp, _vp, _vp,
                                    _vp, _vp, C.c_size_t, _vp]
     L.hv_model_forward_f32.argtypes = L.hv_model_forward.argtypes
+    L.hv_model_forward_ex.argtypes = [C.POINTER(ModelDev), _vp, C.c_int, _vp, _vp, _vp, _vp,
+                                      _vp, _vp, _vp, C.c_size_t, C.c_int, _vp]
+    L.hv_model_forward_f32_ex.argtypes = L.hv_model_forward_ex.argtypes
     L.hv_quantize_images.argtypes = [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]
     L.hv_schedule_compile.argtypes = [_vp, C.c_int, C.POINTER(Schedule)]
     L.hv_schedule_packed_bytes.restype = C.c_size_t
@@ -190,5 +194,6 @@ def exported_symbols():
             "hv_selector_finalize",
             "hv_patch_embedding", "hv_profile_enable", "hv_profile_read",
             "hv_model_workspace_bytes", "hv_model_forward", "hv_model_forward_f32",
+            "hv_model_forward_ex", "hv_model_forward_f32_ex",
             "hv_quantize_images", "hv_schedule_compile", "hv_schedule_packed_bytes",
             "hv_schedule_bind")

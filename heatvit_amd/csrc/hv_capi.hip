@@ -228,6 +228,11 @@ struct LnChain {
   bool *next_done;
 };
 
+// Whether the fused FFN's 64-row blocks of `rows` rows fill less than one
+// round of the GPU's 256 CUs at two workgroups each (then blocks of 32 rows
+// finish sooner, one forward at a time).
+static bool small_rows(long long rows) { return rows < 2 * 256 * 64; }
+
 // Images per batch from which the attention kernel runs the QKV GEMM.
 static constexpr int kFusedQkvMinBatch = 32;
 
@@ -235,10 +240,12 @@ static constexpr int kFusedQkvMinBatch = 32;
 // LN1, QKV, attention, proj + residual, LN2, FFN1 + GELU, FFN2 + residual.
 // warnings (optional, [B]) receive the LayerNorms' negative-variance bit.
 // bias_max (optional, device): the largest |bias| of bqkv, bproj, b1 and b2.
+// rows32: the fused FFN in blocks of 32 rows (launch_ffn).
 static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *offsets,
                          int batch, int max_rows, int8_t *z, const hv_block_ckpt *ck,
                          int32_t *warnings, const BlockWs &w, hipStream_t s,
-                         const LnChain &chain = LnChain{}, const unsigned *bias_max = nullptr) {
+                         const LnChain &chain = LnChain{}, const unsigned *bias_max = nullptr,
+                         bool rows32 = false) {
   const int32_t *rows_dev = offsets + batch;
   const LnWarn lw{offsets, batch, warnings};
   int8_t *qkv = ck && ck->fused_qkv ? ck->fused_qkv : w.qkv;
@@ -336,7 +343,7 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   if (ln2_in && !ck) {
     const LnPrologue fl{nullptr, ln, lw};
     ProfScope ps(HV_PROF_FFN, s);
-    rc = launch_ffn(g1, g2, s, &fl, chained ? &fe : nullptr, &g);
+    rc = launch_ffn(g1, g2, s, &fl, chained ? &fe : nullptr, &g, rows32);
     if (rc != 1) {
       if (rc == HV_OK && chained && chain.next_done) *chain.next_done = true;
       return rc;
@@ -499,7 +506,8 @@ int hv_block_forward(const hv_block_dev *p, const int8_t *x, const int32_t *offs
   if (!cv.ok || !workspace) return fail(HV_EVALUE, HV_ERR_ADDRESS, "block: workspace too small");
   if ((rc = launch_image_check(offsets, batch, max_rows, status, warnings, (hipStream_t)stream)))
     return rc;
-  return block_forward(*p, x, offsets, batch, max_rows, z, ck, warnings, w, (hipStream_t)stream);
+  return block_forward(*p, x, offsets, batch, max_rows, z, ck, warnings, w, (hipStream_t)stream,
+                       LnChain{}, nullptr, small_rows(max_rows));
 }
 
 struct SelectorWs {
@@ -667,7 +675,7 @@ size_t hv_model_workspace_bytes(int batch) {
 static int model_forward(const hv_model_dev *p, const void *images, bool float_images, int batch,
                          int32_t *logits, int32_t *token_counts, int32_t *state,
                          int32_t *warnings, int8_t *ckpt, int32_t *ckpt_rows, void *workspace,
-                         size_t workspace_bytes, hipStream_t s) {
+                         size_t workspace_bytes, int options, hipStream_t s) {
   if (!p || !images || !logits) return fail(HV_EVALUE, HV_ERR_ADDRESS, "model: null argument");
   if (batch <= 0) return fail(HV_EVALUE, HV_ERR_DIMENSION, "model: empty batch");
   if ((long long)batch * HV_MAX_TOKENS * 768 > 0x7fffffffLL)
@@ -749,8 +757,12 @@ static int model_forward(const hv_model_dev *p, const void *images, bool float_i
     bool next_done = false;
     const LnChain chain{ln1_ready, chain_next ? (blk < 12 ? &p->blocks[blk] : &fin) : nullptr,
                         w.blk.ln, &next_done};
+    // One forward at a time, 32-row FFN blocks once a selector has cut the
+    // rows (or for small batches); pipelined callers keep 64.
+    const bool rows32 =
+        !(options & HV_FWD_PIPELINED) && (sel > 0 || small_rows((long long)max_rows));
     if ((rc = block_forward(p->blocks[blk - 1], w.xa, w.off_a, batch, max_rows, w.xb, nullptr,
-                            warnings, w.blk, s, chain, w.bias_max + 4 * (blk - 1))))
+                            warnings, w.blk, s, chain, w.bias_max + 4 * (blk - 1), rows32)))
       return rc;
     ln1_ready = next_done ? w.blk.ln : nullptr;
     if (blk == 12) final_done = next_done;
@@ -782,7 +794,18 @@ int hv_model_forward(const hv_model_dev *p, const int8_t *images, int batch, int
                      hv_stream_t stream) {
   clear_error();
   return model_forward(p, images, false, batch, logits, token_counts, state, warnings, ckpt,
-                       ckpt_rows, workspace, workspace_bytes, (hipStream_t)stream);
+                       ckpt_rows, workspace, workspace_bytes, 0, (hipStream_t)stream);
+}
+
+int hv_model_forward_ex(const hv_model_dev *p, const int8_t *images, int batch, int32_t *logits,
+                        int32_t *token_counts, int32_t *state, int32_t *warnings, int8_t *ckpt,
+                        int32_t *ckpt_rows, void *workspace, size_t workspace_bytes, int options,
+                        hv_stream_t stream) {
+  clear_error();
+  if (options & ~HV_FWD_PIPELINED)
+    return fail(HV_EVALUE, HV_ERR_OPCODE, "model: unknown options 0x%x", options);
+  return model_forward(p, images, false, batch, logits, token_counts, state, warnings, ckpt,
+                       ckpt_rows, workspace, workspace_bytes, options, (hipStream_t)stream);
 }
 
 int hv_model_forward_f32(const hv_model_dev *p, const float *images, int batch, int32_t *logits,
@@ -791,7 +814,18 @@ int hv_model_forward_f32(const hv_model_dev *p, const float *images, int batch, 
                          hv_stream_t stream) {
   clear_error();
   return model_forward(p, images, true, batch, logits, token_counts, state, warnings, ckpt,
-                       ckpt_rows, workspace, workspace_bytes, (hipStream_t)stream);
+                       ckpt_rows, workspace, workspace_bytes, 0, (hipStream_t)stream);
+}
+
+int hv_model_forward_f32_ex(const hv_model_dev *p, const float *images, int batch,
+                            int32_t *logits, int32_t *token_counts, int32_t *state,
+                            int32_t *warnings, int8_t *ckpt, int32_t *ckpt_rows, void *workspace,
+                            size_t workspace_bytes, int options, hv_stream_t stream) {
+  clear_error();
+  if (options & ~HV_FWD_PIPELINED)
+    return fail(HV_EVALUE, HV_ERR_OPCODE, "model: unknown options 0x%x", options);
+  return model_forward(p, images, true, batch, logits, token_counts, state, warnings, ckpt,
+                       ckpt_rows, workspace, workspace_bytes, options, (hipStream_t)stream);
 }
 
 int hv_quantize_images(const float *images, int batch, int input_exp, int layout, int8_t *out,

@@ -1194,6 +1194,261 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
   }
 }
 
+// ---------------------------------------------------------------------------
+// The fused FFN over blocks of 32 rows by eight wavefronts (k_ffn32): the
+// same phases and epilogues as k_ffn, with a quarter of k_ffn's work per
+// wavefront, for batches whose 64-row blocks would leave CUs idle (the
+// pruned stages of one forward at a time).  One row tile of 32:
+//   phase P  wavefront w < 6: projection column tile w (K = 192);
+//   LN       16 lanes per row (ln_rows16);
+//   phase A  wavefront w: FFN1 column tiles w, w + 8, w + 16, GELU from the
+//            step table into the hidden block [32][768] (784-byte rows);
+//   phase B  wavefront w < 6: FFN2 column tile w over K = 768, residual;
+//   LNE      the next block's LayerNorm 1 of the output rows.
+// ---------------------------------------------------------------------------
+static constexpr int kFfn32Rows = 32;
+
+// LayerNorm (nonlinear.py:136-186, int32 form) of a block of 32 rows by 512
+// threads: 16 lanes per row, 12 channels each, every lane working out its
+// row's constants (no broadcast).  Row i is read from src + min(i, clamp) *
+// SS and written to dst + i * DS when i < store_rows; rows i < report_rows
+// (row r0 + i of the batch) report a negative variance to lw.
+template <int SS, int DS>
+__device__ __forceinline__ void ln_rows16(const int8_t *src, int clamp, int8_t *dst,
+                                          int store_rows, const Ln32 &ln, const LnWarn &lw,
+                                          int r0, int report_rows) {
+  const int tid = threadIdx.x, sub = tid & 15, row = tid >> 4;
+  int w[3], gm[3], bt[3], out[3];
+  const int *xr = reinterpret_cast<const int *>(src + min(row, clamp) * SS + sub * 12);
+  const int *gp = reinterpret_cast<const int *>(ln.gamma + sub * 12);
+  const int *bp = reinterpret_cast<const int *>(ln.beta + sub * 12);
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    w[q] = xr[q];
+    gm[q] = gp[q];
+    bt[q] = bp[q];
+  }
+  const bool neg = ln32_row<16>(w, gm, bt, ln, out);
+  if (sub == 0 && neg && lw.img_warn && row < report_rows)
+    ln_warn_row(lw.offsets, lw.batch, lw.img_warn, r0 + row);
+  if (row < store_rows) {
+    int *yr = reinterpret_cast<int *>(dst + row * DS + sub * 12);
+#pragma unroll
+    for (int q = 0; q < 3; ++q) yr[q] = out[q];
+  }
+}
+
+template <int DIRS1, int DIRS2, bool LN, bool LNE, bool PJ>
+__global__ __launch_bounds__(512, 4) void k_ffn32(GemmArgs g1, GemmArgs g2, LnPrologue fl,
+                                               LnPrologue fe, GemmArgs gp, int dirsp) {
+  static_assert(!PJ || LN, "the projection feeds the LayerNorm in front");
+  static_assert(kFfn32Rows * kLnPrologueRow <= 4 * kGeluLutMaxWords, "output rows fit the table");
+  __shared__ __attribute__((aligned(16))) int8_t hid[kFfn32Rows * kFfnHRow];
+  __shared__ __attribute__((aligned(16))) unsigned lut[kGeluLutMaxWords];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int M = g1.m_dev ? min(*g1.m_dev, g1.m) : g1.m;
+  if ((int)blockIdx.x >= (M + kFfn32Rows - 1) / kFfn32Rows) return;  // uniform
+  const int r0 = blockIdx.x * kFfn32Rows;
+  const int arow = min(r0 + l32, M - 1);
+  // the step table in one round of at most four 16-byte vectors per thread,
+  // written to LDS before the barrier in front of phase A
+  static_assert(kGeluLutMaxWords / 4 <= 4 * 512, "one staging round");
+  const int n4 = g1.lut_words >> 2;
+  v4i tv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    tv[i] = reinterpret_cast<const v4i *>(kGeluLut + g1.lut_off)[min(tid + 512 * i, n4 - 1)];
+  auto write_lut = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) reinterpret_cast<v4i *>(lut)[min(tid + 512 * i, n4 - 1)] = tv[i];
+  };
+  const Rq r1a = rq_setup(g1.shift_a, -(1 << 23), (1 << 23) - 1);
+  const Rq r2a = rq_setup(g2.shift_a, -128, 127), r2b = rq_setup(g2.os, -128, 127);
+  constexpr bool LA1 = DIRS1 & 1;
+  const bool all1 = tensor_narrow(g1.bias_max, g1.acc_lim);
+  int qhi = g1.lut_qhi;
+  asm("" : "+v"(qhi));  // the table clamp as one med3 (both bounds in VGPRs)
+
+  // Phase P (PJ): wavefront w < 6 computes y tile w and keeps its bytes as
+  // phase B's residual; the y rows go to LDS (208-byte rows) for LayerNorm 2.
+  v4i yres = v4i{0};
+  if constexpr (PJ) {
+    if (wave < 6) {
+      const int ct = wave;
+      const Rq rpa = rq_setup(gp.shift_a, -128, 127), rpb = rq_setup(gp.os, -128, 127);
+      const bool allp = tensor_narrow(gp.bias_max, gp.acc_lim);
+      const int8_t *ap = gp.a + (size_t)arow * 192 + 16 * h;
+      const int8_t *bp = gp.b + (size_t)ct * 6 * 1024 + lane * 16;
+      v4i pa[6], pw[6], b4[4];
+#pragma unroll
+      for (int kt = 0; kt < 6; ++kt) {
+        pa[kt] = *reinterpret_cast<const v4i *>(ap + kt * 32);
+        pw[kt] = *reinterpret_cast<const v4i *>(bp + kt * 1024);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        b4[q] = *reinterpret_cast<const v4i *>(gp.bias + ct * 32 + 16 * h + 4 * q);
+      const v4i x4 =
+          *reinterpret_cast<const v4i *>(gp.res + (size_t)arow * 192 + ct * 32 + 16 * h);
+      v16i acc = v16i{0};
+#pragma unroll
+      for (int kt = 0; kt < 6; ++kt)
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(pw[kt], pa[kt], acc, 0, 0, 0);
+      switch (dirsp) {
+        case 0: yres = proj_epi<false, false>(gp, acc, b4, x4, rpa, rpb, allp); break;
+        case 1: yres = proj_epi<true, false>(gp, acc, b4, x4, rpa, rpb, allp); break;
+        case 2: yres = proj_epi<false, true>(gp, acc, b4, x4, rpa, rpb, allp); break;
+        default: yres = proj_epi<true, true>(gp, acc, b4, x4, rpa, rpb, allp); break;
+      }
+      *reinterpret_cast<v4i *>(&hid[l32 * kLnPrologueRow + ct * 32 + 16 * h]) = yres;
+    }
+  }
+  // Phase A operands: the row tile's A fragments (LayerNorm 2 rows through
+  // hid, or the caller's rows).
+  v4i af[6];
+  if constexpr (PJ) {
+    write_lut();
+    __syncthreads();  // y complete in LDS; LayerNorm 2 in place
+    ln_rows16<kLnPrologueRow, kLnPrologueRow>(hid, kFfn32Rows - 1, hid, kFfn32Rows, fl.ln, fl.lw,
+                                              r0, M - r0);
+    __syncthreads();
+  } else if constexpr (LN) {
+    ln_rows16<192, kLnPrologueRow>(fl.x + (size_t)r0 * 192, M - 1 - r0, hid, kFfn32Rows, fl.ln,
+                                   fl.lw, r0, M - r0);
+    write_lut();
+    __syncthreads();
+  }
+  if constexpr (LN) {
+#pragma unroll
+    for (int kt = 0; kt < 6; ++kt)
+      af[kt] = *reinterpret_cast<const v4i *>(&hid[l32 * kLnPrologueRow + kt * 32 + 16 * h]);
+    __syncthreads();  // phase A rewrites hid
+  } else {
+    const int8_t *ap = g1.a + (size_t)arow * g1.lda + 16 * h;
+#pragma unroll
+    for (int kt = 0; kt < 6; ++kt) af[kt] = *reinterpret_cast<const v4i *>(ap + kt * 32);
+    write_lut();
+    __syncthreads();
+  }
+  // Phase A: column tiles wave + 8 ci; the next tile's weight fragments load
+  // during the current tile's GELU epilogue, its biases during its MFMAs.
+  {
+    v4i bf[6], bs[4];
+    auto load_w1 = [&](int ci) {
+      const int ct = wave + 8 * ci;
+#pragma unroll
+      for (int kt = 0; kt < 6; ++kt)
+        bf[kt] = *reinterpret_cast<const v4i *>(g1.b + (size_t)(ct * 6 + kt) * 1024 + lane * 16);
+    };
+    load_w1(0);
+#pragma unroll
+    for (int ci = 0; ci < 3; ++ci) {
+      const int c0 = (wave + 8 * ci) * 32 + 16 * h;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) bs[q] = *reinterpret_cast<const v4i *>(g1.bias + c0 + 4 * q);
+      v16i acc = v16i{0};
+#pragma unroll
+      for (int kt = 0; kt < 6; ++kt)
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[kt], af[kt], acc, 0, 0, 0);
+      if (ci + 1 < 3) load_w1(ci + 1);
+      bool fast = all1;
+      if (!all1) {
+        int bmax = bs[0][0], bmin = bmax;
+#pragma unroll
+        for (int j = 1; j < 16; ++j) {
+          bmax = max(bmax, bs[j >> 2][j & 3]);
+          bmin = min(bmin, bs[j >> 2][j & 3]);
+        }
+        fast = __all(bmax <= g1.acc_lim && bmin >= -g1.acc_lim);
+      }
+      int o[16];
+      if (fast) {
+        // the lookups in two stages of eight (registers)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          int qv[8];
+          unsigned ov[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            qv[j] = shift_nowrap<LA1>(acc[8 * hf + j] + bs[2 * hf + (j >> 2)][j & 3], r1a);
+          gelu_table_u8_n<8>(qv, ov, lut, g1.lut_cb, g1.lut_qlo, qhi);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) o[8 * hf + j] = (int)ov[j];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          o[j] = epi_exact(EPI_GELU, acc[j], bs[j >> 2][j & 3], 0, g1.shift_a, g1.shift_b, 0, 0,
+                           0)[0];
+      }
+      *reinterpret_cast<v4i *>(&hid[l32 * kFfnHRow + c0]) =
+          v4i{pack4(o[0], o[1], o[2], o[3]), pack4(o[4], o[5], o[6], o[7]),
+              pack4(o[8], o[9], o[10], o[11]), pack4(o[12], o[13], o[14], o[15])};
+    }
+  }
+  // Phase B: wavefront w < 6 takes FFN2 column tile w over K = 768 in chunks
+  // of 4 K-steps through a ring of two chunk buffers, one chunk ahead; its
+  // operands and first weight chunk load before the barrier.
+  const int ct = wave;
+  v4i wb[2][4], bias4[1][4], res4[1][1];
+  if (wave < 6) {
+    const int arows[1] = {arow};
+    if constexpr (PJ) {
+      epi_operands<1, 1, EPI_I8>(g2, arows, ct, h, bias4, res4);
+      res4[0][0] = yres;
+    } else {
+      epi_operands<1, 1, EPI_RES>(g2, arows, ct, h, bias4, res4);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      wb[0][j] = *reinterpret_cast<const v4i *>(g2.b + ((size_t)ct * 24 + j) * 1024 + lane * 16);
+  }
+  __syncthreads();
+  if (wave < 6) {
+    const int8_t *hp = &hid[l32 * kFfnHRow + 16 * h];
+    const int8_t *bp = g2.b + (size_t)ct * 24 * 1024 + lane * 16;
+    v16i acc[1][1] = {{v16i{0}}};
+#pragma unroll
+    for (int c = 0; c < 6; ++c) {
+      const int cur = c & 1, nxt = cur ^ 1;
+      if (c + 1 < 6) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          wb[nxt][j] = *reinterpret_cast<const v4i *>(bp + ((c + 1) * 4 + j) * 1024);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+            wb[cur][j], *reinterpret_cast<const v4i *>(hp + (c * 4 + j) * 32), acc[0][0], 0, 0,
+            0);
+      __builtin_amdgcn_sched_barrier(0);  // one chunk of LDS reads in flight at a time
+    }
+    epi_tile<1, 1, EPI_RES, true, DIRS2>(g2, acc, bias4, res4, r0, ct, M, h, l32, r2a, r2b,
+                                         nullptr,
+                                         LNE ? reinterpret_cast<int8_t *>(lut) : nullptr,
+                                         kLnPrologueRow);
+  }
+  if constexpr (LNE) {
+    __syncthreads();  // every output row is in the table's LDS
+    ln_rows16<kLnPrologueRow, 192>(reinterpret_cast<const int8_t *>(lut), kFfn32Rows - 1,
+                                   fe.ln.out + (size_t)r0 * 192, M - r0, fe.ln, fe.lw, r0, M - r0);
+  }
+}
+
+template <int DIRS1, bool LN, bool LNE, bool PJ>
+static void launch_ffn32_d(const GemmArgs &g1, const GemmArgs &g2, const LnPrologue &fl,
+                           const LnPrologue &fe, const GemmArgs &gp, int dirsp, int dirs2,
+                           dim3 grid, hipStream_t s) {
+  const dim3 b(512);
+  switch (dirs2) {
+    case 0: hv_launch(k_ffn32<DIRS1, 0, LN, LNE, PJ>, grid, b, 0, s, g1, g2, fl, fe, gp, dirsp); break;
+    case 1: hv_launch(k_ffn32<DIRS1, 1, LN, LNE, PJ>, grid, b, 0, s, g1, g2, fl, fe, gp, dirsp); break;
+    case 2: hv_launch(k_ffn32<DIRS1, 2, LN, LNE, PJ>, grid, b, 0, s, g1, g2, fl, fe, gp, dirsp); break;
+    default: hv_launch(k_ffn32<DIRS1, 3, LN, LNE, PJ>, grid, b, 0, s, g1, g2, fl, fe, gp, dirsp); break;
+  }
+}
+
 template <int DIRS1, bool LN, bool LNE, bool PJ>
 static void launch_ffn_d(const GemmArgs &g1, const GemmArgs &g2, const LnPrologue &fl,
                          const LnPrologue &fe, const GemmArgs &gp, int dirsp, int dirs2, dim3 grid,
@@ -1210,7 +1465,8 @@ static void launch_ffn_d(const GemmArgs &g1, const GemmArgs &g2, const LnPrologu
 // Returns HV_OK when the fused kernel was launched, 1 when the shapes or
 // exponents need the two GEMM launches instead.
 int launch_ffn(const GemmArgs &g1_in, const GemmArgs &g2_in, hipStream_t s,
-               const LnPrologue *ln, const LnPrologue *ln_next, const GemmArgs *proj) {
+               const LnPrologue *ln, const LnPrologue *ln_next, const GemmArgs *proj,
+               bool rows32) {
   GemmArgs g1 = g1_in, g2 = g2_in;
   GemmArgs gp = proj ? *proj : GemmArgs{};
   if (proj) {
@@ -1253,6 +1509,16 @@ int launch_ffn(const GemmArgs &g1_in, const GemmArgs &g2_in, hipStream_t s,
   const LnPrologue fl = ln ? *ln : LnPrologue{}, fe = ln_next ? *ln_next : LnPrologue{};
   const int dp = proj ? epilogue_dirs(gp, EPI_RES) : 0;
   const int mode = (ln ? 1 : 0) | (ln_next ? 2 : 0) | (d1 ? 4 : 0);
+  if (proj && rows32) {
+    const dim3 grid32((g1.m + kFfn32Rows - 1) / kFfn32Rows);
+    switch (mode) {
+      case 1: launch_ffn32_d<4, true, false, true>(g1, g2, fl, fe, gp, dp, d2, grid32, s); break;
+      case 3: launch_ffn32_d<4, true, true, true>(g1, g2, fl, fe, gp, dp, d2, grid32, s); break;
+      case 5: launch_ffn32_d<5, true, false, true>(g1, g2, fl, fe, gp, dp, d2, grid32, s); break;
+      default: launch_ffn32_d<5, true, true, true>(g1, g2, fl, fe, gp, dp, d2, grid32, s); break;
+    }
+    return check_hip(hipGetLastError(), "k_ffn32 launch");
+  }
   if (proj) {
     switch (mode) {
       case 1: launch_ffn_d<4, true, false, true>(g1, g2, fl, fe, gp, dp, d2, grid, lds, s); break;

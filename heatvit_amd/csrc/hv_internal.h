@@ -93,9 +93,11 @@ struct LnPrologue {
   Ln32 ln;
   LnWarn lw;
 };
+// rows32 (with proj): blocks of 32 rows by eight wavefronts (k_ffn32), for
+// batches whose 64-row blocks leave CUs idle; the same outputs.
 int launch_ffn(const GemmArgs &g1, const GemmArgs &g2, hipStream_t s,
                const LnPrologue *ln = nullptr, const LnPrologue *ln_next = nullptr,
-               const GemmArgs *proj = nullptr);
+               const GemmArgs *proj = nullptr, bool rows32 = false);
 // Fills acc_lim / narrow_ok / da / db / os of the int32 epilogue paths.
 void epilogue_limits_pub(GemmArgs &g, int epilogue);
 

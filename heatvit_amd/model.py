@@ -51,9 +51,13 @@ class Engine:
     """Device-resident model plus a reusable workspace for batches of up to
     `max_batch` images.  `forward(images)` takes a device int8 tensor
     [B][150528] and enqueues the whole forward on the current stream; it
-    returns device views (logits, token_counts, selector state, warnings)."""
+    returns device views (logits, token_counts, selector state, warnings).
+    `pipelined`: other forwards run on the GPU at the same time (Pipeline's
+    slots), so the kernels keep the launch shapes that suit a shared GPU
+    (HV_FWD_PIPELINED); the outputs are the same either way."""
 
-    def __init__(self, params, max_batch, device="cuda"):
+    def __init__(self, params, max_batch, device="cuda", pipelined=False):
+        self.options = _lib.HV_FWD_PIPELINED if pipelined else 0
         # a DeviceModel, a compiled-ROM model (heatvit_amd.schedule), or params
         self.model = params if hasattr(params, "struct") else DeviceModel(params, device)
         self.max_batch = int(max_batch)
@@ -75,12 +79,12 @@ class Engine:
         if images.dtype == torch.float32:
             if not images.is_contiguous() or tuple(images.shape[1:]) != (3, 224, 224):
                 raise ValueError("float images must be a contiguous tensor [B][3][224][224]")
-            entry = _lib.lib().hv_model_forward_f32
+            entry = _lib.lib().hv_model_forward_f32_ex
         elif images.dtype != torch.int8 or not images.is_contiguous() or \
                 images.numel() != b * IMAGE_BYTES:
             raise ValueError("images must be a contiguous int8 device tensor [B][150528]")
         else:
-            entry = _lib.lib().hv_model_forward
+            entry = _lib.lib().hv_model_forward_ex
         state = self.state[:, :b] if b == self.max_batch else \
             torch.zeros((3, b, 5), dtype=torch.int32, device=images.device)
         _lib.check(entry(
@@ -88,7 +92,7 @@ class Engine:
             self.token_counts.data_ptr(), state.data_ptr(), self.warnings.data_ptr(),
             None if ckpt is None else ckpt.data_ptr(),
             None if ckpt_rows is None else ckpt_rows.data_ptr(),
-            self.workspace.data_ptr(), self.workspace.numel(),
+            self.workspace.data_ptr(), self.workspace.numel(), self.options,
             torch.cuda.current_stream(images.device).cuda_stream), "model forward")
         return self.logits[:b], self.token_counts[:b], state, self.warnings[:b]
 
@@ -132,7 +136,8 @@ class Pipeline:
             raise ValueError("pipeline depth must be at least 1")
         model = params if hasattr(params, "struct") else DeviceModel(params, device)
         self.model = model
-        self.engines = [Engine(model, max_batch, device) for _ in range(depth)]
+        self.engines = [Engine(model, max_batch, device, pipelined=depth > 1)
+                        for _ in range(depth)]
         self.streams = [torch.cuda.Stream(device=model.device) for _ in range(depth)]
         self._next = 0
 

@@ -373,6 +373,24 @@ int hv_model_forward_f32(const hv_model_dev *p, const float *images, int batch, 
                          int32_t *ckpt_rows, void *workspace, size_t workspace_bytes,
                          hv_stream_t stream);
 
+/* hv_model_forward and hv_model_forward_f32 with options (no counterpart   */
+/* in the reference: launch shapes only, the outputs are the same bytes).   */
+/* Without options a forward is taken to run alone on the GPU: the fused    */
+/* FFN then uses blocks of 32 rows wherever blocks of 64 would leave CUs    */
+/* idle (after the first selector, or for batches under 166 images).        */
+/* HV_FWD_PIPELINED: the caller keeps other forwards in flight on the same  */
+/* GPU (heatvit_amd.model.Pipeline), which fills the CUs the small stages   */
+/* leave idle; the fused FFN keeps its 64-row blocks throughout.           */
+#define HV_FWD_PIPELINED 1
+int hv_model_forward_ex(const hv_model_dev *p, const int8_t *images, int batch, int32_t *logits,
+                        int32_t *token_counts, int32_t *state, int32_t *warnings, int8_t *ckpt,
+                        int32_t *ckpt_rows, void *workspace, size_t workspace_bytes, int options,
+                        hv_stream_t stream);
+int hv_model_forward_f32_ex(const hv_model_dev *p, const float *images, int batch,
+                            int32_t *logits, int32_t *token_counts, int32_t *state,
+                            int32_t *warnings, int8_t *ckpt, int32_t *ckpt_rows, void *workspace,
+                            size_t workspace_bytes, int options, hv_stream_t stream);
+
 /* ------------------------------------------------------------------ */
 /* Kernel-class timing with HIP events (for benchmarks).  While enabled, */
 /* every kernel the forwards launch carries a start/stop event pair      */

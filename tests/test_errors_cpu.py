@@ -117,6 +117,13 @@ def test_block_selector_model_validation(L):
                                   None), _lib.HV_EVALUE, _lib.HV_ERR_ADDRESS)  # workspace
     _expect(L, L.hv_model_forward(C.byref(m), x, 1 << 20, logits, None, None, None, None, None,
                                   x, 256, None), _lib.HV_EVALUE, _lib.HV_ERR_DIMENSION)
+    # the _ex entries refuse option bits they do not know, and otherwise
+    # validate as the plain entries do
+    for entry in (L.hv_model_forward_ex, L.hv_model_forward_f32_ex):
+        _expect(L, entry(C.byref(m), x, 1, logits, None, None, None, None, None, x, 256, 2, None),
+                _lib.HV_EVALUE, _lib.HV_ERR_OPCODE)
+        _expect(L, entry(C.byref(m), x, 1, logits, None, None, None, None, None, x, 256,
+                         _lib.HV_FWD_PIPELINED, None), _lib.HV_EVALUE, _lib.HV_ERR_ADDRESS)
 
 
 def test_success_clears_the_error_class(L):
