@@ -198,6 +198,13 @@ __host__ __device__ __forceinline__ int gelu_q16_r(int x) {
 
 __device__ __forceinline__ int gelu_q16(int x) { return gelu_q16_r<RcpHw>(x); }
 
+// The low bytes of four words as one word, a in the low byte (three byte
+// permutes).
+__device__ __forceinline__ unsigned pack_lo4(unsigned a, unsigned b, unsigned c, unsigned d) {
+  return __builtin_amdgcn_perm(__builtin_amdgcn_perm(d, c, 0x0c0c0400u),
+                               __builtin_amdgcn_perm(b, a, 0x0c0c0400u), 0x05040100u);
+}
+
 // requant of |v| < 2^30 to [lo, hi] by a launch-uniform shift s in
 // [-30, 30].  s >= 1: round_shift_away is (v + 2^(s-1) - (v < 0)) >> s.
 // s <= 0: the left shift saturates, so v is first clamped to
@@ -366,17 +373,37 @@ __host__ __device__ __forceinline__ unsigned softmax_exp_t(int t) {
   return (unsigned)(x >> z16);
 }
 
+// softmax_exp_t(q - mx) with the row maximum folded into the constants:
+// k1 = 16 * 2^32 + 94549 * mx and c1 = 88670 - 16 * 45426 - mx (mod 2^32),
+// so q * -94549 + k1 = (q - mx) * -94549 + 16 * 2^32 exactly and the
+// remainder term takes q - mx in its constant; q is already clamped to at
+// least mx - 17 * 45426.
+__host__ __device__ __forceinline__ unsigned softmax_exp_qm(int q, i64 k1, unsigned c1) {
+  const unsigned z16 = (unsigned)((u64)((i64)q * -94549ll + k1) >> 32);
+  const unsigned s = mul_u24(z16, 45426u) + c1 + (unsigned)q;
+  const unsigned square = (unsigned)(((u64)s * s + 32768u) >> 16);
+  const u64 x = (u64)square * 23495u + (32768u + (22544ull << 16));
+  return (unsigned)(x >> z16);
+}
+
 // The attention's UQ0.8 probability minus 128 (the signed P - 128 operand
 // of the P.V product): p = min(rsa(rsa(e * recip, 16), 8), 255), whose
 // first rounding's discarded bits cannot carry past a multiple of 2^8, so p
 // = min((e * recip + 2^15 + 2^23) >> 24, 255).  With r256 = recip * 2^8 the
 // high word of e * r256 + (2^15 + 2^23) * 2^8 - 128 * 2^32 is p - 128
 // before the clamp (e, recip < 2^17).
-__host__ __device__ __forceinline__ int softmax_prob_m128(unsigned e, unsigned r256) {
+__host__ __device__ __forceinline__ int softmax_prob_m128_raw(unsigned e, unsigned r256) {
   const i64 v = (i64)e * (i64)r256 + (((32768ll + (1ll << 23)) << 8) - (128ll << 32));
-  const int p = (int)(v >> 32);
+  return (int)(v >> 32);
+}
+__host__ __device__ __forceinline__ int softmax_prob_m128(unsigned e, unsigned r256) {
+  const int p = softmax_prob_m128_raw(e, r256);
   return p < 127 ? p : 127;
 }
+
+// softmax_exp_t(0), the largest exponential of a row: every argument is
+// at most 0, and no softmax_exp_t over [-17 * 45426, 0] exceeds it.
+constexpr unsigned kSoftmaxExp0 = 65554u;
 
 // round_div(2^32, sum) for a row sum that includes exp(0) = 65554, so
 // 65554 <= sum < 2^32 and the result is below 2^17 (nonlinear.py:119):

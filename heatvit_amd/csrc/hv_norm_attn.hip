@@ -1,6 +1,8 @@
 // hv_norm_attn.hip -- integer LayerNorm, fused varlen attention and the
 // element-wise evaluators of the golden model's nonlinear primitives.
 #include "hv_device.h"
+#include <type_traits>
+
 #include "hv_internal.h"
 
 namespace hv {
@@ -375,100 +377,149 @@ __device__ __forceinline__ v4i qkv_epi(const AttnArgs &g, const v16i &acc, const
 // column) over four runs of four consecutive keys, and each run is one
 // dword of Vt, and adds its keys' sum to the channel's 128 sum_k V[k]
 // in vsum (LDS atomics; vsum zeroed before).  Units of one row tile of 32
-// and one of Q, K, V
-// (its two column tiles of 32): Q and K over the row tiles that hold key
-// tiles, V over those that hold keys; the units are numbered Q, K, V in turn
-// and unit u runs on wavefront u % 4, which loads the weight fragments once
-// per group.  Rows from N up to the 64-key chunk end are stored as zero
-// (the padded keys); Q and K rows past the key tiles are not stored.
-template <bool LA>
-__device__ __forceinline__ void qkv_head(const AttnArgs &g, int8_t *Qs, int8_t *Ks, int8_t *Vt,
-                                         int *vsum, int row0, int N, int h, int wave, int lane) {
+// and one of Q, K, V (its two column tiles of 32): Q and K over the row
+// tiles that hold key tiles, V over those that hold keys.  The head's
+// biases sit in LDS (bias_s, loaded by the caller).  Keys from the last V
+// tile to the 64-key chunk end are stored as zero; Q and K rows past the
+// key tiles are not stored.
+__device__ __forceinline__ void qkv_load_w(v4i (&w)[6], const int8_t *wqkv, int ctg, int lane) {
+#pragma unroll
+  for (int kt = 0; kt < 6; ++kt)
+    w[kt] = *reinterpret_cast<const v4i *>(wqkv + (size_t)(ctg * 6 + kt) * 1024 + lane * 16);
+}
+
+__device__ __forceinline__ void qkv_load_a(v4i (&a)[6], const int8_t *rows) {
+#pragma unroll
+  for (int kt = 0; kt < 6; ++kt) a[kt] = *reinterpret_cast<const v4i *>(rows + kt * 32);
+}
+
+// One unit: row tile rt of group p (0 Q, 1 K, 2 V; ISV: p == 2) from the A
+// fragments a and the group's weight fragments w.  NARROW: every bias of
+// the tensor within the accumulator bound, so the requant never takes the
+// general (called) form and no call runs with the prefetched operands
+// live; Q and K then start their accumulators at the bias.  Rows from N to
+// the tile end hold the product of row N - 1 (the A rows are clamped) and
+// are stored unmasked: the scores of those keys are masked to -2^30
+// (P = 0), so in (P - 128) V + 128 sum_k V[k] each such key adds
+// -128 V[k] + 128 V[k] = 0 whatever its V, its K row only meets masked
+// scores, and Q rows from N on are never read.
+template <bool LA, bool NARROW, bool ISV>
+__device__ __forceinline__ void qkv_unit(const AttnArgs &g, const v4i (&w)[2][6],
+                                         const v4i (&a)[6], int p, int rt, int8_t *Qs,
+                                         int8_t *Ks, int8_t *Vt, int *vsum, const int *bias_s,
+                                         int rows_k, int lane, const Rq &rq) {
   const int l32 = lane & 31, hh = lane >> 5;
-  const int rows_k = ((N + 15) >> 4) * 16;
-  const int nqk = (rows_k + 31) >> 5, nv = (N + 31) >> 5;  // row tiles per group
-  const Rq rq = rq_setup(g.qkv_shift, -128, 127);
-  const bool all_narrow = tensor_narrow(g.bqkv_max, g.qkv_acc_lim);
-#pragma unroll 1
-  for (int p = 0; p < 3; ++p) {
-    // this wavefront's units of group p: u = p * nqk + rt with u % 4 == wave
-    const int nrt = p < 2 ? nqk : nv;
-    const int rt0 = (wave - p * nqk) & 3;
-    if (rt0 >= nrt) continue;
-    v4i w[2][6];
+  if constexpr (ISV) {
+    // channel of this lane's column under the weight packing
+    const int pj = 16 * ((l32 >> 2) & 1) + 4 * (l32 >> 3) + (l32 & 3);
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      const int ctg = p * 6 + h * 2 + c;  // 32-column tile of the 576
+      v16i acc = v16i{0};
 #pragma unroll
       for (int kt = 0; kt < 6; ++kt)
-        w[c][kt] = *reinterpret_cast<const v4i *>(g.wqkv + (size_t)(ctg * 6 + kt) * 1024 +
-                                                  lane * 16);
-    }
-#pragma unroll 1
-    for (int rt = rt0; rt < nrt; rt += 4) {
-      const int r = rt * 32 + l32;
-      const int8_t *ap = g.ln1 + (size_t)(row0 + min(r, N - 1)) * 192 + 16 * hh;
-      v4i a[6];
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[kt], w[c][kt], acc, 0, 0, 0);
+      const int bias = bias_s[128 + c * 32 + pj];
+      if (NARROW || __all(bias <= g.qkv_acc_lim && bias >= -g.qkv_acc_lim)) {
 #pragma unroll
-      for (int kt = 0; kt < 6; ++kt) a[kt] = *reinterpret_cast<const v4i *>(ap + kt * 32);
-      if (p == 2) {
-        // channel of this lane's column under the weight packing
-        const int pj = 16 * ((l32 >> 2) & 1) + 4 * (l32 >> 3) + (l32 & 3);
+        for (int j = 0; j < 16; ++j) acc[j] = rq_dir_nowrap<LA>(acc[j] + bias, rq);
+      } else {
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const int bias = g.bqkv[(p * 6 + h * 2 + c) * 32 + pj];
-          v16i acc = v16i{0};
-#pragma unroll
-          for (int kt = 0; kt < 6; ++kt)
-            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[kt], w[c][kt], acc, 0, 0, 0);
-          if (all_narrow || __all(bias <= g.qkv_acc_lim && bias >= -g.qkv_acc_lim)) {
-#pragma unroll
-            for (int j = 0; j < 16; ++j) acc[j] = rq_dir_nowrap<LA>(acc[j] + bias, rq);
-          } else {
-#pragma unroll
-            for (int j = 0; j < 16; ++j) acc[j] = attn_requant8(acc[j], bias, g.qkv_shift);
-          }
-          int8_t *vrow = Vt + (c * 32 + pj) * kVStride;
-          int vs = 0;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const int t0 = rt * 32 + 8 * k + 4 * hh;  // keys t0 .. t0 + 3
-            unsigned wd = 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int v = t0 + i < N ? acc[4 * k + i] : 0;
-              vs += v;
-              wd |= (unsigned)(v & 0xFF) << (8 * i);
-            }
-            *reinterpret_cast<unsigned *>(vrow + vt_pos(t0)) = wd;
-          }
-          atomicAdd(&vsum[c * 32 + pj], vs * 128);
-          __builtin_amdgcn_sched_barrier(0);  // one column tile's registers at a time
-        }
-        continue;
+        for (int j = 0; j < 16; ++j) acc[j] = attn_requant8(acc[j], bias, g.qkv_shift);
       }
+      int8_t *vrow = Vt + (c * 32 + pj) * kVStride;
+      int vs = 0;
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const int ctg = p * 6 + h * 2 + c;
-        v4i b4[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          b4[q] = *reinterpret_cast<const v4i *>(g.bqkv + ctg * 32 + 16 * hh + 4 * q);
-        v16i acc = v16i{0};
-#pragma unroll
-        for (int kt = 0; kt < 6; ++kt)
-          acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[c][kt], a[kt], acc, 0, 0, 0);
-        v4i o = qkv_epi<LA>(g, acc, b4, rq, all_narrow);
-        if (r >= N) o = v4i{0};
-        const int ch = c * 32 + 16 * hh;  // channel within the head
-        if (r < rows_k) *reinterpret_cast<v4i *>(&(p == 0 ? Qs : Ks)[r * kKStride + ch]) = o;
-        __builtin_amdgcn_sched_barrier(0);  // one column tile's registers at a time
+      for (int k = 0; k < 4; ++k) {
+        const int t0 = rt * 32 + 8 * k + 4 * hh;  // keys t0 .. t0 + 3
+        const unsigned wd = pack_lo4(acc[4 * k], acc[4 * k + 1], acc[4 * k + 2], acc[4 * k + 3]);
+        vs = __builtin_amdgcn_sdot4((int)wd, 0x01010101, vs, false);
+        *reinterpret_cast<unsigned *>(vrow + vt_pos(t0)) = wd;
       }
+      atomicAdd(&vsum[c * 32 + pj], vs * 128);
+      __builtin_amdgcn_sched_barrier(0);  // one column tile's registers at a time
     }
+    return;
   }
+  const int r = rt * 32 + l32;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    // this lane's 16 channels c*32 + 16*hh + j
+    const int *bc = bias_s + p * 64 + c * 32 + 16 * hh;
+    v16i acc = NARROW ? *reinterpret_cast<const v16i *>(bc) : v16i{0};
+#pragma unroll
+    for (int kt = 0; kt < 6; ++kt)
+      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[c][kt], a[kt], acc, 0, 0, 0);
+    v4i o;
+    if (NARROW) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        o[q] = (int)pack_lo4(rq_dir_nowrap<LA>(acc[4 * q], rq), rq_dir_nowrap<LA>(acc[4 * q + 1], rq),
+                             rq_dir_nowrap<LA>(acc[4 * q + 2], rq),
+                             rq_dir_nowrap<LA>(acc[4 * q + 3], rq));
+    } else {
+      v4i b4[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) b4[q] = *reinterpret_cast<const v4i *>(bc + 4 * q);
+      o = qkv_epi<LA>(g, acc, b4, rq, false);
+    }
+    const int ch = c * 32 + 16 * hh;  // channel within the head
+    if (r < rows_k) *reinterpret_cast<v4i *>(&(p == 0 ? Qs : Ks)[r * kKStride + ch]) = o;
+    __builtin_amdgcn_sched_barrier(0);  // one column tile's registers at a time
+  }
+}
+
+// Wavefront p < 3 runs group p (0 Q, 1 K, 2 V) over all its row tiles
+// with the group's weights loaded once; the three wavefronts walk the row
+// tiles in step, so the A rows of one tile are fetched from L2 about once
+// and served from L1 to the other two.  The next tile's A rows load into
+// the other of two register sets while the current one multiplies (the
+// last tile reloads its own rows).
+template <bool LA, bool NARROW, bool ISV>
+__device__ __forceinline__ void qkv_rows(const AttnArgs &g, int p, int8_t *Qs, int8_t *Ks,
+                                         int8_t *Vt, int *vsum, const int *bias_s, int row0,
+                                         int N, int h, int lane) {
+  const int rows_k = ((N + 15) >> 4) * 16;
+  const int nrt = ISV ? (N + 31) >> 5 : (rows_k + 31) >> 5;  // row tiles of the group
+  const Rq rq = rq_setup(g.qkv_shift, -128, 127);
+  const int8_t *ln1 = g.ln1 + (size_t)row0 * 192 + 16 * (lane >> 5);
+  auto a_rows = [&](int rt) {
+    return ln1 + (size_t)min(min(rt, nrt - 1) * 32 + (lane & 31), N - 1) * 192;
+  };
+  v4i w[2][6], a0[6], a1[6];
+  qkv_load_w(w[0], g.wqkv, p * 6 + h * 2, lane);
+  qkv_load_w(w[1], g.wqkv, p * 6 + h * 2 + 1, lane);
+  qkv_load_a(a0, a_rows(0));
+#pragma unroll 1
+  for (int rt = 0; rt < nrt; rt += 2) {
+    qkv_load_a(a1, a_rows(rt + 1));
+    qkv_unit<LA, NARROW, ISV>(g, w, a0, p, rt, Qs, Ks, Vt, vsum, bias_s, rows_k, lane, rq);
+    if (rt + 1 >= nrt) break;
+    qkv_load_a(a0, a_rows(rt + 2));
+    qkv_unit<LA, NARROW, ISV>(g, w, a1, p, rt + 1, Qs, Ks, Vt, vsum, bias_s, rows_k, lane, rq);
+  }
+}
+
+template <bool LA, bool NARROW>
+__device__ __forceinline__ void qkv_units(const AttnArgs &g, int8_t *Qs, int8_t *Ks, int8_t *Vt,
+                                          int *vsum, const int *bias_s, int row0, int N, int h,
+                                          int wave, int lane) {
+  if (wave == 2)
+    qkv_rows<LA, NARROW, true>(g, 2, Qs, Ks, Vt, vsum, bias_s, row0, N, h, lane);
+  else if (wave < 2)
+    qkv_rows<LA, NARROW, false>(g, wave, Qs, Ks, Vt, vsum, bias_s, row0, N, h, lane);
+}
+
+template <bool LA>
+__device__ __forceinline__ void qkv_head(const AttnArgs &g, int8_t *Qs, int8_t *Ks, int8_t *Vt,
+                                         int *vsum, const int *bias_s, int row0, int N, int h,
+                                         int wave, int lane) {
+  if (tensor_narrow(g.bqkv_max, g.qkv_acc_lim))
+    qkv_units<LA, true>(g, Qs, Ks, Vt, vsum, bias_s, row0, N, h, wave, lane);
+  else
+    qkv_units<LA, false>(g, Qs, Ks, Vt, vsum, bias_s, row0, N, h, wave, lane);
   // keys of the last 64-key chunk past the V tiles: zero (four keys of one
   // channel per dword)
-  const int kz = nv * 32, runs = (((N + 63) >> 6) * 64 - kz) >> 2;
+  const int nv = (N + 31) >> 5, kz = nv * 32, runs = (((N + 63) >> 6) * 64 - kz) >> 2;
   for (int i = threadIdx.x; i < runs * 64; i += blockDim.x)
     *reinterpret_cast<unsigned *>(Vt + (i & 63) * kVStride + vt_pos(kz + 4 * (i >> 6))) = 0u;
 }
@@ -518,12 +569,19 @@ __device__ __forceinline__ void attn_tiles(const AttnArgs &g, const int8_t *Ks, 
     }
     mx = max(mx, __shfl_xor(mx, 16));
     mx = max(mx, __shfl_xor(mx, 32));
+    // exp(max(q - mx, -17 * 45426)) with mx folded into the constants
+    const int qlo = mx - 17 * 45426;
+    i64 k1 = (16ll << 32) + 94549ll * mx;
+    unsigned c1 = (unsigned)(88670 - 16 * 45426) - (unsigned)mx;
+    // opaque to the compiler, which otherwise re-expands q * -94549 + k1
+    // into a 64-bit (mx - q) product
+    asm volatile("" : "+v"(k1), "+v"(c1));
     unsigned sum = 0;
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const unsigned e = softmax_exp_t(max(st[kt][i] - mx, -17 * 45426));
+        const unsigned e = softmax_exp_qm(max(st[kt][i], qlo), k1, c1);
         st[kt][i] = (int)e;
         sum += e;
       }
@@ -532,32 +590,40 @@ __device__ __forceinline__ void attn_tiles(const AttnArgs &g, const int8_t *Ks, 
     sum += __shfl_xor(sum, 32);
     const unsigned r256 = softmax_recip24(sum) << 8;  // sum <= 197 * 65554 < 2^24
     v4i pk[NC];
+    // The bytes P - 128 (softmax_prob_m128), packed by byte permutes.  No
+    // exponential exceeds exp(0) = kSoftmaxExp0, so when no lane's
+    // probability at exp(0) reaches the clamp the clamp is left out.
+    auto probs = [&](auto clamp_c) {
+      constexpr bool CLAMP = decltype(clamp_c)::value;
 #pragma unroll
-    for (int kc = 0; kc < NC; ++kc) {
+      for (int kc = 0; kc < NC; ++kc) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int kt = kc * 4 + t;
-        unsigned w = 0x80808080u;  // keys past the tiles: P = 0
-        if (kt < NT) {
-          // the bytes P - 128 (softmax_prob_m128), packed by byte permutes
-          unsigned pm[4];
+        for (int t = 0; t < 4; ++t) {
+          const int kt = kc * 4 + t;
+          unsigned w = 0x80808080u;  // keys past the tiles: P = 0
+          if (kt < NT) {
+            unsigned pm[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            pm[i] = (unsigned)softmax_prob_m128((unsigned)st[kt][i], r256);
-            if (CKPT && g.prob && q < N && kt * 16 + 4 * grp + i < N)
-              g.prob[(((size_t)b * 3 + h) * 197 + q) * 197 + kt * 16 + 4 * grp + i] =
-                  (uint8_t)(pm[i] + 128);
+            for (int i = 0; i < 4; ++i) {
+              pm[i] = (unsigned)(CLAMP ? softmax_prob_m128((unsigned)st[kt][i], r256)
+                                       : softmax_prob_m128_raw((unsigned)st[kt][i], r256));
+              if (CKPT && g.prob && q < N && kt * 16 + 4 * grp + i < N)
+                g.prob[(((size_t)b * 3 + h) * 197 + q) * 197 + kt * 16 + 4 * grp + i] =
+                    (uint8_t)(pm[i] + 128);
+            }
+            w = pack_lo4(pm[0], pm[1], pm[2], pm[3]);
           }
-          w = __builtin_amdgcn_perm(__builtin_amdgcn_perm(pm[3], pm[2], 0x0c0c0400u),
-                                    __builtin_amdgcn_perm(pm[1], pm[0], 0x0c0c0400u),
-                                    0x05040100u);
+          pk[kc][t] = (int)w;
+          // keeps the scheduler from hoisting every tile's 64-bit products
+          // at once (register pressure, spills)
+          __builtin_amdgcn_sched_barrier(0);
         }
-        pk[kc][t] = (int)w;
-        // keeps the scheduler from hoisting every tile's 64-bit products
-        // at once (register pressure, spills)
-        __builtin_amdgcn_sched_barrier(0);
       }
-    }
+    };
+    if (CKPT || !__all(softmax_prob_m128_raw(kSoftmaxExp0, r256) <= 127))
+      probs(std::true_type{});
+    else
+      probs(std::false_type{});
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
       v4i acc = v4i{0};
@@ -591,6 +657,8 @@ __global__ __launch_bounds__(256, 3) void k_attention(AttnArgs g) {
   __shared__ __attribute__((aligned(16))) int8_t Vt[64 * kVStride];
   __shared__ __attribute__((aligned(16))) int vsum[64];  // 128 * sum_k V[k][d]
   __shared__ __attribute__((aligned(16))) int8_t Qs[FQ ? kMaxKeys * kKStride : 16];
+  // the head's QKV biases: group p, column tile c, column j at p*64 + c*32 + j
+  __shared__ __attribute__((aligned(64))) int bias_s[FQ ? 192 : 16];
 
   // The grid is a multiple of 8 and workgroups go round-robin over the 8
   // XCDs, so XCD x runs logical items [x*T8, (x+1)*T8): the three heads of
@@ -604,15 +672,16 @@ __global__ __launch_bounds__(256, 3) void k_attention(AttnArgs g) {
   // Images with a token count outside [1, 197] or rows outside the
   // buffers are skipped (reported by the block's image check).
   if (N <= 0 || N > HV_MAX_TOKENS || row0 < 0 || row0 > g.rows_cap - N) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n16 = (N + 15) >> 4;  // key / query tiles
   const int n64 = (N + 63) >> 6;  // PV chunks of 64 keys
   const int8_t *qkv = FQ ? nullptr : g.qkv + (size_t)row0 * 576;
 
   if constexpr (FQ) {
     if (tid < 64) vsum[tid] = 0;
+    if (tid < 192) bias_s[tid] = g.bqkv[((tid >> 6) * 6 + h * 2 + ((tid >> 5) & 1)) * 32 + (tid & 31)];
     __syncthreads();
-    qkv_head<FQL>(g, Qs, Ks, Vt, vsum, row0, N, h, wave, lane);
+    qkv_head<FQL>(g, Qs, Ks, Vt, vsum, bias_s, row0, N, h, wave, lane);
   } else {
   for (int i = tid; i < n16 * 16 * 4; i += 256) {
     const int r = i >> 2, c = (i & 3) * 16;
@@ -645,8 +714,8 @@ __global__ __launch_bounds__(256, 3) void k_attention(AttnArgs g) {
   __syncthreads();
   // The probabilities enter P V as the signed bytes P - 128: P V =
   // (P - 128) V + 128 sum_k V[k], one MFMA per tile instead of two.  The
-  // per-channel sums run over the zero-padded keys too (with FQ qkv_head
-  // has added them up).
+  // per-channel sums run over the padded keys too (with FQ qkv_head has
+  // added them up), so a padded key's P = 0 cancels whatever its V.
   if constexpr (!FQ) {
     if (tid < 64) {
       const int *row = reinterpret_cast<const int *>(&Vt[tid * kVStride]);

@@ -281,12 +281,6 @@ __device__ __forceinline__ void package_row(const int8_t *cand, int C, int pkg, 
 
 constexpr int kImgThreads = 1024, kXsRow = 208;
 
-// The low bytes of four words as one word (byte permutes).
-__device__ __forceinline__ unsigned pack_lo4(unsigned a, unsigned b, unsigned c, unsigned d) {
-  return __builtin_amdgcn_perm(__builtin_amdgcn_perm(d, c, 0x0c0c0400u),
-                               __builtin_amdgcn_perm(b, a, 0x0c0c0400u), 0x05040100u);
-}
-
 // One workgroup per image (XCD-major).  Per layer, the (head, tile) units of
 // the three heads run over the eight wavefronts; the layer's GELU step table
 // (when its output shift has one) is staged once for the three heads:

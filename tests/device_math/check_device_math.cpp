@@ -9,7 +9,8 @@
 //            hvo_softmax_attention and hvo_softmax_selector on random rows,
 //            the branch-free 32-bit reciprocal over all its row sums, and
 //            the exp alone against hvo_softmax_exp for every x_tilde in
-//            [-2^25, 0] plus a million larger magnitudes;
+//            [-2^25, 0] plus a million larger magnitudes, and the exp with
+//            the row maximum folded into its constants against it;
 //   layernorm the int32 limb-split normalisation (ln_row_consts / ln_norm)
 //            against hvo_layernorm on random and degenerate rows over the
 //            exponent range the kernel takes it for.
@@ -101,6 +102,34 @@ static long check_exp_t() {
   for (int x = -(1 << 25); x <= 0; ++x) one(x);
   std::mt19937_64 rng(11);
   for (int i = 0; i < 1000000; ++i) one(-(int)(rng() % 2147483647u));
+  return bad;
+}
+
+// softmax_exp_qm (the row maximum folded into its constants) against
+// softmax_exp_t of the difference over random maxima and arguments, and
+// the premise of the kernel's clamp vote: over [-17 * 45426, 0] no
+// exponential exceeds exp(0) = kSoftmaxExp0 (it steps down at segment
+// boundaries, so it is not monotone, but each segment below the top one
+// stays under half of it).
+static long check_exp_qm() {
+  long bad = 0;
+  for (int t = -17 * 45426; t <= 0; ++t)
+    if (softmax_exp_t(t) > kSoftmaxExp0 && ++bad < 5)
+      std::printf("softmax_exp_t above exp(0) at %d\n", t);
+  if (softmax_exp_t(0) != kSoftmaxExp0) ++bad;
+  std::mt19937_64 rng(13);
+  for (int i = 0; i < 4000000; ++i) {
+    const int mx = (int)(rng() % (1u << 24)) - (1 << 23);
+    const int lo = mx - 17 * 45426;
+    int q = mx - (int)(rng() % (20 * 45426));
+    if (i % 7 == 0) q = mx - (int)(rng() % 64);
+    const int qc = q > lo ? q : lo;
+    const long long k1 = (16ll << 32) + 94549ll * mx;
+    const unsigned c1 = (unsigned)(88670 - 16 * 45426) - (unsigned)mx;
+    const int t = q - mx > -17 * 45426 ? q - mx : -17 * 45426;
+    if (softmax_exp_qm(qc, k1, c1) != softmax_exp_t(t))
+      if (++bad < 5) std::printf("softmax_exp_qm mismatch q %d mx %d\n", q, mx);
+  }
   return bad;
 }
 
@@ -204,7 +233,8 @@ static long check_layernorm(int rows) {
 int main(int argc, char **argv) {
   const int rows = argc > 1 ? std::atoi(argv[1]) : 100000;
   const long g = check_gelu(),
-             s = check_softmax(rows) + check_recip24() + check_exp() + check_exp_nx() + check_exp_t(),
+             s = check_softmax(rows) + check_recip24() + check_exp() + check_exp_nx() + check_exp_t() +
+                 check_exp_qm(),
              l = check_layernorm(rows) + check_round_div_d();
   std::printf("gelu_bad=%ld softmax_bad=%ld layernorm_bad=%ld\n", g, s, l);
   return (g || s || l) ? 1 : 0;
