@@ -313,6 +313,47 @@ __device__ __forceinline__ void gelu_table_u8_n(const int (&q)[N], unsigned (&o)
     o[j] = off >= __builtin_amdgcn_ubfe(w[j], 16, 8) ? w[j] >> 8 : w[j];
   }
 }
+// gelu_table_u8_n with the results packed four to a word (value j in byte
+// j % 4 of word j / 4): instead of shifting each entry past its change and
+// packing the low bytes, one byte permute per pair of entries picks byte 0
+// or 1 of each (the selector from the two comparisons), and a third joins
+// the pairs.
+template <int N>
+__device__ __forceinline__ void gelu_table_pack_n(const int (&q)[N], unsigned (&o)[N / 4],
+                                                  const unsigned *lut, int cb, int qlo, int qhi) {
+  static_assert(N % 4 == 0, "whole words");
+  const char *t = reinterpret_cast<const char *>(lut);
+  int c[N], w1[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    asm("v_med3_i32 %0, %1, %2, %3" : "=v"(c[j]) : "v"(q[j]), "v"(qlo), "v"(qhi));
+    int b = c[j] >> kGeluCoarseShift;
+    asm("" : "+v"(b));
+    w1[j] = *reinterpret_cast<const int *>(t + cb + b * 4);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  unsigned w[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j)
+    w[j] = *reinterpret_cast<const unsigned *>(t + (w1[j] >> 5) + (c[j] >> (w1[j] & 31)) * 4);
+  __builtin_amdgcn_sched_barrier(0);
+  unsigned pair[N / 2];
+#pragma unroll
+  for (int k = 0; k < N / 2; ++k) {
+    const int a = 2 * k, b = a + 1;
+    const bool pa = __builtin_amdgcn_ubfe((unsigned)c[a], 0, (unsigned)w1[a]) >=
+                    __builtin_amdgcn_ubfe(w[a], 16, 8);
+    const bool pb = __builtin_amdgcn_ubfe((unsigned)c[b], 0, (unsigned)w1[b]) >=
+                    __builtin_amdgcn_ubfe(w[b], 16, 8);
+    // bytes 0-3 of the pool are w[a], 4-7 w[b]; the upper two bytes zero
+    const unsigned sel = (pb ? 0x0c0c0500u : 0x0c0c0400u) + (pa ? 1u : 0u);
+    pair[k] = __builtin_amdgcn_perm(w[b], w[a], sel);
+  }
+#pragma unroll
+  for (int k = 0; k < N / 4; ++k)
+    o[k] = __builtin_amdgcn_perm(pair[2 * k + 1], pair[2 * k], 0x05040100u);
+}
+
 // The same as a sign-extended int.
 __device__ __forceinline__ int gelu_table(int q, const unsigned *lut, int cb, int qlo, int qhi) {
   return (int)(int8_t)gelu_table_u8(q, lut, cb, qlo, qhi);

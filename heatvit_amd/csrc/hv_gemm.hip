@@ -126,8 +126,7 @@ __device__ __forceinline__ void stage_lut(const GemmArgs &g, unsigned *lut) {
 }
 
 __device__ __forceinline__ int pack4(int a, int b, int c, int d) {
-  return (int)((unsigned)(a & 0xFF) | ((unsigned)(b & 0xFF) << 8) | ((unsigned)(c & 0xFF) << 16) |
-               ((unsigned)d << 24));
+  return (int)pack_lo4((unsigned)a, (unsigned)b, (unsigned)c, (unsigned)d);
 }
 
 
@@ -974,15 +973,14 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
     // Weight fragments single-buffered: the next column tile's load is
     // issued after the current tile's MFMAs and lands during its GELU
     // epilogues; the biases are double-buffered.
-    v4i bf[6], bs[2][4];
-    auto load_w1 = [&](int ci, v4i (&bi)[4]) {
+    v4i bf[6];
+    v16i bs[2];
+    auto load_w1 = [&](int ci, v16i &bi) {
       const int ct = wave + 4 * ci;
 #pragma unroll
       for (int kt = 0; kt < 6; ++kt)
         bf[kt] = *reinterpret_cast<const v4i *>(g1.b + (size_t)(ct * 6 + kt) * 1024 + lane * 16);
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        bi[q] = *reinterpret_cast<const v4i *>(g1.bias + ct * 32 + 16 * h + 4 * q);
+      bi = *reinterpret_cast<const v16i *>(g1.bias + ct * 32 + 16 * h);
     };
     // Phase P (PJ): y tiles wave, wave + 4, wave + 8 of the 2 x 6 (phase B's
     // tiles), K = 192 from the ctx rows; their bytes stay in yres and go to
@@ -1071,10 +1069,11 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
     for (int ci = 0; ci < 6; ++ci) {
       const int cur = ci & 1;
       const int c0 = (wave + 4 * ci) * 32 + 16 * h;
+      // the accumulators start at the bias (the first MFMA's C operand)
       v16i acc[2];
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
-        acc[rt] = v16i{0};
+        acc[rt] = bs[cur];
 #pragma unroll
         for (int kt = 0; kt < 6; ++kt)
           acc[rt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[kt], af[rt][kt], acc[rt], 0, 0, 0);
@@ -1082,35 +1081,34 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
       if (ci + 1 < 6) load_w1(ci + 1, bs[cur ^ 1]);
       bool fast = all1;
       if (!all1) {
-        int bmax = bs[cur][0][0], bmin = bmax;
+        int bmax = bs[cur][0], bmin = bmax;
 #pragma unroll
         for (int j = 1; j < 16; ++j) {
-          bmax = max(bmax, bs[cur][j >> 2][j & 3]);
-          bmin = min(bmin, bs[cur][j >> 2][j & 3]);
+          bmax = max(bmax, bs[cur][j]);
+          bmin = min(bmin, bs[cur][j]);
         }
         fast = __all(bmax <= g1.acc_lim && bmin >= -g1.acc_lim);
       }
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
-        int o[16];
+        v4i ow;
         if (fast) {
           int qv[16];
-          unsigned ov[16];
+          unsigned ov[4];
 #pragma unroll
-          for (int j = 0; j < 16; ++j)
-            qv[j] = shift_nowrap<LA1>(acc[rt][j] + bs[cur][j >> 2][j & 3], r1a);
-          gelu_table_u8_n<16>(qv, ov, lut, g1.lut_cb, g1.lut_qlo, qhi);
-#pragma unroll
-          for (int j = 0; j < 16; ++j) o[j] = (int)ov[j];
+          for (int j = 0; j < 16; ++j) qv[j] = shift_nowrap<LA1>(acc[rt][j], r1a);
+          gelu_table_pack_n<16>(qv, ov, lut, g1.lut_cb, g1.lut_qlo, qhi);
+          ow = v4i{(int)ov[0], (int)ov[1], (int)ov[2], (int)ov[3]};
         } else {
+          int o[16];
 #pragma unroll
           for (int j = 0; j < 16; ++j)
-            o[j] = epi_exact(EPI_GELU, acc[rt][j], bs[cur][j >> 2][j & 3], 0, g1.shift_a,
+            o[j] = epi_exact(EPI_GELU, acc[rt][j] - bs[cur][j], bs[cur][j], 0, g1.shift_a,
                              g1.shift_b, 0, 0, 0)[0];
+          ow = v4i{pack4(o[0], o[1], o[2], o[3]), pack4(o[4], o[5], o[6], o[7]),
+                   pack4(o[8], o[9], o[10], o[11]), pack4(o[12], o[13], o[14], o[15])};
         }
-        *reinterpret_cast<v4i *>(&hid[(32 * rt + l32) * kFfnHRow + c0]) =
-            v4i{pack4(o[0], o[1], o[2], o[3]), pack4(o[4], o[5], o[6], o[7]),
-                pack4(o[8], o[9], o[10], o[11]), pack4(o[12], o[13], o[14], o[15])};
+        *reinterpret_cast<v4i *>(&hid[(32 * rt + l32) * kFfnHRow + c0]) = ow;
       }
     }
     // The first phase-B tile's operands and first weight chunk load before
@@ -1334,7 +1332,7 @@ __global__ __launch_bounds__(512, 4) void k_ffn32(GemmArgs g1, GemmArgs g2, LnPr
   // Phase A: column tiles wave + 8 ci; the next tile's weight fragments load
   // during the current tile's GELU epilogue, its biases during its MFMAs.
   {
-    v4i bf[6], bs[4];
+    v4i bf[6];
     auto load_w1 = [&](int ci) {
       const int ct = wave + 8 * ci;
 #pragma unroll
@@ -1345,46 +1343,46 @@ __global__ __launch_bounds__(512, 4) void k_ffn32(GemmArgs g1, GemmArgs g2, LnPr
 #pragma unroll
     for (int ci = 0; ci < 3; ++ci) {
       const int c0 = (wave + 8 * ci) * 32 + 16 * h;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) bs[q] = *reinterpret_cast<const v4i *>(g1.bias + c0 + 4 * q);
-      v16i acc = v16i{0};
+      // the accumulator starts at the bias (the first MFMA's C operand)
+      const v16i bs = *reinterpret_cast<const v16i *>(g1.bias + c0);
+      v16i acc = bs;
 #pragma unroll
       for (int kt = 0; kt < 6; ++kt)
         acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[kt], af[kt], acc, 0, 0, 0);
       if (ci + 1 < 3) load_w1(ci + 1);
       bool fast = all1;
       if (!all1) {
-        int bmax = bs[0][0], bmin = bmax;
+        int bmax = bs[0], bmin = bmax;
 #pragma unroll
         for (int j = 1; j < 16; ++j) {
-          bmax = max(bmax, bs[j >> 2][j & 3]);
-          bmin = min(bmin, bs[j >> 2][j & 3]);
+          bmax = max(bmax, bs[j]);
+          bmin = min(bmin, bs[j]);
         }
         fast = __all(bmax <= g1.acc_lim && bmin >= -g1.acc_lim);
       }
-      int o[16];
+      v4i ow;
       if (fast) {
         // the lookups in two stages of eight (registers)
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
           int qv[8];
-          unsigned ov[8];
+          unsigned ov[2];
 #pragma unroll
-          for (int j = 0; j < 8; ++j)
-            qv[j] = shift_nowrap<LA1>(acc[8 * hf + j] + bs[2 * hf + (j >> 2)][j & 3], r1a);
-          gelu_table_u8_n<8>(qv, ov, lut, g1.lut_cb, g1.lut_qlo, qhi);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) o[8 * hf + j] = (int)ov[j];
+          for (int j = 0; j < 8; ++j) qv[j] = shift_nowrap<LA1>(acc[8 * hf + j], r1a);
+          gelu_table_pack_n<8>(qv, ov, lut, g1.lut_cb, g1.lut_qlo, qhi);
+          ow[2 * hf] = (int)ov[0];
+          ow[2 * hf + 1] = (int)ov[1];
         }
       } else {
+        int o[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j)
-          o[j] = epi_exact(EPI_GELU, acc[j], bs[j >> 2][j & 3], 0, g1.shift_a, g1.shift_b, 0, 0,
+          o[j] = epi_exact(EPI_GELU, acc[j] - bs[j], bs[j], 0, g1.shift_a, g1.shift_b, 0, 0,
                            0)[0];
+        ow = v4i{pack4(o[0], o[1], o[2], o[3]), pack4(o[4], o[5], o[6], o[7]),
+                 pack4(o[8], o[9], o[10], o[11]), pack4(o[12], o[13], o[14], o[15])};
       }
-      *reinterpret_cast<v4i *>(&hid[l32 * kFfnHRow + c0]) =
-          v4i{pack4(o[0], o[1], o[2], o[3]), pack4(o[4], o[5], o[6], o[7]),
-              pack4(o[8], o[9], o[10], o[11]), pack4(o[12], o[13], o[14], o[15])};
+      *reinterpret_cast<v4i *>(&hid[l32 * kFfnHRow + c0]) = ow;
     }
   }
   // Phase B: wavefront w < 6 takes FFN2 column tile w over K = 768 in chunks
