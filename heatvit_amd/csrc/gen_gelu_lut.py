@@ -18,9 +18,12 @@ change).  Table layout (32-bit words):
   (L1 holds n1e words, its length rounded up to even; L2 follows it)
   L2, one word per 2^s2 values of c, at most one change inside it: byte 0
       G at the entry's first c, byte 1 G from the change on (byte 0 again
-      when there is none), byte 2 the change's offset inside the entry
-      (< 2^s2 <= 256).  The lookup is byte 1 when c mod 2^s2 >= byte 2, else
-      byte 0: one byte compare and one byte select.
+      when there is none), bits 16..31 the low 16 bits of the c at which
+      the change happens (the entry's first c when there is none).  An
+      entry's 2^s2 <= 256 values of c lie inside one aligned block of 2^16,
+      so comparing low 16 bits compares the values: the lookup is byte 1
+      when (c mod 2^16) >= bits 16..31, else byte 0 (one 16-bit compare and
+      one byte select).
   G is constant for q <= qlo and for q >= qhi.  Each table is padded to a
   multiple of four words, so tables start on 16-byte boundaries.  s2 is the
   largest value in [0, S1] that leaves at most one change inside every entry
@@ -104,12 +107,13 @@ def build_table(so, q, o):
         for fb in range(1 << (S1 - s2)):
             u0 = lo + (fb << s2)
             t0 = int(uo[min(u0, span)])
-            t1, at = t0, 255
+            t1, at = t0, 0
             for c in sel[(sel >> s2) == fb]:
                 d = int(c) - (fb << s2)
                 if d:                           # d == 0: t0 already holds it
                     t1, at = int(uo[lo + c]), d
-            l2.append((t0 & 255) | ((t1 & 255) << 8) | (at << 16))
+            cabs = qlo + u0 + at                # the c of the change
+            l2.append((t0 & 255) | ((t1 & 255) << 8) | ((cabs & 0xFFFF) << 16))
     return qlo, qhi, l1, np.array(l2, np.uint32)
 
 
@@ -125,9 +129,8 @@ def lookup(qlo, qhi, l1, l2, q):
     n1e = len(l1) + (len(l1) & 1)
     # byte address in the whole table (L1, padding, L2) -> L2 word index
     f2 = ((w1 >> 5) + 4 * (c >> s2)) // 4 - n1e
-    off = c & ((1 << s2) - 1)
     a = l2[f2].astype(np.int64)
-    return sx(np.where(off >= ((a >> 16) & 255), (a >> 8) & 255, a & 255), 8)
+    return sx(np.where((c & 0xFFFF) >= ((a >> 16) & 0xFFFF), (a >> 8) & 255, a & 255), 8)
 
 
 def main(out):

@@ -266,10 +266,12 @@ __device__ __forceinline__ int gelu_post(i64 v, int shift_in, int shift_out) {
 // the byte offset that makes (c >> kGeluCoarseShift) << 2 address the coarse
 // words.  The coarse word of c = clamp(q) holds s2 in its low five bits and,
 // above them, a byte offset such that c's entry sits at offset + 4 * (c >>
-// s2); the word itself is the shift amount and the field width (the hardware
-// reads their low five bits).  The entry's bytes are the value before and
-// after its one change and the change's offset: the result is the value in
-// the low byte of the returned word (the upper bits are not cleared).
+// s2); the word itself is the shift amount (the hardware reads its low five
+// bits).  The entry's bytes 0 and 1 are the value before and after its one
+// change and bits 16..31 the low 16 bits of the c where it changes (an
+// entry's values of c share one aligned block of 2^16, so the low halves
+// compare as the values): the result is the value in the low byte of the
+// returned word (the upper bits are not cleared).
 constexpr int kGeluCoarseShift = 8;
 
 __device__ __forceinline__ unsigned gelu_table_u8(int q, const unsigned *lut, int cb, int qlo,
@@ -280,9 +282,8 @@ __device__ __forceinline__ unsigned gelu_table_u8(int q, const unsigned *lut, in
   int b = c >> kGeluCoarseShift;
   asm("" : "+v"(b));  // keeps b * 4 + cb one shift-add (not a shift, mask and add)
   const int w1 = *reinterpret_cast<const int *>(t + cb + b * 4);
-  const unsigned off = __builtin_amdgcn_ubfe((unsigned)c, 0, (unsigned)w1);  // c mod 2^s2
   const unsigned w = *reinterpret_cast<const unsigned *>(t + (w1 >> 5) + (c >> (w1 & 31)) * 4);
-  return off >= __builtin_amdgcn_ubfe(w, 16, 8) ? w >> 8 : w;
+  return ((unsigned)c & 0xFFFFu) >= (w >> 16) ? w >> 8 : w;
 }
 
 // gelu_table_u8 of N values in stages (the N coarse reads, then the N
@@ -308,10 +309,7 @@ __device__ __forceinline__ void gelu_table_u8_n(const int (&q)[N], unsigned (&o)
     w[j] = *reinterpret_cast<const unsigned *>(t + (w1[j] >> 5) + (c[j] >> (w1[j] & 31)) * 4);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int j = 0; j < N; ++j) {
-    const unsigned off = __builtin_amdgcn_ubfe((unsigned)c[j], 0, (unsigned)w1[j]);
-    o[j] = off >= __builtin_amdgcn_ubfe(w[j], 16, 8) ? w[j] >> 8 : w[j];
-  }
+  for (int j = 0; j < N; ++j) o[j] = ((unsigned)c[j] & 0xFFFFu) >= (w[j] >> 16) ? w[j] >> 8 : w[j];
 }
 // gelu_table_u8_n with the results packed four to a word (value j in byte
 // j % 4 of word j / 4): instead of shifting each entry past its change and
@@ -341,12 +339,16 @@ __device__ __forceinline__ void gelu_table_pack_n(const int (&q)[N], unsigned (&
 #pragma unroll
   for (int k = 0; k < N / 2; ++k) {
     const int a = 2 * k, b = a + 1;
-    const bool pa = __builtin_amdgcn_ubfe((unsigned)c[a], 0, (unsigned)w1[a]) >=
-                    __builtin_amdgcn_ubfe(w[a], 16, 8);
-    const bool pb = __builtin_amdgcn_ubfe((unsigned)c[b], 0, (unsigned)w1[b]) >=
-                    __builtin_amdgcn_ubfe(w[b], 16, 8);
+    const bool pb = ((unsigned)c[b] & 0xFFFFu) >= (w[b] >> 16);
+    // entry a's comparison as a lane mask, added as the carry-in of one
+    // add (the compiler otherwise spends a select and an or on it)
+    const unsigned long long pa =
+        __builtin_amdgcn_uicmp((unsigned)c[a] & 0xFFFFu, w[a] >> 16, 35 /* unsigned >= */);
     // bytes 0-3 of the pool are w[a], 4-7 w[b]; the upper two bytes zero
-    const unsigned sel = (pb ? 0x0c0c0500u : 0x0c0c0400u) + (pa ? 1u : 0u);
+    const unsigned selb = pb ? 0x0c0c0500u : 0x0c0c0400u;
+    unsigned sel;
+    unsigned long long carry_out;
+    asm("v_addc_co_u32_e64 %0, %1, %2, 0, %3" : "=v"(sel), "=s"(carry_out) : "v"(selb), "s"(pa));
     pair[k] = __builtin_amdgcn_perm(w[b], w[a], sel);
   }
 #pragma unroll
