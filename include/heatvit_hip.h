@@ -300,8 +300,9 @@ int hv_selector_forward(const hv_selector_dev *p, const int8_t *tokens, const in
                         void *workspace, size_t workspace_bytes, hv_stream_t stream);
 
 /* hv_selector_forward with no workspace argument and no allocation: the
- * head scores and statistics live in a fixed device array of the library
- * (about 3 MB per GPU, held until the process ends), so callers that cannot
+ * package rows (192 bytes per image) and the offset scratch live in a fixed
+ * 256 KiB device array of the library (per GPU, held until the process
+ * ends), so callers that cannot
  * call hipMalloc (code under HIP graph capture, serving loops, harnesses
  * that forbid allocation) can run the selector.  No counterpart in the
  * reference.  batch <= HV_SELECTOR_NOALLOC_MAX_BATCH (HV_EVALUE /
