@@ -566,6 +566,100 @@ __host__ __device__ __forceinline__ LnRow ln_row_consts(int sx, int sxx, int s, 
   return r;
 }
 
+// ln_row_consts from double-precision steps that are exact by their error
+// bounds, for sx = sum x and sxx = sum x^2 of 192 int8 values, s in
+// [16, 28] and t = 2 s - 32.  E supplies two estimates that the code
+// corrects exactly: a float square root and a double reciprocal (the
+// hardware's v_sqrt_f32 / v_rcp_f64 on the device).
+//   mean = round_div(sx 2^s, 192) = floor((sx 2^(s-6) + 1) / 3): n / 3 has
+//     fractional part 0, 1/3 or 2/3 (no ties); the product with the double
+//     nearest 1/3 is within 2^-17 of n / 3, so adding 2^-10 before the floor
+//     gives it exactly;
+//   e2 = floor((sxx 2^t + 96) / 192) the same way (fractions in steps of
+//     1/192, error below 2^-13);
+//   mean_sq = floor((mean^2 + 2^31) / 2^32) from u = |mean| 2^-16: u^2 =
+//     hi + lo exactly (fma), and u^2 - floor(hi) is a multiple of 2^-32
+//     below 2, so its double sum is exact;
+//   sd = isqrt(var + 4295) from the float estimate (within one), corrected
+//     by the exact sign of sd^2 - x and (sd + 1)^2 - x;
+//   inv = round_div(2^48, sd) from the reciprocal estimate after one Newton
+//     step: the floor is within one, and the exact remainder fixes it and
+//     decides the rounding;
+//   A = inv 2^s and C = 2^47 - mean inv split into the limbs of
+//     ln_row_consts (double floors for A; 24-bit halves of mean and inv and
+//     64-bit products with carries for C).
+template <typename E>
+__host__ __device__ __forceinline__ LnRow ln_row_consts_e(int sx, int sxx, int s, int t) {
+#pragma clang fp contract(off)
+  LnRow r;
+  const double third = 1.0 / 3.0;
+  const double nm = ldexp((double)sx, s - 6) + 1.0;
+  const double mean = floor(fma(nm, third, 0x1p-10));
+  const double n2 = ldexp((double)sxx, t) + 96.0;
+  const double e2 = floor(fma(n2, third * 0x1p-6, 0x1p-10));
+  const double u = fabs(mean) * 0x1p-16;
+  const double hi = u * u, lo = fma(u, u, -hi), fh = floor(hi);
+  const double mean_sq = fh + (((hi - fh) + lo) >= 0.5 ? 1.0 : 0.0);
+  double var = e2 - mean_sq;
+  r.neg_var = var < 0.0;
+  if (var < 0.0) var = 0.0;
+  const double x = var + 4295.0;
+  double sd = floor((double)E::sqrt_est((float)x));
+  {
+    const double d = fma(sd, sd, -x);  // sd^2 - x, exact
+    sd = d > 0.0 ? sd - 1.0 : ((d + 2.0 * sd + 1.0) <= 0.0 ? sd + 1.0 : sd);
+  }
+  double rc = E::rcp_est(sd);
+  rc = fma(rc, fma(-sd, rc, 1.0), rc);
+  double inv = floor(0x1p48 * rc);
+  double rem = fma(-inv, sd, 0x1p48);  // exact
+  if (rem < 0.0) {
+    inv -= 1.0;
+    rem += sd;
+  } else if (rem >= sd) {
+    inv += 1.0;
+    rem -= sd;
+  }
+  if (2.0 * rem >= sd) inv += 1.0;
+  // A = inv 2^s = a0 + a1 2^24 + a2 2^48 (signed 24-bit limbs)
+  const double A = ldexp(inv, s);
+  double h1 = floor(A * 0x1p-24), l0 = fma(-h1, 0x1p24, A);
+  if (l0 >= 0x1p23) {
+    l0 -= 0x1p24;
+    h1 += 1.0;
+  }
+  double h2 = floor(h1 * 0x1p-24), l1 = fma(-h2, 0x1p24, h1);
+  if (l1 >= 0x1p23) {
+    l1 -= 0x1p24;
+    h2 += 1.0;
+  }
+  r.a0 = (int)l0;
+  r.a1 = (int)l1;
+  r.a2 = (int)h2;
+  // C = 2^47 - mean inv with mean = m2 2^24 + m1, inv = i1 2^24 + i0
+  const double m2d = floor(mean * 0x1p-24), i1d = floor(inv * 0x1p-24);
+  const int m2 = (int)m2d, m1 = (int)fma(-m2d, 0x1p24, mean);
+  const int i1 = (int)i1d, i0 = (int)fma(-i1d, 0x1p24, inv);
+  const i64 p0 = (i64)((u64)(unsigned)m1 * (unsigned)i0);
+  const i64 p1 = (i64)m2 * i0 + (i64)m1 * i1;
+  const i64 p2 = (i64)m2 * i1;
+  const i64 t0 = (1ll << 47) - p0;
+  r.c0 = (int)(t0 & 0xFFFFFF);
+  const i64 t1 = (t0 >> 24) - p1;
+  r.c1 = (int)(t1 & 0xFFFFFF);
+  const i64 c2 = (t1 >> 24) - p2;
+  r.c2 = c2 > (1 << 30) ? (1 << 30) : (c2 < -(1 << 30) ? -(1 << 30) : (int)c2);
+  const double xt = floor(ldexp(mean - 1.0, -s));
+  r.xt = xt > 127.0 ? 127 : (xt < -129.0 ? -129 : (int)xt);
+  return r;
+}
+
+// The device's estimates for ln_row_consts_e.
+struct LnEstHw {
+  __device__ static float sqrt_est(float x) { return __builtin_amdgcn_sqrtf(x); }
+  __device__ static double rcp_est(double x) { return __builtin_amdgcn_rcp(x); }
+};
+
 // v sign-extended from bit 23.  The limbs a0, a1, a2 already are signed
 // 24-bit values; restating it where they are used lets the compiler emit
 // v_mad_i32_i24 for the limb products even when the row constants arrive
@@ -608,7 +702,7 @@ __device__ __forceinline__ bool ln32_row(const int (&w)[48 / LPR], const int (&g
     sx += __shfl_xor(sx, off);
     sxx += __shfl_xor(sxx, off);
   }
-  const LnRow r = ln_row_consts(sx, sxx, ln.s, ln.t);
+  const LnRow r = ln_row_consts_e<LnEstHw>(sx, sxx, ln.s, ln.t);
   const int rnd = 1 << (ln.os - 1);
 #pragma unroll
   for (int q = 0; q < NW; ++q) out[q] = 0;

@@ -854,7 +854,7 @@ __device__ __forceinline__ void ln_rows(const int8_t *src, int clamp, int8_t *ds
       sxx[r] += __shfl_xor(sxx[r], off);
     }
   const int mr = sub & 1;
-  const LnRow mine = ln_row_consts(mr ? sx[1] : sx[0], mr ? sxx[1] : sxx[0], ln.s, ln.t);
+  const LnRow mine = ln_row_consts_e<LnEstHw>(mr ? sx[1] : sx[0], mr ? sxx[1] : sxx[0], ln.s, ln.t);
   if (sub < 2 && mine.neg_var && lw.img_warn && grp + 32 * sub < report_rows)
     ln_warn_row(lw.offsets, lw.batch, lw.img_warn, r0 + grp + 32 * sub);
   const int rnd = 1 << (ln.os - 1);

@@ -156,7 +156,7 @@ __device__ __forceinline__ void ln32_groups(const int8_t *__restrict__ x, const 
       msx = (sub % R) == r ? sx[r] : msx;
       msxx = (sub % R) == r ? sxx[r] : msxx;
     }
-    const LnRow mine = ln_row_consts(msx, msxx, ln.s, ln.t);
+    const LnRow mine = ln_row_consts_e<LnEstHw>(msx, msxx, ln.s, ln.t);
     if (sub < R && row0 + sub < nrows) {
       if (neg_var) neg_var[row0 + sub] = mine.neg_var ? 1 : 0;
       if (mine.neg_var && lw.img_warn) ln_warn_row(lw.offsets, lw.batch, lw.img_warn, row0 + sub);

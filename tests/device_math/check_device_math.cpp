@@ -133,6 +133,60 @@ static long check_exp_qm() {
   return bad;
 }
 
+// ln_row_consts_e (double-precision steps, estimates corrected exactly)
+// against ln_row_consts field by field, for every input scale the int32
+// LayerNorm takes (s = 16..28, t = 2 s - 32), over the row sums of random
+// and degenerate int8 rows, with the square-root and reciprocal estimates
+// exact and off by several ulps either way (the hardware's are within one).
+struct LnEstExact {
+  static float sqrt_est(float x) { return std::sqrt(x); }
+  static double rcp_est(double x) { return 1.0 / x; }
+};
+template <int K>
+struct LnEstOff {
+  static float sqrt_est(float x) {
+    float v = std::sqrt(x);
+    for (int i = 0; i < (K > 0 ? K : -K); ++i) v = std::nextafter(v, K > 0 ? 1e30f : 0.0f);
+    return v;
+  }
+  static double rcp_est(double x) { return (1.0 / x) * (1.0 + K * 0x1p-24); }
+};
+
+template <typename E>
+static long ln_consts_same(int sx, int sxx, int s) {
+  const LnRow a = ln_row_consts(sx, sxx, s, 2 * s - 32), b = ln_row_consts_e<E>(sx, sxx, s, 2 * s - 32);
+  const bool same = a.a0 == b.a0 && a.a1 == b.a1 && a.a2 == b.a2 && a.c0 == b.c0 && a.c1 == b.c1 &&
+                    a.c2 == b.c2 && a.xt == b.xt && a.neg_var == b.neg_var;
+  return same ? 0 : 1;
+}
+
+static long check_ln_consts(int rows) {
+  std::mt19937_64 rng(17);
+  long bad = 0;
+  for (int it = 0; it < rows; ++it) {
+    const int kind = it % 8, base = (int)(rng() % 256) - 128, amp = 1 + (int)(rng() % 128);
+    const int outlier = (int)(rng() % 192);
+    int sx = 0, sxx = 0;
+    for (int c = 0; c < 192; ++c) {
+      int v;
+      if (kind == 0) v = base;
+      else if (kind == 1) v = c == outlier ? (rng() & 1 ? 127 : -128) : base;
+      else if (kind == 2) v = (rng() & 1) ? 127 : -128;
+      else if (kind == 3) v = base + (int)(rng() % 3) - 1;
+      else v = base + (int)(rng() % (2 * amp + 1)) - amp;
+      v = v < -128 ? -128 : (v > 127 ? 127 : v);
+      sx += v;
+      sxx += v * v;
+    }
+    for (int s = 16; s <= 28; ++s) {
+      long e = ln_consts_same<LnEstExact>(sx, sxx, s) + ln_consts_same<LnEstOff<4>>(sx, sxx, s) +
+               ln_consts_same<LnEstOff<-4>>(sx, sxx, s);
+      if (e && ++bad < 5) std::printf("ln_row_consts_e mismatch sx %d sxx %d s %d\n", sx, sxx, s);
+    }
+  }
+  return bad;
+}
+
 // round_div_pos_d (one double quotient) against round_div_pos over random
 // operands of every magnitude below 2^52, the selector's ranges included.
 static long check_round_div_d() {
@@ -235,7 +289,7 @@ int main(int argc, char **argv) {
   const long g = check_gelu(),
              s = check_softmax(rows) + check_recip24() + check_exp() + check_exp_nx() + check_exp_t() +
                  check_exp_qm(),
-             l = check_layernorm(rows) + check_round_div_d();
+             l = check_layernorm(rows) + check_round_div_d() + check_ln_consts(rows);
   std::printf("gelu_bad=%ld softmax_bad=%ld layernorm_bad=%ld\n", g, s, l);
   return (g || s || l) ? 1 : 0;
 }
