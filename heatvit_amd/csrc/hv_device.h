@@ -704,8 +704,7 @@ __device__ __forceinline__ bool ln32_row(const int (&w)[48 / LPR], const int (&g
   }
   const LnRow r = ln_row_consts_e<LnEstHw>(sx, sxx, ln.s, ln.t);
   const int rnd = 1 << (ln.os - 1);
-#pragma unroll
-  for (int q = 0; q < NW; ++q) out[q] = 0;
+  int ov[4 * NW];
 #pragma unroll
   for (int j = 0; j < 4 * NW; ++j) {
     const int sh = 8 * (j & 3);
@@ -713,10 +712,12 @@ __device__ __forceinline__ bool ln32_row(const int (&w)[48 / LPR], const int (&g
     const int g = (int)(int8_t)(gm[j >> 2] >> sh);
     const int b = (int)(int8_t)(bt[j >> 2] >> sh);
     const int a = ln_norm(xv, r) * g + b * (1 << ln.bs);
-    int o = (a + rnd + (a >> 31)) >> ln.os;
-    o = min(max(o, -128), 127);
-    out[j >> 2] |= (o & 0xFF) << sh;
+    const int o = (a + rnd + (a >> 31)) >> ln.os;
+    ov[j] = min(max(o, -128), 127);
   }
+#pragma unroll
+  for (int q = 0; q < NW; ++q)
+    out[q] = (int)pack_lo4(ov[4 * q], ov[4 * q + 1], ov[4 * q + 2], ov[4 * q + 3]);
   return r.neg_var;
 }
 

@@ -869,9 +869,7 @@ __device__ __forceinline__ void ln_rows(const int8_t *src, int clamp, int8_t *ds
     c.c1 = __shfl(mine.c1, src_lane);
     c.c2 = __shfl(mine.c2, src_lane);
     c.xt = __shfl(mine.xt, src_lane);
-    int out[6];
-#pragma unroll
-    for (int q = 0; q < 6; ++q) out[q] = 0;
+    int ov[24], out[6];
 #pragma unroll
     for (int j = 0; j < 24; ++j) {
       const int sh = 8 * (j & 3);
@@ -879,10 +877,12 @@ __device__ __forceinline__ void ln_rows(const int8_t *src, int clamp, int8_t *ds
       const int g = __builtin_amdgcn_sbfe(gw[j >> 2], sh, 8);
       const int bb = __builtin_amdgcn_sbfe(bw[j >> 2], sh, 8) * (1 << ln.bs);
       const int a = ln_norm(xv, c) * g + bb;
-      int o = (a + rnd + (a >> 31)) >> ln.os;
-      o = min(max(o, -128), 127);
-      out[j >> 2] |= (o & 0xFF) << sh;
+      const int o = (a + rnd + (a >> 31)) >> ln.os;
+      ov[j] = min(max(o, -128), 127);
     }
+#pragma unroll
+    for (int q = 0; q < 6; ++q)
+      out[q] = (int)pack_lo4(ov[4 * q], ov[4 * q + 1], ov[4 * q + 2], ov[4 * q + 3]);
     if (grp + 32 * r < store_rows) {
       int2 *yr = reinterpret_cast<int2 *>(dst + (grp + 32 * r) * DS + sub * 24);
 #pragma unroll

@@ -176,17 +176,17 @@ __device__ __forceinline__ void ln32_groups(const int8_t *__restrict__ x, const 
         c.c2 = __shfl(mine.c2, src);
         c.xt = __shfl(mine.xt, src);
       }
-      int out[6];
-#pragma unroll
-      for (int q = 0; q < 6; ++q) out[q] = 0;
+      int ov[24], out[6];
 #pragma unroll
       for (int j = 0; j < 24; ++j) {
         const int xv = __builtin_amdgcn_sbfe(w[r][j >> 2], 8 * (j & 3), 8);
         const int a = ln_norm(xv, c) * g[j] + bb[j];
-        int o = (a + rnd + (a >> 31)) >> ln.os;
-        o = min(max(o, -128), 127);
-        out[j >> 2] |= (o & 0xFF) << (8 * (j & 3));
+        const int o = (a + rnd + (a >> 31)) >> ln.os;
+        ov[j] = min(max(o, -128), 127);
       }
+#pragma unroll
+      for (int q = 0; q < 6; ++q)
+        out[q] = (int)pack_lo4(ov[4 * q], ov[4 * q + 1], ov[4 * q + 2], ov[4 * q + 3]);
       if (row0 + r < nrows) {
         int2 *yr = reinterpret_cast<int2 *>(ln.out + (size_t)(row0 + r) * 192 + sub * 24);
 #pragma unroll
