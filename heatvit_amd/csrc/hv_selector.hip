@@ -279,6 +279,23 @@ __device__ __forceinline__ void package_row(const int8_t *cand, int C, int pkg, 
   }
 }
 
+// Eight GELU post-ops of a layer from its step table in LDS, packed four
+// to a word: q = rsa(v, s) (or v << -s after the pre-clamp) with the
+// direction of the launch-uniform shift chosen once; the table's clamp
+// [qlo, qhi] lies inside the 24-bit range, so q needs no clamp of its own.
+__device__ __forceinline__ void sel_gelu_pack8(const int (&v)[8], const Rq &ra, const unsigned *lut,
+                                               const SelLut &t, unsigned (&ow)[2]) {
+  int q[8];
+  if (ra.s > 0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = (v[i] + ra.rnd + (v[i] >> 31)) >> ra.s;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = min(max(v[i], ra.vlo), ra.vhi) << -ra.s;
+  }
+  gelu_table_pack_n<8>(q, ow, lut, t.cb, t.qlo, t.qhi);
+}
+
 constexpr int kImgThreads = 1024, kXsRow = 208;
 
 // One workgroup per image (XCD-major).  Per layer, the (head, tile) units of
@@ -426,21 +443,21 @@ __global__ __launch_bounds__(kImgThreads) void k_selector_image(
         }
       }
       if (fast[0] && fast[1] && tl.off >= 0) {
-        int qv[8];
-        unsigned ov[8];
+        int vv[8];
+        unsigned ow[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           const int jb = (tv[u] & 1) * 16 + 4 * grp;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) qv[4 * u + i] = rq(acc[u][i] + bl[hh[u]][jb + i], ra);
+          for (int i = 0; i < 4; ++i) vv[4 * u + i] = acc[u][i] + bl[hh[u]][jb + i];
         }
-        gelu_table_u8_n<8>(qv, ov, lut, tl.cb, tl.qlo, tl.qhi);
+        sel_gelu_pack8(vv, ra, lut, tl, ow);
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           const int rt = tv[u] >> 1, jb = (tv[u] & 1) * 16 + 4 * grp;
           if (valid[u])
             *reinterpret_cast<unsigned *>(&act_a[(hh[u] * kCandPad + rt * 16 + col) * 32 + jb]) =
-                pack_lo4(ov[4 * u], ov[4 * u + 1], ov[4 * u + 2], ov[4 * u + 3]);
+                ow[u];
         }
       } else {
 #pragma unroll
@@ -533,22 +550,21 @@ __global__ __launch_bounds__(kImgThreads) void k_selector_image(
         acc[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(wb, a, v4i{0}, 0, 0, 0);
       }
       if (fast[0] && fast[1] && t1.off >= 0) {
-        int qv[8];
-        unsigned ov[8];
+        int vv[8];
+        unsigned ow[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           const int jb = (tv[u] & 1) * 16 + 4 * grp;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) qv[4 * u + i] = rq(acc[u][i] + (int)bb1[hh[u]][jb + i], ra);
+          for (int i = 0; i < 4; ++i) vv[4 * u + i] = acc[u][i] + (int)bb1[hh[u]][jb + i];
         }
-        gelu_table_u8_n<8>(qv, ov, lut, t1.cb, t1.qlo, t1.qhi);
+        sel_gelu_pack8(vv, ra, lut, t1, ow);
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           const int jb = (tv[u] & 1) * 16 + 4 * grp;
           if (valid[u])
             *reinterpret_cast<unsigned *>(
-                &act_b[(hh[u] * kCandPad + (tv[u] >> 1) * 16 + col) * 32 + jb]) =
-                pack_lo4(ov[4 * u], ov[4 * u + 1], ov[4 * u + 2], ov[4 * u + 3]);
+                &act_b[(hh[u] * kCandPad + (tv[u] >> 1) * 16 + col) * 32 + jb]) = ow[u];
         }
       } else {
 #pragma unroll
@@ -601,19 +617,18 @@ __global__ __launch_bounds__(kImgThreads) void k_selector_image(
         acc[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(wb, a, v4i{0}, 0, 0, 0);
       }
       if (fast[0] && fast[1] && t2.off >= 0) {
-        int qv[8];
-        unsigned ov[8];
+        int vv[8];
+        unsigned ow[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) qv[4 * u + i] = rq(acc[u][i] + bb2[hh[u]][4 * grp + i], ra);
-        gelu_table_u8_n<8>(qv, ov, lut, t2.cb, t2.qlo, t2.qhi);
+          for (int i = 0; i < 4; ++i) vv[4 * u + i] = acc[u][i] + bb2[hh[u]][4 * grp + i];
+        sel_gelu_pack8(vv, ra, lut, t2, ow);
 #pragma unroll
         for (int u = 0; u < 2; ++u)
           if (valid[u])
             *reinterpret_cast<unsigned *>(
-                &act_a[(hh[u] * kCandPad + rt[u] * 16 + col) * 16 + 4 * grp]) =
-                pack_lo4(ov[4 * u], ov[4 * u + 1], ov[4 * u + 2], ov[4 * u + 3]);
+                &act_a[(hh[u] * kCandPad + rt[u] * 16 + col) * 16 + 4 * grp]) = ow[u];
       } else {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
