@@ -944,19 +944,20 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
   __shared__ __attribute__((aligned(16))) unsigned lut[kGeluLutMaxWords];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, l32 = lane & 31;
-  const int M = g1.m_dev ? min(*g1.m_dev, g1.m) : g1.m;
-  const int nrb = (M + kFfnRows - 1) / kFfnRows;
-  if ((int)blockIdx.x >= nrb) return;  // uniform: before any barrier
   // The step table loads in one round (at most eight 16-byte vectors per
-  // thread) and lands while the first row block's LayerNorm or A fragments
-  // load; its LDS writes precede the barrier in front of phase A.  Threads
-  // past the end reload the last vector (no predicated loads or writes).
+  // thread), issued before the live row count it does not depend on, and
+  // lands while the row block's LayerNorm or A fragments load; its LDS writes
+  // precede the barrier in front of phase A.  Threads past the end reload the
+  // last vector (no predicated loads or writes).
   static_assert(kGeluLutMaxWords / 4 <= 8 * 256, "one staging round");
   const int n4 = g1.lut_words >> 2;
   v4i tv[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     tv[i] = reinterpret_cast<const v4i *>(kGeluLut + g1.lut_off)[min(tid + 256 * i, n4 - 1)];
+  const int M = g1.m_dev ? min(*g1.m_dev, g1.m) : g1.m;
+  const int nrb = (M + kFfnRows - 1) / kFfnRows;
+  if ((int)blockIdx.x >= nrb) return;  // uniform: before any barrier
   auto write_lut = [&]() {
 #pragma unroll
     for (int i = 0; i < 8; ++i) reinterpret_cast<v4i *>(lut)[min(tid + 256 * i, n4 - 1)] = tv[i];
@@ -1245,18 +1246,31 @@ __global__ __launch_bounds__(512, 4) void k_ffn32(GemmArgs g1, GemmArgs g2, LnPr
   __shared__ __attribute__((aligned(16))) unsigned lut[kGeluLutMaxWords];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, l32 = lane & 31;
-  const int M = g1.m_dev ? min(*g1.m_dev, g1.m) : g1.m;
-  if ((int)blockIdx.x >= (M + kFfn32Rows - 1) / kFfn32Rows) return;  // uniform
-  const int r0 = blockIdx.x * kFfn32Rows;
-  const int arow = min(r0 + l32, M - 1);
-  // the step table in one round of at most four 16-byte vectors per thread,
-  // written to LDS before the barrier in front of phase A
+  // Loads that need no row index go out before the live row count, whose
+  // latency they share: the step table in one round of at most four 16-byte
+  // vectors per thread (written to LDS before the barrier in front of phase
+  // A) and, with PJ, wavefront w < 6's projection weights and biases.
   static_assert(kGeluLutMaxWords / 4 <= 4 * 512, "one staging round");
   const int n4 = g1.lut_words >> 2;
   v4i tv[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     tv[i] = reinterpret_cast<const v4i *>(kGeluLut + g1.lut_off)[min(tid + 512 * i, n4 - 1)];
+  v4i pw[6], pb4[4];
+  if constexpr (PJ) {
+    if (wave < 6) {
+      const int8_t *bp = gp.b + (size_t)wave * 6 * 1024 + lane * 16;
+#pragma unroll
+      for (int kt = 0; kt < 6; ++kt) pw[kt] = *reinterpret_cast<const v4i *>(bp + kt * 1024);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        pb4[q] = *reinterpret_cast<const v4i *>(gp.bias + wave * 32 + 16 * h + 4 * q);
+    }
+  }
+  const int M = g1.m_dev ? min(*g1.m_dev, g1.m) : g1.m;
+  if ((int)blockIdx.x >= (M + kFfn32Rows - 1) / kFfn32Rows) return;  // uniform
+  const int r0 = blockIdx.x * kFfn32Rows;
+  const int arow = min(r0 + l32, M - 1);
   auto write_lut = [&]() {
 #pragma unroll
     for (int i = 0; i < 4; ++i) reinterpret_cast<v4i *>(lut)[min(tid + 512 * i, n4 - 1)] = tv[i];
@@ -1277,16 +1291,9 @@ __global__ __launch_bounds__(512, 4) void k_ffn32(GemmArgs g1, GemmArgs g2, LnPr
       const Rq rpa = rq_setup(gp.shift_a, -128, 127), rpb = rq_setup(gp.os, -128, 127);
       const bool allp = tensor_narrow(gp.bias_max, gp.acc_lim);
       const int8_t *ap = gp.a + (size_t)arow * 192 + 16 * h;
-      const int8_t *bp = gp.b + (size_t)ct * 6 * 1024 + lane * 16;
-      v4i pa[6], pw[6], b4[4];
+      v4i pa[6];
 #pragma unroll
-      for (int kt = 0; kt < 6; ++kt) {
-        pa[kt] = *reinterpret_cast<const v4i *>(ap + kt * 32);
-        pw[kt] = *reinterpret_cast<const v4i *>(bp + kt * 1024);
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        b4[q] = *reinterpret_cast<const v4i *>(gp.bias + ct * 32 + 16 * h + 4 * q);
+      for (int kt = 0; kt < 6; ++kt) pa[kt] = *reinterpret_cast<const v4i *>(ap + kt * 32);
       const v4i x4 =
           *reinterpret_cast<const v4i *>(gp.res + (size_t)arow * 192 + ct * 32 + 16 * h);
       v16i acc = v16i{0};
@@ -1294,10 +1301,10 @@ __global__ __launch_bounds__(512, 4) void k_ffn32(GemmArgs g1, GemmArgs g2, LnPr
       for (int kt = 0; kt < 6; ++kt)
         acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(pw[kt], pa[kt], acc, 0, 0, 0);
       switch (dirsp) {
-        case 0: yres = proj_epi<false, false>(gp, acc, b4, x4, rpa, rpb, allp); break;
-        case 1: yres = proj_epi<true, false>(gp, acc, b4, x4, rpa, rpb, allp); break;
-        case 2: yres = proj_epi<false, true>(gp, acc, b4, x4, rpa, rpb, allp); break;
-        default: yres = proj_epi<true, true>(gp, acc, b4, x4, rpa, rpb, allp); break;
+        case 0: yres = proj_epi<false, false>(gp, acc, pb4, x4, rpa, rpb, allp); break;
+        case 1: yres = proj_epi<true, false>(gp, acc, pb4, x4, rpa, rpb, allp); break;
+        case 2: yres = proj_epi<false, true>(gp, acc, pb4, x4, rpa, rpb, allp); break;
+        default: yres = proj_epi<true, true>(gp, acc, pb4, x4, rpa, rpb, allp); break;
       }
       *reinterpret_cast<v4i *>(&hid[l32 * kLnPrologueRow + ct * 32 + 16 * h]) = yres;
     }

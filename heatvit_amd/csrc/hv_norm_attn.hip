@@ -475,9 +475,9 @@ __device__ __forceinline__ void qkv_unit(const AttnArgs &g, const v4i (&w)[2][6]
 // the other of two register sets while the current one multiplies (the
 // last tile reloads its own rows).
 template <bool LA, bool NARROW, bool ISV>
-__device__ __forceinline__ void qkv_rows(const AttnArgs &g, int p, int8_t *Qs, int8_t *Ks,
-                                         int8_t *Vt, int *vsum, const int *bias_s, int row0,
-                                         int N, int h, int lane) {
+__device__ __forceinline__ void qkv_rows(const AttnArgs &g, const v4i (&w)[2][6], int p,
+                                         int8_t *Qs, int8_t *Ks, int8_t *Vt, int *vsum,
+                                         const int *bias_s, int row0, int N, int lane) {
   const int rows_k = ((N + 15) >> 4) * 16;
   const int nrt = ISV ? (N + 31) >> 5 : (rows_k + 31) >> 5;  // row tiles of the group
   const Rq rq = rq_setup(g.qkv_shift, -128, 127);
@@ -485,9 +485,7 @@ __device__ __forceinline__ void qkv_rows(const AttnArgs &g, int p, int8_t *Qs, i
   auto a_rows = [&](int rt) {
     return ln1 + (size_t)min(min(rt, nrt - 1) * 32 + (lane & 31), N - 1) * 192;
   };
-  v4i w[2][6], a0[6], a1[6];
-  qkv_load_w(w[0], g.wqkv, p * 6 + h * 2, lane);
-  qkv_load_w(w[1], g.wqkv, p * 6 + h * 2 + 1, lane);
+  v4i a0[6], a1[6];
   qkv_load_a(a0, a_rows(0));
 #pragma unroll 1
   for (int rt = 0; rt < nrt; rt += 2) {
@@ -500,23 +498,23 @@ __device__ __forceinline__ void qkv_rows(const AttnArgs &g, int p, int8_t *Qs, i
 }
 
 template <bool LA, bool NARROW>
-__device__ __forceinline__ void qkv_units(const AttnArgs &g, int8_t *Qs, int8_t *Ks, int8_t *Vt,
-                                          int *vsum, const int *bias_s, int row0, int N, int h,
-                                          int wave, int lane) {
+__device__ __forceinline__ void qkv_units(const AttnArgs &g, const v4i (&w)[2][6], int8_t *Qs,
+                                          int8_t *Ks, int8_t *Vt, int *vsum, const int *bias_s,
+                                          int row0, int N, int wave, int lane) {
   if (wave == 2)
-    qkv_rows<LA, NARROW, true>(g, 2, Qs, Ks, Vt, vsum, bias_s, row0, N, h, lane);
+    qkv_rows<LA, NARROW, true>(g, w, 2, Qs, Ks, Vt, vsum, bias_s, row0, N, lane);
   else if (wave < 2)
-    qkv_rows<LA, NARROW, false>(g, wave, Qs, Ks, Vt, vsum, bias_s, row0, N, h, lane);
+    qkv_rows<LA, NARROW, false>(g, w, wave, Qs, Ks, Vt, vsum, bias_s, row0, N, lane);
 }
 
 template <bool LA>
-__device__ __forceinline__ void qkv_head(const AttnArgs &g, int8_t *Qs, int8_t *Ks, int8_t *Vt,
-                                         int *vsum, const int *bias_s, int row0, int N, int h,
-                                         int wave, int lane) {
+__device__ __forceinline__ void qkv_head(const AttnArgs &g, const v4i (&w)[2][6], int8_t *Qs,
+                                         int8_t *Ks, int8_t *Vt, int *vsum, const int *bias_s,
+                                         int row0, int N, int wave, int lane) {
   if (tensor_narrow(g.bqkv_max, g.qkv_acc_lim))
-    qkv_units<LA, true>(g, Qs, Ks, Vt, vsum, bias_s, row0, N, h, wave, lane);
+    qkv_units<LA, true>(g, w, Qs, Ks, Vt, vsum, bias_s, row0, N, wave, lane);
   else
-    qkv_units<LA, false>(g, Qs, Ks, Vt, vsum, bias_s, row0, N, h, wave, lane);
+    qkv_units<LA, false>(g, w, Qs, Ks, Vt, vsum, bias_s, row0, N, wave, lane);
   // keys of the last 64-key chunk past the V tiles: zero (four keys of one
   // channel per dword)
   const int nv = (N + 31) >> 5, kz = nv * 32, runs = (((N + 63) >> 6) * 64 - kz) >> 2;
@@ -667,21 +665,32 @@ __global__ __launch_bounds__(256, 3) void k_attention(AttnArgs g) {
   const int L = (blockIdx.x & 7) * T8 + (blockIdx.x >> 3);
   if (L >= T) return;
   const int b = L / 3, h = L - 3 * b;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // FQ: wavefront p < 3's weight fragments of Q, K or V and the head's
+  // biases load before the row offsets, whose latency they share
+  v4i w[2][6];
+  int bias_v = 0;
+  if constexpr (FQ) {
+    if (wave < 3) {
+      qkv_load_w(w[0], g.wqkv, wave * 6 + h * 2, lane);
+      qkv_load_w(w[1], g.wqkv, wave * 6 + h * 2 + 1, lane);
+    }
+    if (tid < 192) bias_v = g.bqkv[((tid >> 6) * 6 + h * 2 + ((tid >> 5) & 1)) * 32 + (tid & 31)];
+  }
   const int row0 = g.offsets[b];
   const int N = g.offsets[b + 1] - row0;
   // Images with a token count outside [1, 197] or rows outside the
   // buffers are skipped (reported by the block's image check).
   if (N <= 0 || N > HV_MAX_TOKENS || row0 < 0 || row0 > g.rows_cap - N) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n16 = (N + 15) >> 4;  // key / query tiles
   const int n64 = (N + 63) >> 6;  // PV chunks of 64 keys
   const int8_t *qkv = FQ ? nullptr : g.qkv + (size_t)row0 * 576;
 
   if constexpr (FQ) {
     if (tid < 64) vsum[tid] = 0;
-    if (tid < 192) bias_s[tid] = g.bqkv[((tid >> 6) * 6 + h * 2 + ((tid >> 5) & 1)) * 32 + (tid & 31)];
+    if (tid < 192) bias_s[tid] = bias_v;
     __syncthreads();
-    qkv_head<FQL>(g, Qs, Ks, Vt, vsum, bias_s, row0, N, h, wave, lane);
+    qkv_head<FQL>(g, w, Qs, Ks, Vt, vsum, bias_s, row0, N, wave, lane);
   } else {
   for (int i = tid; i < n16 * 16 * 4; i += 256) {
     const int r = i >> 2, c = (i & 3) * 16;
