@@ -703,8 +703,9 @@ static int run_lds(const GemmArgs &g, hipStream_t s) {
 // registers); the other K = 192 and the K = 768 GEMMs (QKV, proj, FFN2,
 // patch embedding) the LDS-staged kernel with 128x64 tiles and two
 // persistent workgroups per CU (three per CU, one workgroup per tile,
-// 128x128 tiles and 64x128 tiles were slower); other K and the gathered
-// head rows the runtime-K direct kernel.
+// 128x128 tiles and 64x128 tiles were slower); the gathered head rows with
+// K = 192 the direct kernel with every K step loaded up front; other K the
+// runtime-K direct kernel.
 template <int EPI>
 static int dispatch(const GemmArgs &g, int a_mode, hipStream_t s) {
   if constexpr (EPI == EPI_PATCH) {
@@ -715,7 +716,13 @@ static int dispatch(const GemmArgs &g, int a_mode, hipStream_t s) {
     return run_lds<2, 1, 2, EPI_PATCH, A_PATCH, 24>(g, s);
   } else {
     if (a_mode == (A_ROWS | A_UNSIGNED)) return run<1, 1, 2, EPI, A_ROWS | A_UNSIGNED, 0>(g, s);
-    if (a_mode == A_GATHER) return run<1, 1, 2, EPI, A_GATHER, 0>(g, s);
+    if (a_mode == A_GATHER) {
+      // the classifier head (K = 192 on the CLS rows): every fragment in
+      // flight at once, one memory round trip instead of six
+      if constexpr (EPI == EPI_I32)
+        if (g.k == 192) return run<1, 1, 2, EPI, A_GATHER, 6>(g, s);
+      return run<1, 1, 2, EPI, A_GATHER, 0>(g, s);
+    }
     if (a_mode != A_ROWS) return fail(HV_EVALUE, HV_ERR_OPCODE, "gemm: bad A mode %d", a_mode);
     if constexpr (EPI == EPI_GELU) {
       if (g.k == 192) return run<1, 1, 2, EPI, A_ROWS, 6>(g, s);
@@ -1309,8 +1316,16 @@ __global__ __launch_bounds__(512, 4) void k_ffn32(GemmArgs g1, GemmArgs g2, LnPr
       *reinterpret_cast<v4i *>(&hid[l32 * kLnPrologueRow + ct * 32 + 16 * h]) = yres;
     }
   }
-  // Phase A operands: the row tile's A fragments (LayerNorm 2 rows through
-  // hid, or the caller's rows).
+  // Phase A's first weight tile loads during LayerNorm 2; the row tile's A
+  // fragments come through hid (LayerNorm 2 rows) or from the caller's rows.
+  v4i bf[6];
+  auto load_w1 = [&](int ci) {
+    const int ct = wave + 8 * ci;
+#pragma unroll
+    for (int kt = 0; kt < 6; ++kt)
+      bf[kt] = *reinterpret_cast<const v4i *>(g1.b + (size_t)(ct * 6 + kt) * 1024 + lane * 16);
+  };
+  load_w1(0);
   v4i af[6];
   if constexpr (PJ) {
     write_lut();
@@ -1339,14 +1354,6 @@ __global__ __launch_bounds__(512, 4) void k_ffn32(GemmArgs g1, GemmArgs g2, LnPr
   // Phase A: column tiles wave + 8 ci; the next tile's weight fragments load
   // during the current tile's GELU epilogue, its biases during its MFMAs.
   {
-    v4i bf[6];
-    auto load_w1 = [&](int ci) {
-      const int ct = wave + 8 * ci;
-#pragma unroll
-      for (int kt = 0; kt < 6; ++kt)
-        bf[kt] = *reinterpret_cast<const v4i *>(g1.b + (size_t)(ct * 6 + kt) * 1024 + lane * 16);
-    };
-    load_w1(0);
 #pragma unroll
     for (int ci = 0; ci < 3; ++ci) {
       const int c0 = (wave + 8 * ci) * 32 + 16 * h;
@@ -1393,10 +1400,10 @@ __global__ __launch_bounds__(512, 4) void k_ffn32(GemmArgs g1, GemmArgs g2, LnPr
     }
   }
   // Phase B: wavefront w < 6 takes FFN2 column tile w over K = 768 in chunks
-  // of 4 K-steps through a ring of two chunk buffers, one chunk ahead; its
-  // operands and first weight chunk load before the barrier.
+  // of 4 K-steps through a ring of three chunk buffers, two chunks ahead;
+  // its operands and first two weight chunks load before the barrier.
   const int ct = wave;
-  v4i wb[2][4], bias4[1][4], res4[1][1];
+  v4i wb[3][4], bias4[1][4], res4[1][1];
   if (wave < 6) {
     const int arows[1] = {arow};
     if constexpr (PJ) {
@@ -1406,8 +1413,9 @@ __global__ __launch_bounds__(512, 4) void k_ffn32(GemmArgs g1, GemmArgs g2, LnPr
       epi_operands<1, 1, EPI_RES>(g2, arows, ct, h, bias4, res4);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      wb[0][j] = *reinterpret_cast<const v4i *>(g2.b + ((size_t)ct * 24 + j) * 1024 + lane * 16);
+    for (int j = 0; j < 8; ++j)
+      wb[j >> 2][j & 3] =
+          *reinterpret_cast<const v4i *>(g2.b + ((size_t)ct * 24 + j) * 1024 + lane * 16);
   }
   __syncthreads();
   if (wave < 6) {
@@ -1416,11 +1424,11 @@ __global__ __launch_bounds__(512, 4) void k_ffn32(GemmArgs g1, GemmArgs g2, LnPr
     v16i acc[1][1] = {{v16i{0}}};
 #pragma unroll
     for (int c = 0; c < 6; ++c) {
-      const int cur = c & 1, nxt = cur ^ 1;
-      if (c + 1 < 6) {
+      const int cur = c % 3, nxt = (c + 2) % 3;
+      if (c + 2 < 6) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          wb[nxt][j] = *reinterpret_cast<const v4i *>(bp + ((c + 1) * 4 + j) * 1024);
+          wb[nxt][j] = *reinterpret_cast<const v4i *>(bp + ((c + 2) * 4 + j) * 1024);
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j)
