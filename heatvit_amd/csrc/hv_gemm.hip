@@ -221,6 +221,10 @@ __device__ __forceinline__ void epi_tile(const GemmArgs &g, const v16i (&acc)[MT
           constexpr bool LA = DIRS & 1, LB = (DIRS >> 1) & 1;
           if (EPI == EPI_I8) {
             o[j] = rq_dir_nowrap<LA>(v, rq_a);
+          } else if (EPI == EPI_I32) {
+            // |acc + bias| < 2^30 and a left shift stays inside int32 (the
+            // acc_lim bound): the int32 requant needs no saturation
+            o[j] = shift_nowrap<LA>(v, rq_a);
           } else if (EPI == EPI_GELU && (DIRS & 4)) {
             // the table's clamp [qlo, qhi] lies inside the 24-bit range
             o[j] = (int)gelu_lut(shift_nowrap<LA>(v, rq_a), lut, qhi, g);
@@ -610,7 +614,8 @@ static bool fast_epilogue(const GemmArgs &g, int epi) {
   auto in = [](int s) { return s >= -30 && s <= 30; };
   if (!g.narrow_ok || !in(g.shift_a)) return false;
   switch (epi) {
-    case EPI_I8: return true;
+    case EPI_I8:
+    case EPI_I32: return true;
     case EPI_GELU: return in(g.shift_b);
     case EPI_RES:
     case EPI_PATCH: return g.da <= 21 && g.db <= 21 && in(g.os);

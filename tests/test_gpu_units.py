@@ -182,6 +182,31 @@ def test_gemm_epilogues_vs_oracle(ops, oracle, m, n, k):
         assert np.array_equal(got, want.reshape(got.shape)), (mid, rexp, out)
 
 
+@pytest.mark.parametrize("k", [192, 64])
+def test_gemm_int32_writeback_shifts(ops, oracle, k):
+    """The int32 epilogue (gemm_writeback with output_bits 32,
+    gemm.py:123-131) with right, zero and left shifts, on gathered rows
+    (the classifier head's shape at K = 192) and whole rows; the wide biases
+    put some column tiles on the exact path and the others on the int32
+    shift."""
+    rng = np.random.default_rng(k)
+    a = rng.integers(-128, 128, (300, k))
+    w = rng.integers(-128, 128, (k, 1000))
+    rows = np.sort(rng.choice(300, 64, replace=False)).astype(np.int32)
+    narrow = rng.integers(-(1 << 20), 1 << 20, 1000)
+    wide = narrow.copy()
+    wide[::97] = rng.choice([-1, 1], wide[::97].size) * ((1 << 31) - 1 - rng.integers(0, 1 << 20, wide[::97].size))
+    for bias in (narrow, wide):
+        acc_g = oracle.gemm(a[rows], w, bias)
+        acc = oracle.gemm(a, w, bias)
+        for src, dst in ((-14, -14), (-14, -9), (-20, -4), (-9, -14), (-8, -13), (-30, -2),
+                         (-4, -30)):
+            got = ops.gemm_writeback(a, w, bias, src, dst, 32, a_rows=rows)
+            assert np.array_equal(got, oracle.gemm_writeback(acc_g, src, dst, 32)), (src, dst)
+            got = ops.gemm_writeback(a, w, bias, src, dst, 32)
+            assert np.array_equal(got, oracle.gemm_writeback(acc, src, dst, 32)), (src, dst)
+
+
 def test_gemm_gather_rows(ops, oracle):
     rng = np.random.default_rng(5)
     a = rng.integers(-128, 128, (500, 192))
