@@ -509,22 +509,57 @@ __host__ __device__ __forceinline__ u64 isqrt_u64(u64 x) {
 // input scales in [-16, -4] (s = x_scale + 32 in [16, 28], the x^2 rounding
 // shift -(2*x_scale + 32) <= 0 so sum_square = (sum x^2) << t exactly).
 //
-// norm = sat24(rsa(V, 48)) with V = (x*2^s - mean) * inv = x*A - B,
-// A = inv*2^s (< 2^71), B = mean*inv.  Since inv > 0, V < 0 exactly when
-// x <= xt = floor((mean - 1) / 2^s), and rsa(V, 48) = floor(W / 2^48) with
-// W = x*A + C - [x <= xt], C = 2^47 - B.  A is split into signed 24-bit
-// limbs (a2, a1, a0) and C into (c2, c1, c0) with c1, c0 in [0, 2^24), so
-// floor(W / 2^48) follows from three 24-bit multiply-adds and two carries,
-// all inside int32 (|x*a0|, |x*a1| <= 2^30, |x*a2| <= 2^29 + 128).  c2 is
-// clamped to [-2^30, 2^30]: beyond that |x*a2 + c2 + carry| > 2^29 - 200
-// saturates to the same 24-bit bound either way.
+// norm = sat24(rsa(V, 48)) with V = (x*2^s - mean) * inv, inv =
+// round_div(2^48, sd) >= 1.  V < 0 exactly when x <= xt = floor((mean - 1)
+// / 2^s), and rsa(V, 48) = floor((V + 2^47 - n) / 2^48) with n = [V < 0].
+// With Y_n = mean*inv - 2^47 + n and K_n = ceil(Y_n / 2^s), V + 2^47 - n =
+// 2^s (x*inv - K_n) + R_n for some R_n in [0, 2^s), and a remainder below
+// 2^s does not move the floor by 2^48, so
+//   rsa(V, 48) = floor((x*inv - K_n) / 2^(48 - s)).
+// K_1 = K_0 + 1 when 2^s divides Y_0 (a "tie" row), else K_1 = K_0.  With
+// |x| <= 128, inv < 2^42 and |mean| <= 2^(s+7), x*inv - K_0 is an integer
+// of magnitude below 2^51, so one double fma of x with inv*2^(s-48) and
+// -K_0*2^(s-48) yields t = (x*inv - K_0)*2^(s-48) exactly, and floor and
+// the int32 conversion (|result| < 2^31) keep it exact.  For n = 1 on a tie
+// row the value is floor(t - 2^(s-48)): t is a multiple of 2^(s-48) < 1, so
+// that is floor(t) - 1 when t is an integer and floor(t) otherwise.
 struct LnRow {
-  int a0, a1, a2, c0, c1, c2, xt;
-  bool neg_var;
+  double inv;  // inv * 2^(s-48)
+  double add;  // -K_0 * 2^(s-48)
+  int xt;
+  bool tie, neg_var;
 };
 
-__host__ __device__ __forceinline__ int sext24(long long v) {
-  return (int)((unsigned)((unsigned long long)v << 8)) >> 8;
+// The LnRow fields from mean, inv and C = 2^47 - mean*inv given as
+// C = c2*2^48 + low, 0 <= low < 2^48: -K_0 = floor(C / 2^s) = c2*2^(48-s) +
+// (low >> s).  K_1 differs from K_0 when 2^s divides low, and then matters
+// only for an x <= xt whose t is an integer, x*inv = K_0 (mod 2^(48-s)):
+// with inv = 2^e io (io odd), such x exist when 2^e divides K_0 mod
+// 2^(48-s) and are x = (K_0 / 2^e) io^-1 (mod 2^(48-s-e)) (all x once
+// e >= 48 - s); tie marks a row where one of them lies in [-128, xt].
+__host__ __device__ __forceinline__ void ln_row_fill(LnRow &r, double mean, double inv, i64 c2,
+                                                     i64 low, int s) {
+  const i64 f = c2 * (1ll << (48 - s)) + (low >> s);
+  r.inv = ldexp(inv, s - 48);
+  r.add = ldexp((double)f, s - 48);
+  const double xt = floor(ldexp(mean - 1.0, -s));
+  r.xt = xt > 127.0 ? 127 : (xt < -129.0 ? -129 : (int)xt);
+  r.tie = false;
+  if ((low & ((1ll << s) - 1)) == 0 && r.xt >= -128) {
+    const int sh = 48 - s;
+    const u64 mm = (1ull << sh) - 1, k0 = (u64)(-f) & mm, iv = (u64)inv;
+    const int e = __builtin_ctzll(iv);
+    if (e >= sh) {
+      r.tie = k0 == 0;
+    } else if ((k0 & ((1ull << e) - 1)) == 0) {
+      const u64 io = iv >> e, pm = (1ull << (sh - e)) - 1;
+      u64 ii = io;  // io^-1 mod 2^64: each step doubles the correct low bits
+#pragma unroll
+      for (int k = 0; k < 5; ++k) ii *= 2 - io * ii;
+      const u64 rr = ((k0 >> e) * ii) & pm;
+      r.tie = -128 + (i64)((rr + 128) & pm) <= r.xt;
+    }
+  }
 }
 
 // round_div(2^48, d) for 1 <= d < 2^32: double estimate, exact correction.
@@ -537,7 +572,8 @@ __host__ __device__ __forceinline__ u64 recip48(u64 d) {
   return 2 * r >= d ? q + 1 : q;
 }
 
-// Per-row constants from the row sums sx = sum x, sxx = sum x^2.
+// Per-row constants from the row sums sx = sum x, sxx = sum x^2, in 64- and
+// 128-bit integers (the form ln_row_consts_e is checked against).
 __host__ __device__ __forceinline__ LnRow ln_row_consts(int sx, int sxx, int s, int t) {
   LnRow r;
   const i64 mean = round_div_pos((i64)sx * (1ll << s), 192);
@@ -550,19 +586,9 @@ __host__ __device__ __forceinline__ LnRow ln_row_consts(int sx, int sxx, int s, 
   if (var < 0) var = 0;
   const u64 sd = isqrt_u64((u64)var + 4295u);
   const u64 inv = recip48(sd);  // < 2^42
-  const i128 A = (i128)inv << s;
-  r.a0 = sext24((long long)(A & 0xFFFFFF));
-  const i128 A1 = (A - r.a0) >> 24;
-  r.a1 = sext24((long long)(A1 & 0xFFFFFF));
-  r.a2 = sext24((long long)((A1 - r.a1) >> 24));  // < 2^22 + 2 for s <= 28
   const i128 C = ((i128)1 << 47) - (i128)mean * (i128)inv;
-  r.c0 = (int)(C & 0xFFFFFF);
-  const i128 C1 = C >> 24;
-  r.c1 = (int)(C1 & 0xFFFFFF);
-  const i128 c2 = C1 >> 24;
-  r.c2 = c2 > (1 << 30) ? (1 << 30) : (c2 < -(1 << 30) ? -(1 << 30) : (int)c2);
-  const i64 xt = (mean - 1) >> s;
-  r.xt = xt > 127 ? 127 : (xt < -129 ? -129 : (int)xt);
+  const i128 c2 = C >> 48;
+  ln_row_fill(r, (double)mean, (double)inv, (i64)c2, (i64)(C - (c2 << 48)), s);
   return r;
 }
 
@@ -585,9 +611,8 @@ __host__ __device__ __forceinline__ LnRow ln_row_consts(int sx, int sxx, int s, 
 //   inv = round_div(2^48, sd) from the reciprocal estimate after one Newton
 //     step: the floor is within one, and the exact remainder fixes it and
 //     decides the rounding;
-//   A = inv 2^s and C = 2^47 - mean inv split into the limbs of
-//     ln_row_consts (double floors for A; 24-bit halves of mean and inv and
-//     64-bit products with carries for C).
+//   C = 2^47 - mean inv from 24-bit halves of mean and inv and 64-bit
+//     products with carries.
 template <typename E>
 __host__ __device__ __forceinline__ LnRow ln_row_consts_e(int sx, int sxx, int s, int t) {
 #pragma clang fp contract(off)
@@ -621,21 +646,6 @@ __host__ __device__ __forceinline__ LnRow ln_row_consts_e(int sx, int sxx, int s
     rem -= sd;
   }
   if (2.0 * rem >= sd) inv += 1.0;
-  // A = inv 2^s = a0 + a1 2^24 + a2 2^48 (signed 24-bit limbs)
-  const double A = ldexp(inv, s);
-  double h1 = floor(A * 0x1p-24), l0 = fma(-h1, 0x1p24, A);
-  if (l0 >= 0x1p23) {
-    l0 -= 0x1p24;
-    h1 += 1.0;
-  }
-  double h2 = floor(h1 * 0x1p-24), l1 = fma(-h2, 0x1p24, h1);
-  if (l1 >= 0x1p23) {
-    l1 -= 0x1p24;
-    h2 += 1.0;
-  }
-  r.a0 = (int)l0;
-  r.a1 = (int)l1;
-  r.a2 = (int)h2;
   // C = 2^47 - mean inv with mean = m2 2^24 + m1, inv = i1 2^24 + i0
   const double m2d = floor(mean * 0x1p-24), i1d = floor(inv * 0x1p-24);
   const int m2 = (int)m2d, m1 = (int)fma(-m2d, 0x1p24, mean);
@@ -644,13 +654,8 @@ __host__ __device__ __forceinline__ LnRow ln_row_consts_e(int sx, int sxx, int s
   const i64 p1 = (i64)m2 * i0 + (i64)m1 * i1;
   const i64 p2 = (i64)m2 * i1;
   const i64 t0 = (1ll << 47) - p0;
-  r.c0 = (int)(t0 & 0xFFFFFF);
   const i64 t1 = (t0 >> 24) - p1;
-  r.c1 = (int)(t1 & 0xFFFFFF);
-  const i64 c2 = (t1 >> 24) - p2;
-  r.c2 = c2 > (1 << 30) ? (1 << 30) : (c2 < -(1 << 30) ? -(1 << 30) : (int)c2);
-  const double xt = floor(ldexp(mean - 1.0, -s));
-  r.xt = xt > 127.0 ? 127 : (xt < -129.0 ? -129 : (int)xt);
+  ln_row_fill(r, mean, inv, (t1 >> 24) - p2, ((t1 & 0xFFFFFF) << 24) | (t0 & 0xFFFFFF), s);
   return r;
 }
 
@@ -660,18 +665,15 @@ struct LnEstHw {
   __device__ static double rcp_est(double x) { return __builtin_amdgcn_rcp(x); }
 };
 
-// v sign-extended from bit 23.  The limbs a0, a1, a2 already are signed
-// 24-bit values; restating it where they are used lets the compiler emit
-// v_mad_i32_i24 for the limb products even when the row constants arrive
-// through a cross-lane shuffle (it otherwise picks v_mad_u64_u32 and
-// v_mul_lo_u32, which issue at a quarter of the rate).
-__host__ __device__ __forceinline__ int i24(int v) { return (int)((unsigned)v << 8) >> 8; }
-
-// norm_q16 of one element (sat24 included).
+// norm_q16 of one element (sat24 included).  TIE: the row may tie (its
+// elements with x <= xt on an integer t step down by one); without TIE the
+// caller has found that no row it handles ties.
+template <bool TIE>
 __host__ __device__ __forceinline__ int ln_norm(int x, const LnRow &r) {
-  const int u0 = x * i24(r.a0) + r.c0 - (x <= r.xt ? 1 : 0);
-  const int u1 = x * i24(r.a1) + r.c1 + (u0 >> 24);
-  const int v = x * i24(r.a2) + r.c2 + (u1 >> 24);
+  const double t = fma((double)x, r.inv, r.add);
+  const double f = floor(t);
+  int v = (int)f;
+  if (TIE && r.tie && x <= r.xt && t == f) v -= 1;
   return v < -(1 << 23) ? -(1 << 23) : (v > (1 << 23) - 1 ? (1 << 23) - 1 : v);
 }
 
@@ -685,6 +687,42 @@ struct Ln32 {
   int8_t *out;
   int s, t, bs, os;  // x_scale + 32, 2*x_scale + 32, beta shift, output shift
 };
+
+// Lane src's row constants (the fields ln_norm<TIE> reads).
+template <bool TIE>
+__device__ __forceinline__ LnRow ln_row_shfl(const LnRow &m, int src) {
+  LnRow c;
+  c.inv = __shfl(m.inv, src);
+  c.add = __shfl(m.add, src);
+  if (TIE) {
+    c.xt = __shfl(m.xt, src);
+    c.tie = __shfl((int)m.tie, src) != 0;
+  }
+  return c;
+}
+
+// The NW words of one lane's elements of a row with constants r: gamma,
+// beta << bs and the output requant, packed four to a word.
+template <bool TIE, int NW>
+__device__ __forceinline__ void ln32_elems(const int (&w)[NW], const int (&gm)[NW],
+                                           const int (&bt)[NW], const Ln32 &ln, const LnRow &r,
+                                           int (&out)[NW]) {
+  const int rnd = 1 << (ln.os - 1);
+  int ov[4 * NW];
+#pragma unroll
+  for (int j = 0; j < 4 * NW; ++j) {
+    const int sh = 8 * (j & 3);
+    const int xv = (int)(int8_t)(w[j >> 2] >> sh);
+    const int g = (int)(int8_t)(gm[j >> 2] >> sh);
+    const int b = (int)(int8_t)(bt[j >> 2] >> sh);
+    const int a = ln_norm<TIE>(xv, r) * g + b * (1 << ln.bs);
+    const int o = (a + rnd + (a >> 31)) >> ln.os;
+    ov[j] = min(max(o, -128), 127);
+  }
+#pragma unroll
+  for (int q = 0; q < NW; ++q)
+    out[q] = (int)pack_lo4(ov[4 * q], ov[4 * q + 1], ov[4 * q + 2], ov[4 * q + 3]);
+}
 
 template <int LPR>
 __device__ __forceinline__ bool ln32_row(const int (&w)[48 / LPR], const int (&gm)[48 / LPR],
@@ -703,21 +741,10 @@ __device__ __forceinline__ bool ln32_row(const int (&w)[48 / LPR], const int (&g
     sxx += __shfl_xor(sxx, off);
   }
   const LnRow r = ln_row_consts_e<LnEstHw>(sx, sxx, ln.s, ln.t);
-  const int rnd = 1 << (ln.os - 1);
-  int ov[4 * NW];
-#pragma unroll
-  for (int j = 0; j < 4 * NW; ++j) {
-    const int sh = 8 * (j & 3);
-    const int xv = (int)(int8_t)(w[j >> 2] >> sh);
-    const int g = (int)(int8_t)(gm[j >> 2] >> sh);
-    const int b = (int)(int8_t)(bt[j >> 2] >> sh);
-    const int a = ln_norm(xv, r) * g + b * (1 << ln.bs);
-    const int o = (a + rnd + (a >> 31)) >> ln.os;
-    ov[j] = min(max(o, -128), 127);
-  }
-#pragma unroll
-  for (int q = 0; q < NW; ++q)
-    out[q] = (int)pack_lo4(ov[4 * q], ov[4 * q + 1], ov[4 * q + 2], ov[4 * q + 3]);
+  if (__any(r.tie))
+    ln32_elems<true, NW>(w, gm, bt, ln, r, out);
+  else
+    ln32_elems<false, NW>(w, gm, bt, ln, r, out);
   return r.neg_var;
 }
 

@@ -819,6 +819,38 @@ static_assert(kFfnRows * kLnPrologueRow <= 4 * kGeluLutMaxWords, "output rows fi
 // report a negative variance to lw (the int32 form cannot produce one:
 // with x_scale >= -16 the sum of squares is exact and the rounding of the
 // mean moves mean^2 by less than the smallest nonzero variance).
+// ln_rows' output half: rows grp and grp + 32 with the constants of lanes
+// base + 0 and base + 1 of the 8-lane group.
+template <bool TIE, int DS>
+__device__ __forceinline__ void ln_rows_out(const LnRow &mine, const int (&w)[2][6],
+                                            const int (&gw)[6], const int (&bw)[6], const Ln32 &ln,
+                                            int8_t *dst, int store_rows, int grp, int sub) {
+  const int rnd = 1 << (ln.os - 1);
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const LnRow c = ln_row_shfl<TIE>(mine, (threadIdx.x & 63 & ~7) + r);
+    int ov[24], out[6];
+#pragma unroll
+    for (int j = 0; j < 24; ++j) {
+      const int sh = 8 * (j & 3);
+      const int xv = __builtin_amdgcn_sbfe(w[r][j >> 2], sh, 8);
+      const int g = __builtin_amdgcn_sbfe(gw[j >> 2], sh, 8);
+      const int bb = __builtin_amdgcn_sbfe(bw[j >> 2], sh, 8) * (1 << ln.bs);
+      const int a = ln_norm<TIE>(xv, c) * g + bb;
+      const int o = (a + rnd + (a >> 31)) >> ln.os;
+      ov[j] = min(max(o, -128), 127);
+    }
+#pragma unroll
+    for (int q = 0; q < 6; ++q)
+      out[q] = (int)pack_lo4(ov[4 * q], ov[4 * q + 1], ov[4 * q + 2], ov[4 * q + 3]);
+    if (grp + 32 * r < store_rows) {
+      int2 *yr = reinterpret_cast<int2 *>(dst + (grp + 32 * r) * DS + sub * 24);
+#pragma unroll
+      for (int q = 0; q < 3; ++q) yr[q] = int2{out[2 * q], out[2 * q + 1]};
+    }
+  }
+}
+
 template <int SS, int DS>
 __device__ __forceinline__ void ln_rows(const int8_t *src, int clamp, int8_t *dst, int store_rows,
                                         const Ln32 &ln, const LnWarn &lw, int r0,
@@ -869,38 +901,10 @@ __device__ __forceinline__ void ln_rows(const int8_t *src, int clamp, int8_t *ds
   const LnRow mine = ln_row_consts_e<LnEstHw>(mr ? sx[1] : sx[0], mr ? sxx[1] : sxx[0], ln.s, ln.t);
   if (sub < 2 && mine.neg_var && lw.img_warn && grp + 32 * sub < report_rows)
     ln_warn_row(lw.offsets, lw.batch, lw.img_warn, r0 + grp + 32 * sub);
-  const int rnd = 1 << (ln.os - 1);
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    LnRow c;
-    const int src_lane = (threadIdx.x & 63 & ~7) + r;
-    c.a0 = __shfl(mine.a0, src_lane);
-    c.a1 = __shfl(mine.a1, src_lane);
-    c.a2 = __shfl(mine.a2, src_lane);
-    c.c0 = __shfl(mine.c0, src_lane);
-    c.c1 = __shfl(mine.c1, src_lane);
-    c.c2 = __shfl(mine.c2, src_lane);
-    c.xt = __shfl(mine.xt, src_lane);
-    int ov[24], out[6];
-#pragma unroll
-    for (int j = 0; j < 24; ++j) {
-      const int sh = 8 * (j & 3);
-      const int xv = __builtin_amdgcn_sbfe(w[r][j >> 2], sh, 8);
-      const int g = __builtin_amdgcn_sbfe(gw[j >> 2], sh, 8);
-      const int bb = __builtin_amdgcn_sbfe(bw[j >> 2], sh, 8) * (1 << ln.bs);
-      const int a = ln_norm(xv, c) * g + bb;
-      const int o = (a + rnd + (a >> 31)) >> ln.os;
-      ov[j] = min(max(o, -128), 127);
-    }
-#pragma unroll
-    for (int q = 0; q < 6; ++q)
-      out[q] = (int)pack_lo4(ov[4 * q], ov[4 * q + 1], ov[4 * q + 2], ov[4 * q + 3]);
-    if (grp + 32 * r < store_rows) {
-      int2 *yr = reinterpret_cast<int2 *>(dst + (grp + 32 * r) * DS + sub * 24);
-#pragma unroll
-      for (int q = 0; q < 3; ++q) yr[q] = int2{out[2 * q], out[2 * q + 1]};
-    }
-  }
+  if (__any(mine.tie))
+    ln_rows_out<true, DS>(mine, w, gw, bw, ln, dst, store_rows, grp, sub);
+  else
+    ln_rows_out<false, DS>(mine, w, gw, bw, ln, dst, store_rows, grp, sub);
 }
 
 // Epilogue of one attention-projection tile in the fused FFN: lane l's 16

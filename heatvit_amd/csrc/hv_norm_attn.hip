@@ -96,23 +96,44 @@ __global__ __launch_bounds__(256) void k_layernorm(const int8_t *__restrict__ x,
   }  // row loop
 }
 
+// One row's 24 outputs of this lane, packed four to a word.
+template <bool TIE>
+__device__ __forceinline__ void ln32_elems24(const int (&w)[6], const int (&g)[24],
+                                             const int (&bb)[24], const LnRow &c, int rnd, int os,
+                                             int (&out)[6]) {
+  int ov[24];
+#pragma unroll
+  for (int j = 0; j < 24; ++j) {
+    const int xv = __builtin_amdgcn_sbfe(w[j >> 2], 8 * (j & 3), 8);
+    const int a = ln_norm<TIE>(xv, c) * g[j] + bb[j];
+    const int o = (a + rnd + (a >> 31)) >> os;
+    ov[j] = min(max(o, -128), 127);
+  }
+#pragma unroll
+  for (int q = 0; q < 6; ++q)
+    out[q] = (int)pack_lo4(ov[4 * q], ov[4 * q + 1], ov[4 * q + 2], ov[4 * q + 3]);
+}
+
 // int32 LayerNorm for input scales in [-16, -4] with gamma at the common
 // exponent (g_exp - 16 <= b_exp), beta shift bs <= 22 and output shift os in
 // [1, 29] (LnRow in hv_device.h).  Eight lanes per row, 24 channels each,
 // and R rows per 8-lane group: the row sums are all-reduced over the group,
-// lane j works out the constants (mean, 2^48 / std, limb split) of row
-// j % R and the group reads each row's constants from its lane, so a row's
-// 64/128-bit set-up runs once per R rows of the group instead of once per
-// row.  Gamma and beta << bs stay in registers per lane; each element costs
-// three 24-bit multiply-adds for norm_q16, one for gamma/beta and the
-// requant.  R (4 or 1) follows the live row count, so small batches keep
-// enough groups in flight.
-template <int R>
-__device__ __forceinline__ void ln32_groups(const int8_t *__restrict__ x, const Ln32 &ln, int nrows,
+// lane j works out the constants (mean, 2^48 / std, the fma operands of
+// LnRow) of row j % R and the group reads each row's constants from its
+// lane, so a row's set-up runs once per R rows of the group instead of once
+// per row.  Gamma and beta << bs stay in registers per lane; each element
+// costs one double fma, floor and conversion for norm_q16, one 24-bit
+// multiply-add for gamma/beta and the requant.  R (4 or 1) follows the live
+// row count, so small batches keep enough groups in flight.  TIE: the
+// element form with the rounding-tie correction (LnRow); returns whether
+// this lane met a row that needs it.
+template <int R, bool TIE>
+__device__ __forceinline__ bool ln32_groups(const int8_t *__restrict__ x, const Ln32 &ln, int nrows,
                                             int grp, int ngroups, int sub, const int (&g)[24],
                                             const int (&bb)[24], uint8_t *neg_var, const LnWarn &lw) {
   const int lane = threadIdx.x & 63, base = lane & ~7;
   const int rnd = 1 << (ln.os - 1);
+  bool tie_seen = false;
   for (int row0 = grp * R; row0 < nrows; row0 += ngroups * R) {
     int w[R][6];
 #pragma unroll
@@ -161,32 +182,12 @@ __device__ __forceinline__ void ln32_groups(const int8_t *__restrict__ x, const 
       if (neg_var) neg_var[row0 + sub] = mine.neg_var ? 1 : 0;
       if (mine.neg_var && lw.img_warn) ln_warn_row(lw.offsets, lw.batch, lw.img_warn, row0 + sub);
     }
+    tie_seen |= mine.tie && row0 + sub % R < nrows;  // (rows past the end read as zeros)
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      LnRow c;
-      if (R == 1) {
-        c = mine;
-      } else {
-        const int src = base + r;
-        c.a0 = __shfl(mine.a0, src);
-        c.a1 = __shfl(mine.a1, src);
-        c.a2 = __shfl(mine.a2, src);
-        c.c0 = __shfl(mine.c0, src);
-        c.c1 = __shfl(mine.c1, src);
-        c.c2 = __shfl(mine.c2, src);
-        c.xt = __shfl(mine.xt, src);
-      }
-      int ov[24], out[6];
-#pragma unroll
-      for (int j = 0; j < 24; ++j) {
-        const int xv = __builtin_amdgcn_sbfe(w[r][j >> 2], 8 * (j & 3), 8);
-        const int a = ln_norm(xv, c) * g[j] + bb[j];
-        const int o = (a + rnd + (a >> 31)) >> ln.os;
-        ov[j] = min(max(o, -128), 127);
-      }
-#pragma unroll
-      for (int q = 0; q < 6; ++q)
-        out[q] = (int)pack_lo4(ov[4 * q], ov[4 * q + 1], ov[4 * q + 2], ov[4 * q + 3]);
+      int out[6];
+      ln32_elems24<TIE>(w[r], g, bb, R == 1 ? mine : ln_row_shfl<TIE>(mine, base + r), rnd,
+                        ln.os, out);
       if (row0 + r < nrows) {
         int2 *yr = reinterpret_cast<int2 *>(ln.out + (size_t)(row0 + r) * 192 + sub * 24);
 #pragma unroll
@@ -194,6 +195,7 @@ __device__ __forceinline__ void ln32_groups(const int8_t *__restrict__ x, const 
       }
     }
   }
+  return tie_seen;
 }
 
 __global__ __launch_bounds__(256) void k_layernorm32(const int8_t *__restrict__ x, Ln32 ln,
@@ -222,8 +224,15 @@ __global__ __launch_bounds__(256) void k_layernorm32(const int8_t *__restrict__ 
   // measured on MI355X: four rows per group at 50K rows (11.1 against
   // 12.2 us with one), one row per group below about 30K, where the
   // launch is latency-bound and more groups in flight win
-  if (nrows >= 32768) ln32_groups<4>(x, ln, nrows, grp, ngroups, sub, g, bb, neg_var, lw);
-  else ln32_groups<1>(x, ln, nrows, grp, ngroups, sub, g, bb, neg_var, lw);
+  // A wavefront that met a row with a rounding tie runs its rows again in
+  // the corrected element form (rare; same outputs for the other rows).
+  if (nrows >= 32768) {
+    if (__any(ln32_groups<4, false>(x, ln, nrows, grp, ngroups, sub, g, bb, neg_var, lw)))
+      ln32_groups<4, true>(x, ln, nrows, grp, ngroups, sub, g, bb, neg_var, lw);
+  } else {
+    if (__any(ln32_groups<1, false>(x, ln, nrows, grp, ngroups, sub, g, bb, neg_var, lw)))
+      ln32_groups<1, true>(x, ln, nrows, grp, ngroups, sub, g, bb, neg_var, lw);
+  }
 }
 
 // The int32 LayerNorm applies (and *ln is filled) when the input scale is in

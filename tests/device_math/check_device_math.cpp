@@ -11,9 +11,10 @@
 //            the exp alone against hvo_softmax_exp for every x_tilde in
 //            [-2^25, 0] plus a million larger magnitudes, and the exp with
 //            the row maximum folded into its constants against it;
-//   layernorm the int32 limb-split normalisation (ln_row_consts / ln_norm)
-//            against hvo_layernorm on random and degenerate rows over the
-//            exponent range the kernel takes it for.
+//   layernorm the int32 normalisation (ln_row_consts / ln_norm: one double
+//            fma per element) against hvo_layernorm on random and degenerate
+//            rows over the exponent range the kernel takes it for, and
+//            ln_norm against the 128-bit rsa on constructed tie rows.
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -155,8 +156,8 @@ struct LnEstOff {
 template <typename E>
 static long ln_consts_same(int sx, int sxx, int s) {
   const LnRow a = ln_row_consts(sx, sxx, s, 2 * s - 32), b = ln_row_consts_e<E>(sx, sxx, s, 2 * s - 32);
-  const bool same = a.a0 == b.a0 && a.a1 == b.a1 && a.a2 == b.a2 && a.c0 == b.c0 && a.c1 == b.c1 &&
-                    a.c2 == b.c2 && a.xt == b.xt && a.neg_var == b.neg_var;
+  const bool same = a.inv == b.inv && a.add == b.add && a.xt == b.xt && a.tie == b.tie &&
+                    a.neg_var == b.neg_var;
   return same ? 0 : 1;
 }
 
@@ -243,7 +244,7 @@ static long check_softmax(int rows) {
 static long check_layernorm(int rows) {
   std::mt19937_64 rng(7);
   int8_t x[192], g[192], b[192], ref[192];
-  long bad = 0;
+  long bad = 0, ties = 0;
   for (int it = 0; it < rows; ++it) {
     const int x_exp = -4 - (int)(rng() % 13);  // [-16, -4]
     const int g_exp = -4 - (int)(rng() % 9);
@@ -275,11 +276,86 @@ static long check_layernorm(int rows) {
     const LnRow r = ln_row_consts(sx, sxx, x_exp + 32, 2 * x_exp + 32);
     if ((int)r.neg_var != nv) ++bad;
     for (int c = 0; c < 192; ++c) {
-      const int a = ln_norm(x[c], r) * g[c] + b[c] * (1 << bs);
+      const int nq = ln_norm<true>(x[c], r);
+      if (!r.tie && ln_norm<false>(x[c], r) != nq) ++bad;
+      ties += r.tie;
+      const int a = nq * g[c] + b[c] * (1 << bs);
       int o = (a + (1 << (os - 1)) + (a >> 31)) >> os;
       o = o < -128 ? -128 : (o > 127 ? 127 : o);
       if (o != ref[c] && ++bad < 5) std::printf("layernorm mismatch row %d col %d\n", it, c);
     }
+  }
+  std::printf("layernorm rows %d, elements on tie rows %ld\n", rows, ties);
+  return bad;
+}
+
+// ln_norm against sat24(rsa((x 2^s - mean) inv, 48)) for every int8 x, on
+// (mean, inv) pairs over the whole range the constants allow (|mean| <=
+// 2^(s+7), 1 <= inv < 2^42).  Half of them are built so that an element
+// x0 below the mean lands exactly on a rounding tie: inv = 2^k io (io odd)
+// and mean = x0 2^s + 2^(47-k) make V(x0) = -io 2^47; on those rows the form
+// without the tie correction must be wrong at x0, or the check could not
+// see a missing correction.  The row's tie flag must be set exactly on the
+// rows where some element needs the correction.
+// fixed.rsa (round half away from zero, fixed.py) of a 128-bit value by
+// 48 bits, then the 24-bit saturation of nonlinear.layernorm's norm.
+static int norm_ref(i128 v) {
+  const i128 mag = ((v < 0 ? -v : v) + ((i128)1 << 47)) >> 48;
+  const i128 q = v < 0 ? -mag : mag;
+  return (int)(q > (1 << 23) - 1 ? (1 << 23) - 1 : (q < -(1 << 23) ? -(1 << 23) : q));
+}
+
+static LnRow ln_row_exact(i64 mean, u64 inv, int s) {
+  LnRow r;
+  const i128 C = ((i128)1 << 47) - (i128)mean * (i128)inv;
+  const i128 c2 = C >> 48;
+  ln_row_fill(r, (double)mean, (double)inv, (i64)c2, (i64)(C - (c2 << 48)), s);
+  r.neg_var = false;
+  return r;
+}
+
+static long check_ln_norm(int rows) {
+  std::mt19937_64 rng(29);
+  long bad = 0, built = 0, caught = 0;
+  for (int it = 0; it < rows; ++it) {
+    const int s = 16 + (int)(rng() % 13);
+    u64 inv = 1 + (rng() % ((1ull << (1 + rng() % 42)) - 1));
+    i64 mean = (i64)(rng() % (1ull << (s + 8))) - (1ll << (s + 7));
+    int x0 = 1000;
+    if (it & 1) {
+      // (it & 3) == 1: the edge where the tie element is the last one below
+      // the mean (k = 47 - s, x0 = xt in {-128, -127}, every other x ties)
+      const bool edge = (it & 3) == 1;
+      const int kmin = 39 - s > 22 ? 39 - s : 22;
+      const int k = edge ? 47 - s : kmin + (int)(rng() % (42 - kmin));
+      const u64 io = 1 | (rng() % (1ull << (42 - k < 19 ? 42 - k : 19)));
+      x0 = edge ? -128 + (int)(rng() & 1) : (int)(rng() % 200) - 100;
+      inv = io << k;
+      mean = (i64)x0 * (1ll << s) + (1ll << (47 - k));
+      if (inv >= (1ull << 42) || mean > (1ll << (s + 7))) continue;
+      ++built;
+    }
+    const LnRow r = ln_row_exact(mean, inv, s);
+    bool needs = false;  // some element needs the tie correction
+    for (int x = -128; x < 128; ++x) {
+      const i128 v = ((i128)x * ((i128)1 << s) - mean) * (i128)inv;
+      const int ref = norm_ref(v);
+      if (ln_norm<true>(x, r) != ref && ++bad < 5)
+        std::printf("ln_norm mismatch mean %lld inv %llu s %d x %d\n", (long long)mean,
+                    (unsigned long long)inv, s, x);
+      if (!r.tie && ln_norm<false>(x, r) != ref && ++bad < 5)
+        std::printf("ln_norm<false> mismatch on a row without ties\n");
+      if (x == x0 && r.tie && ln_norm<false>(x, r) != ref) ++caught;
+      needs |= ln_norm<false>(x, r) != ref;
+    }
+    // the tie flag is exact: set on the rows that need the correction only
+    if (r.tie != needs && ++bad < 5)
+      std::printf("ln tie flag %d for a row that %s the correction\n", (int)r.tie,
+                  needs ? "needs" : "does not need");
+  }
+  if (built < rows / 4 || caught != built) {
+    std::printf("ln_norm constructed ties %ld, caught %ld\n", built, caught);
+    ++bad;
   }
   return bad;
 }
@@ -289,7 +365,8 @@ int main(int argc, char **argv) {
   const long g = check_gelu(),
              s = check_softmax(rows) + check_recip24() + check_exp() + check_exp_nx() + check_exp_t() +
                  check_exp_qm(),
-             l = check_layernorm(rows) + check_round_div_d() + check_ln_consts(rows);
+             l = check_layernorm(rows) + check_round_div_d() + check_ln_consts(rows) +
+                 check_ln_norm(rows);
   std::printf("gelu_bad=%ld softmax_bad=%ld layernorm_bad=%ld\n", g, s, l);
   return (g || s || l) ? 1 : 0;
 }
