@@ -417,14 +417,20 @@ __host__ __device__ __forceinline__ unsigned softmax_exp_t(int t) {
 }
 
 // softmax_exp_t(q - mx) with the row maximum folded into the constants:
-// k1 = 16 * 2^32 + 94549 * mx and c1 = 88670 - 16 * 45426 - mx (mod 2^32),
-// so q * -94549 + k1 = (q - mx) * -94549 + 16 * 2^32 exactly and the
-// remainder term takes q - mx in its constant; q is already clamped to at
-// least mx - 17 * 45426.
-__host__ __device__ __forceinline__ unsigned softmax_exp_qm(int q, i64 k1, unsigned c1) {
+// k1 = 16 * 2^32 + 94549 * mx and c1s = (88670 - 16 * 45426 - mx) * 2^8
+// (mod 2^32), so q * -94549 + k1 = (q - mx) * -94549 + 16 * 2^32 exactly
+// and the remainder term takes q - mx in its constant; q is already clamped
+// to at least mx - 17 * 45426.  The remainder is carried as s8 = 2^8 s
+// (s <= 88671, so s8 < 2^25): square = floor((s^2 + 2^15) / 2^16) is then
+// the high word of s8^2 + 2^31, one 64-bit multiply-add without a shift.
+__host__ __device__ __forceinline__ unsigned softmax_exp_qm(int q, i64 k1, unsigned c1s) {
   const unsigned z16 = (unsigned)((u64)((i64)q * -94549ll + k1) >> 32);
-  const unsigned s = mul_u24(z16, 45426u) + c1 + (unsigned)q;
-  const unsigned square = (unsigned)(((u64)s * s + 32768u) >> 16);
+  unsigned t8 = ((unsigned)q << 8) + c1s;
+#ifdef __HIP_DEVICE_COMPILE__
+  asm("" : "+v"(t8));  // one shift-add, then one 24-bit multiply-add
+#endif
+  const unsigned s8 = mul_u24(z16, 45426u << 8) + t8;
+  const unsigned square = (unsigned)(((u64)s8 * s8 + (1ull << 31)) >> 32);
   const u64 x = (u64)square * 23495u + (32768u + (22544ull << 16));
   return (unsigned)(x >> z16);
 }

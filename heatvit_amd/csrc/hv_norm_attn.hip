@@ -579,16 +579,16 @@ __device__ __forceinline__ void attn_tiles(const AttnArgs &g, const int8_t *Ks, 
     // exp(max(q - mx, -17 * 45426)) with mx folded into the constants
     const int qlo = mx - 17 * 45426;
     i64 k1 = (16ll << 32) + 94549ll * mx;
-    unsigned c1 = (unsigned)(88670 - 16 * 45426) - (unsigned)mx;
+    unsigned c1s = ((unsigned)(88670 - 16 * 45426) - (unsigned)mx) << 8;
     // opaque to the compiler, which otherwise re-expands q * -94549 + k1
     // into a 64-bit (mx - q) product
-    asm volatile("" : "+v"(k1), "+v"(c1));
+    asm volatile("" : "+v"(k1), "+v"(c1s));
     unsigned sum = 0;
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const unsigned e = softmax_exp_qm(max(st[kt][i], qlo), k1, c1);
+        const unsigned e = softmax_exp_qm(max(st[kt][i], qlo), k1, c1s);
         st[kt][i] = (int)e;
         sum += e;
       }

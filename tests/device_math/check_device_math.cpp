@@ -126,10 +126,20 @@ static long check_exp_qm() {
     if (i % 7 == 0) q = mx - (int)(rng() % 64);
     const int qc = q > lo ? q : lo;
     const long long k1 = (16ll << 32) + 94549ll * mx;
-    const unsigned c1 = (unsigned)(88670 - 16 * 45426) - (unsigned)mx;
+    const unsigned c1s = ((unsigned)(88670 - 16 * 45426) - (unsigned)mx) << 8;
     const int t = q - mx > -17 * 45426 ? q - mx : -17 * 45426;
-    if (softmax_exp_qm(qc, k1, c1) != softmax_exp_t(t))
+    if (softmax_exp_qm(qc, k1, c1s) != softmax_exp_t(t))
       if (++bad < 5) std::printf("softmax_exp_qm mismatch q %d mx %d\n", q, mx);
+  }
+  // every argument, at the ends of the score range and at random maxima
+  for (int m = 0; m < 6; ++m) {
+    const int mx = m == 0 ? -(1 << 23) : m == 1 ? (1 << 23) - 1 : m == 2 ? 0
+                 : (int)(rng() % (1u << 24)) - (1 << 23);
+    const long long k1 = (16ll << 32) + 94549ll * mx;
+    const unsigned c1s = ((unsigned)(88670 - 16 * 45426) - (unsigned)mx) << 8;
+    for (int t = -17 * 45426; t <= 0; ++t)
+      if (softmax_exp_qm(mx + t, k1, c1s) != softmax_exp_t(t) && ++bad < 5)
+        std::printf("softmax_exp_qm mismatch t %d mx %d\n", t, mx);
   }
   return bad;
 }
