@@ -641,15 +641,19 @@ __device__ __forceinline__ void attn_tiles(const AttnArgs &g, const int8_t *Ks, 
       }
       if (q < N) {
         const v4i cs = *reinterpret_cast<const v4i *>(&vsum[dt * 16 + 4 * grp]);
-        int word = 0;
+        int o[4];
+        if (g.ctx_fast) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int v = acc[i] + cs[i];
-          const int o = g.ctx_fast ? min(max((v + g.ctx_rnd + (v >> 31)) >> g.ctx_shift, -128), 127)
-                                   : attn_ctx_general(v, g.ctx_shift);
-          word |= (o & 0xFF) << (8 * i);
+          for (int i = 0; i < 4; ++i) {
+            const int v = acc[i] + cs[i];
+            o[i] = min(max((v + g.ctx_rnd + (v >> 31)) >> g.ctx_shift, -128), 127);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[i] = attn_ctx_general(acc[i] + cs[i], g.ctx_shift);
         }
-        *reinterpret_cast<int *>(g.ctx + (size_t)(row0 + q) * 192 + h * 64 + dt * 16 + 4 * grp) = word;
+        *reinterpret_cast<int *>(g.ctx + (size_t)(row0 + q) * 192 + h * 64 + dt * 16 + 4 * grp) =
+            (int)pack_lo4(o[0], o[1], o[2], o[3]);
       }
     }
   }
