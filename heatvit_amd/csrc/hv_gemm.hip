@@ -821,14 +821,14 @@ static_assert(kFfnRows * kLnPrologueRow <= 4 * kGeluLutMaxWords, "output rows fi
 // mean moves mean^2 by less than the smallest nonzero variance).
 // ln_rows' output half: rows grp and grp + 32 with the constants of lanes
 // base + 0 and base + 1 of the 8-lane group.
-template <bool TIE, int DS>
+template <bool EXACT, int DS>
 __device__ __forceinline__ void ln_rows_out(const LnRow &mine, const int (&w)[2][6],
                                             const int (&gw)[6], const int (&bw)[6], const Ln32 &ln,
                                             int8_t *dst, int store_rows, int grp, int sub) {
   const int rnd = 1 << (ln.os - 1);
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
-    const LnRow c = ln_row_shfl<TIE>(mine, (threadIdx.x & 63 & ~7) + r);
+    const LnRow c = ln_row_shfl<EXACT>(mine, (threadIdx.x & 63 & ~7) + r);
     int ov[24], out[6];
 #pragma unroll
     for (int j = 0; j < 24; ++j) {
@@ -836,7 +836,7 @@ __device__ __forceinline__ void ln_rows_out(const LnRow &mine, const int (&w)[2]
       const int xv = __builtin_amdgcn_sbfe(w[r][j >> 2], sh, 8);
       const int g = __builtin_amdgcn_sbfe(gw[j >> 2], sh, 8);
       const int bb = __builtin_amdgcn_sbfe(bw[j >> 2], sh, 8) * (1 << ln.bs);
-      const int a = ln_norm<TIE>(xv, c) * g + bb;
+      const int a = __mul24(ln_norm<EXACT>(xv, c), g) + bb;  // both within 24 bits
       const int o = (a + rnd + (a >> 31)) >> ln.os;
       ov[j] = min(max(o, -128), 127);
     }

@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) void k_layernorm(const int8_t *__restrict__ x,
 }
 
 // One row's 24 outputs of this lane, packed four to a word.
-template <bool TIE>
+template <bool EXACT>
 __device__ __forceinline__ void ln32_elems24(const int (&w)[6], const int (&g)[24],
                                              const int (&bb)[24], const LnRow &c, int rnd, int os,
                                              int (&out)[6]) {
@@ -105,7 +105,7 @@ __device__ __forceinline__ void ln32_elems24(const int (&w)[6], const int (&g)[2
 #pragma unroll
   for (int j = 0; j < 24; ++j) {
     const int xv = __builtin_amdgcn_sbfe(w[j >> 2], 8 * (j & 3), 8);
-    const int a = ln_norm<TIE>(xv, c) * g[j] + bb[j];
+    const int a = __mul24(ln_norm<EXACT>(xv, c), g[j]) + bb[j];  // both within 24 bits
     const int o = (a + rnd + (a >> 31)) >> os;
     ov[j] = min(max(o, -128), 127);
   }
@@ -124,16 +124,16 @@ __device__ __forceinline__ void ln32_elems24(const int (&w)[6], const int (&g)[2
 // per row.  Gamma and beta << bs stay in registers per lane; each element
 // costs one double fma, floor and conversion for norm_q16, one 24-bit
 // multiply-add for gamma/beta and the requant.  R (4 or 1) follows the live
-// row count, so small batches keep enough groups in flight.  TIE: the
+// row count, so small batches keep enough groups in flight.  EXACT: the
 // element form with the rounding-tie correction (LnRow); returns whether
 // this lane met a row that needs it.
-template <int R, bool TIE>
+template <int R, bool EXACT>
 __device__ __forceinline__ bool ln32_groups(const int8_t *__restrict__ x, const Ln32 &ln, int nrows,
                                             int grp, int ngroups, int sub, const int (&g)[24],
                                             const int (&bb)[24], uint8_t *neg_var, const LnWarn &lw) {
   const int lane = threadIdx.x & 63, base = lane & ~7;
   const int rnd = 1 << (ln.os - 1);
-  bool tie_seen = false;
+  bool exact_seen = false;
   for (int row0 = grp * R; row0 < nrows; row0 += ngroups * R) {
     int w[R][6];
 #pragma unroll
@@ -182,12 +182,12 @@ __device__ __forceinline__ bool ln32_groups(const int8_t *__restrict__ x, const 
       if (neg_var) neg_var[row0 + sub] = mine.neg_var ? 1 : 0;
       if (mine.neg_var && lw.img_warn) ln_warn_row(lw.offsets, lw.batch, lw.img_warn, row0 + sub);
     }
-    tie_seen |= mine.tie && row0 + sub % R < nrows;  // (rows past the end read as zeros)
+    exact_seen |= mine.tie && row0 + sub % R < nrows;  // (rows past the end read as zeros)
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       int out[6];
-      ln32_elems24<TIE>(w[r], g, bb, R == 1 ? mine : ln_row_shfl<TIE>(mine, base + r), rnd,
-                        ln.os, out);
+      ln32_elems24<EXACT>(w[r], g, bb, R == 1 ? mine : ln_row_shfl<EXACT>(mine, base + r), rnd,
+                          ln.os, out);
       if (row0 + r < nrows) {
         int2 *yr = reinterpret_cast<int2 *>(ln.out + (size_t)(row0 + r) * 192 + sub * 24);
 #pragma unroll
@@ -195,7 +195,7 @@ __device__ __forceinline__ bool ln32_groups(const int8_t *__restrict__ x, const 
       }
     }
   }
-  return tie_seen;
+  return exact_seen;
 }
 
 __global__ __launch_bounds__(256) void k_layernorm32(const int8_t *__restrict__ x, Ln32 ln,
