@@ -401,9 +401,8 @@ __global__ __launch_bounds__(kImgThreads) void k_selector_image(
   {
     const int sh_in = -16 - (p.in_exp + p.local_w_exp), sh_out = p.local_out_exp + 16;
     const Rq ra = rq_setup(sh_in, -(1 << 23), (1 << 23) - 1), rb = rq_setup(sh_out, -128, 127);
-    // a second barrier here measured faster than none (three runs, about 1
-    // us per launch): it holds the waves that finished their row stores
-    // until the last table and weight stores have drained
+    // a second barrier here measured faster than none (three runs, about
+    // 1 us per launch)
     __syncthreads();
     const int nt2 = ntiles * 2, nu = 3 * nt2;
     for (int u0 = wave; u0 < nu; u0 += 2 * NW) {
