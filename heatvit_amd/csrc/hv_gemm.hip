@@ -177,7 +177,9 @@ __device__ __forceinline__ void epi_operands(const GemmArgs &g, const int (&arow
 // channels c0 .. c0+15 of each column tile.
 // lds_out (optional, EPI_RES with 16-byte stores): the output bytes also go
 // to lds_out + (32 * mt + l32) * lds_stride + c0.
-template <int MT, int NT, int EPI, bool FAST, int DIRS>
+// BACC: the accumulators started at the bias (the MFMA's C operand), so the
+// int32 form adds nothing and the exact form takes the bias back out.
+template <int MT, int NT, int EPI, bool FAST, int DIRS, bool BACC = false>
 __device__ __forceinline__ void epi_tile(const GemmArgs &g, const v16i (&acc)[MT][NT],
                                          const v4i (&bias4)[NT][4], const v4i (&res4)[MT][NT],
                                          int r0, int ct0, int M, int h, int l32, const Rq &rq_a,
@@ -217,7 +219,7 @@ __device__ __forceinline__ void epi_tile(const GemmArgs &g, const v16i (&acc)[MT
       if (fast) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-          const int v = acc[mt][nt][j] + bias4[nt][j >> 2][j & 3];
+          const int v = BACC ? acc[mt][nt][j] : acc[mt][nt][j] + bias4[nt][j >> 2][j & 3];
           constexpr bool LA = DIRS & 1, LB = (DIRS >> 1) & 1;
           if (EPI == EPI_I8) {
             o[j] = rq_dir_nowrap<LA>(v, rq_a);
@@ -243,8 +245,9 @@ __device__ __forceinline__ void epi_tile(const GemmArgs &g, const v16i (&acc)[MT
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
           const int r8 = RESLIKE ? (int)(int8_t)(res4[mt][nt][j >> 2] >> (8 * (j & 3))) : 0;
-          const v2i r = epi_exact(EPI, acc[mt][nt][j], bias4[nt][j >> 2][j & 3], r8, g.shift_a,
-                                  g.shift_b, g.da, g.db, g.os);
+          const int b = bias4[nt][j >> 2][j & 3];
+          const v2i r = epi_exact(EPI, BACC ? acc[mt][nt][j] - b : acc[mt][nt][j], b, r8,
+                                  g.shift_a, g.shift_b, g.da, g.db, g.os);
           o[j] = r[0];
           mid[j] = r[1];
         }
@@ -909,17 +912,18 @@ __device__ __forceinline__ void ln_rows(const int8_t *src, int clamp, int8_t *ds
 
 // Epilogue of one attention-projection tile in the fused FFN: lane l's 16
 // bytes of y = align_add(x, requant(ctx Wp + bp)) (transformer.py:267-272,
-// 413-421), in the int32 form when every lane's biases allow it, else exact.
+// 413-421), in the int32 form when every lane's biases allow it, else exact;
+// acc started at the bias bs (the MFMA's C operand).
 template <bool LA, bool LB>
-__device__ __forceinline__ v4i proj_epi(const GemmArgs &gp, const v16i &acc, const v4i (&b4)[4],
+__device__ __forceinline__ v4i proj_epi(const GemmArgs &gp, const v16i &acc, const v16i &bs,
                                         v4i x4, const Rq &rpa, const Rq &rpb, bool all_narrow) {
   bool fast = all_narrow;
   if (!all_narrow) {
-    int bmax = b4[0][0], bmin = bmax;
+    int bmax = bs[0], bmin = bmax;
 #pragma unroll
     for (int j = 1; j < 16; ++j) {
-      bmax = max(bmax, b4[j >> 2][j & 3]);
-      bmin = min(bmin, b4[j >> 2][j & 3]);
+      bmax = max(bmax, bs[j]);
+      bmin = min(bmin, bs[j]);
     }
     fast = __all(bmax <= gp.acc_lim && bmin >= -gp.acc_lim);
   }
@@ -927,7 +931,7 @@ __device__ __forceinline__ v4i proj_epi(const GemmArgs &gp, const v16i &acc, con
   if (fast) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const int t8 = rq_dir_nowrap<LA>(acc[j] + b4[j >> 2][j & 3], rpa);
+      const int t8 = rq_dir_nowrap<LA>(acc[j], rpa);
       const int r8 = (int)(int8_t)(x4[j >> 2] >> (8 * (j & 3)));
       o[j] = rq_dir<LB>(r8 * (1 << gp.da) + t8 * (1 << gp.db), rpb);
     }
@@ -935,7 +939,7 @@ __device__ __forceinline__ v4i proj_epi(const GemmArgs &gp, const v16i &acc, con
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int r8 = (int)(int8_t)(x4[j >> 2] >> (8 * (j & 3)));
-      o[j] = epi_exact(EPI_RES, acc[j], b4[j >> 2][j & 3], r8, gp.shift_a, gp.shift_b, gp.da,
+      o[j] = epi_exact(EPI_RES, acc[j] - bs[j], bs[j], r8, gp.shift_a, gp.shift_b, gp.da,
                        gp.db, gp.os)[0];
     }
   }
@@ -1011,27 +1015,25 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
         const int t = wave + 4 * ti, rt = t / 6, ct = t - rt * 6;
         const int8_t *ap = gp.a + (size_t)min(r0 + 32 * rt + l32, M - 1) * 192 + 16 * h;
         const int8_t *bp = gp.b + (size_t)ct * 6 * 1024 + lane * 16;
-        v4i pa[6], pw[6], b4[4];
+        v4i pa[6], pw[6];
 #pragma unroll
         for (int kt = 0; kt < 6; ++kt) {
           pa[kt] = *reinterpret_cast<const v4i *>(ap + kt * 32);
           pw[kt] = *reinterpret_cast<const v4i *>(bp + kt * 1024);
         }
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          b4[q] = *reinterpret_cast<const v4i *>(gp.bias + ct * 32 + 16 * h + 4 * q);
+        const v16i pbs = *reinterpret_cast<const v16i *>(gp.bias + ct * 32 + 16 * h);
         const v4i x4 = *reinterpret_cast<const v4i *>(
             gp.res + (size_t)min(r0 + 32 * rt + l32, M - 1) * 192 + ct * 32 + 16 * h);
-        v16i acc = v16i{0};
+        v16i acc = pbs;  // the accumulator starts at the bias
 #pragma unroll
         for (int kt = 0; kt < 6; ++kt)
           acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(pw[kt], pa[kt], acc, 0, 0, 0);
         v4i yv;
         switch (dirsp) {
-          case 0: yv = proj_epi<false, false>(gp, acc, b4, x4, rpa, rpb, allp); break;
-          case 1: yv = proj_epi<true, false>(gp, acc, b4, x4, rpa, rpb, allp); break;
-          case 2: yv = proj_epi<false, true>(gp, acc, b4, x4, rpa, rpb, allp); break;
-          default: yv = proj_epi<true, true>(gp, acc, b4, x4, rpa, rpb, allp); break;
+          case 0: yv = proj_epi<false, false>(gp, acc, pbs, x4, rpa, rpb, allp); break;
+          case 1: yv = proj_epi<true, false>(gp, acc, pbs, x4, rpa, rpb, allp); break;
+          case 2: yv = proj_epi<false, true>(gp, acc, pbs, x4, rpa, rpb, allp); break;
+          default: yv = proj_epi<true, true>(gp, acc, pbs, x4, rpa, rpb, allp); break;
         }
         yres[ti] = yv;
         *reinterpret_cast<v4i *>(&hid[(32 * rt + l32) * kLnPrologueRow + ct * 32 + 16 * h]) = yv;
@@ -1136,6 +1138,7 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
       ct = t - rt * 6;
     };
     v4i wb[3][4], bias4[1][4], res4[1][1];
+    v16i bsb;  // the tile's biases, the accumulator's start
     int rt, ct;
     tile_of(0, rt, ct);
     // the tile's biases and residual bytes (PJ: the residual from yres)
@@ -1147,6 +1150,9 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
       } else {
         epi_operands<1, 1, EPI_RES>(g2, arow, ct, h, bias4, res4);
       }
+      bsb = *reinterpret_cast<const v16i *>(g2.bias + ct * 32 + 16 * h);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) bias4[0][j >> 2][j & 3] = bsb[j];
     };
     operands();
 #pragma unroll
@@ -1165,7 +1171,7 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
       const int8_t *bp = g2.b + (size_t)ct * 24 * 1024 + lane * 16;
       int nrt = rt, nct = ct;
       if (ti + 1 < 3) tile_of(ti + 1, nrt, nct);
-      v16i acc[1][1] = {{v16i{0}}};
+      v16i acc[1][1] = {{bsb}};
 #pragma unroll
       for (int c = 0; c < 6; ++c) {
         const int cur = c % 3, nxt = (c + 2) % 3;
@@ -1186,7 +1192,7 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
               0);
         __builtin_amdgcn_sched_barrier(0);  // one chunk of LDS reads in flight at a time
       }
-      epi_tile<1, 1, EPI_RES, true, DIRS2>(
+      epi_tile<1, 1, EPI_RES, true, DIRS2, true>(
           g2, acc, bias4, res4, r0 + 32 * rt, ct, M, h, l32, r2a, r2b, nullptr,
           LNE ? reinterpret_cast<int8_t *>(lut) + 32 * rt * kLnPrologueRow : nullptr,
           kLnPrologueRow);
@@ -1272,15 +1278,14 @@ __global__ __launch_bounds__(512, 4) void k_ffn32(GemmArgs g1, GemmArgs g2, LnPr
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     tv[i] = reinterpret_cast<const v4i *>(kGeluLut + g1.lut_off)[min(tid + 512 * i, n4 - 1)];
-  v4i pw[6], pb4[4];
+  v4i pw[6];
+  v16i pbs;
   if constexpr (PJ) {
     if (wave < 6) {
       const int8_t *bp = gp.b + (size_t)wave * 6 * 1024 + lane * 16;
 #pragma unroll
       for (int kt = 0; kt < 6; ++kt) pw[kt] = *reinterpret_cast<const v4i *>(bp + kt * 1024);
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        pb4[q] = *reinterpret_cast<const v4i *>(gp.bias + wave * 32 + 16 * h + 4 * q);
+      pbs = *reinterpret_cast<const v16i *>(gp.bias + wave * 32 + 16 * h);
     }
   }
   const int M = g1.m_dev ? min(*g1.m_dev, g1.m) : g1.m;
@@ -1312,15 +1317,15 @@ __global__ __launch_bounds__(512, 4) void k_ffn32(GemmArgs g1, GemmArgs g2, LnPr
       for (int kt = 0; kt < 6; ++kt) pa[kt] = *reinterpret_cast<const v4i *>(ap + kt * 32);
       const v4i x4 =
           *reinterpret_cast<const v4i *>(gp.res + (size_t)arow * 192 + ct * 32 + 16 * h);
-      v16i acc = v16i{0};
+      v16i acc = pbs;  // the accumulator starts at the bias
 #pragma unroll
       for (int kt = 0; kt < 6; ++kt)
         acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(pw[kt], pa[kt], acc, 0, 0, 0);
       switch (dirsp) {
-        case 0: yres = proj_epi<false, false>(gp, acc, pb4, x4, rpa, rpb, allp); break;
-        case 1: yres = proj_epi<true, false>(gp, acc, pb4, x4, rpa, rpb, allp); break;
-        case 2: yres = proj_epi<false, true>(gp, acc, pb4, x4, rpa, rpb, allp); break;
-        default: yres = proj_epi<true, true>(gp, acc, pb4, x4, rpa, rpb, allp); break;
+        case 0: yres = proj_epi<false, false>(gp, acc, pbs, x4, rpa, rpb, allp); break;
+        case 1: yres = proj_epi<true, false>(gp, acc, pbs, x4, rpa, rpb, allp); break;
+        case 2: yres = proj_epi<false, true>(gp, acc, pbs, x4, rpa, rpb, allp); break;
+        default: yres = proj_epi<true, true>(gp, acc, pbs, x4, rpa, rpb, allp); break;
       }
       *reinterpret_cast<v4i *>(&hid[l32 * kLnPrologueRow + ct * 32 + 16 * h]) = yres;
     }
@@ -1413,6 +1418,7 @@ __global__ __launch_bounds__(512, 4) void k_ffn32(GemmArgs g1, GemmArgs g2, LnPr
   // its operands and first two weight chunks load before the barrier.
   const int ct = wave;
   v4i wb[3][4], bias4[1][4], res4[1][1];
+  v16i bsb;  // the tile's biases, the accumulator's start
   if (wave < 6) {
     const int arows[1] = {arow};
     if constexpr (PJ) {
@@ -1421,6 +1427,9 @@ __global__ __launch_bounds__(512, 4) void k_ffn32(GemmArgs g1, GemmArgs g2, LnPr
     } else {
       epi_operands<1, 1, EPI_RES>(g2, arows, ct, h, bias4, res4);
     }
+    bsb = *reinterpret_cast<const v16i *>(g2.bias + ct * 32 + 16 * h);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) bias4[0][j >> 2][j & 3] = bsb[j];
 #pragma unroll
     for (int j = 0; j < 8; ++j)
       wb[j >> 2][j & 3] =
@@ -1430,7 +1439,7 @@ __global__ __launch_bounds__(512, 4) void k_ffn32(GemmArgs g1, GemmArgs g2, LnPr
   if (wave < 6) {
     const int8_t *hp = &hid[l32 * kFfnHRow + 16 * h];
     const int8_t *bp = g2.b + (size_t)ct * 24 * 1024 + lane * 16;
-    v16i acc[1][1] = {{v16i{0}}};
+    v16i acc[1][1] = {{bsb}};
 #pragma unroll
     for (int c = 0; c < 6; ++c) {
       const int cur = c % 3, nxt = (c + 2) % 3;
@@ -1446,7 +1455,7 @@ __global__ __launch_bounds__(512, 4) void k_ffn32(GemmArgs g1, GemmArgs g2, LnPr
             0);
       __builtin_amdgcn_sched_barrier(0);  // one chunk of LDS reads in flight at a time
     }
-    epi_tile<1, 1, EPI_RES, true, DIRS2>(g2, acc, bias4, res4, r0, ct, M, h, l32, r2a, r2b,
+    epi_tile<1, 1, EPI_RES, true, DIRS2, true>(g2, acc, bias4, res4, r0, ct, M, h, l32, r2a, r2b,
                                          nullptr,
                                          LNE ? reinterpret_cast<int8_t *>(lut) : nullptr,
                                          kLnPrologueRow);
