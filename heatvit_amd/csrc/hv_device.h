@@ -536,9 +536,15 @@ __host__ __device__ __forceinline__ u64 isqrt_u64(u64 x) {
 // inv / 2^48 <= 1/sd + 2^-49, and |norm| <= 2^16 * 13.83 * 65.47 / 64.47 +
 // 1 < 2^20.  So the element form needs no clamp; the exact form keeps it
 // (and the CPU test checks the bound on random and extreme rows).
+// The element form without the tie step rounds instead of flooring: with
+// u = 2^(s-48), t' = t + u/2 - 1/2 = ((2 N + 1) - 2^(48-s)) u/2 (N = x*inv -
+// K_0, |N| < 2^51) is an exact double, never a whole or half integer, so
+// round-to-nearest(t') = floor(t), and adding 1.5 * 2^52 (|t'| < 2^31) leaves
+// that integer in the low word of the sum: one fma and one add per element.
 struct LnRow {
-  double inv;  // inv * 2^(s-48)
-  double add;  // -K_0 * 2^(s-48)
+  double inv;   // inv * 2^(s-48)
+  double add;   // -K_0 * 2^(s-48)
+  double addm;  // add + u/2 - 1/2
   int xt;
   bool tie;  // some x <= xt needs the tie correction
   bool neg_var;
@@ -556,6 +562,7 @@ __host__ __device__ __forceinline__ void ln_row_fill(LnRow &r, double mean, doub
   const i64 f = c2 * (1ll << (48 - s)) + (low >> s);
   r.inv = ldexp(inv, s - 48);
   r.add = ldexp((double)f, s - 48);
+  r.addm = ldexp((double)(2 * f + 1 - (1ll << (48 - s))), s - 49);
   const double xt = floor(ldexp(mean - 1.0, -s));
   r.xt = xt > 127.0 ? 127 : (xt < -129.0 ? -129 : (int)xt);
   r.tie = false;
@@ -684,10 +691,13 @@ struct LnEstHw {
 // caller has found that no row it handles ties.
 template <bool EXACT>
 __host__ __device__ __forceinline__ int ln_norm(int x, const LnRow &r) {
+  if (!EXACT) {  // within 24 bits (the bound above)
+    const double y = fma((double)x, r.inv, r.addm) + 0x1.8p52;
+    return (int)(unsigned)__builtin_bit_cast(unsigned long long, y);
+  }
   const double t = fma((double)x, r.inv, r.add);
   const double f = floor(t);
   int v = (int)f;
-  if (!EXACT) return v;  // within 24 bits (the bound above)
   if (r.tie && x <= r.xt && t == f) v -= 1;
   return v < -(1 << 23) ? -(1 << 23) : (v > (1 << 23) - 1 ? (1 << 23) - 1 : v);
 }
@@ -708,10 +718,12 @@ template <bool EXACT>
 __device__ __forceinline__ LnRow ln_row_shfl(const LnRow &m, int src) {
   LnRow c;
   c.inv = __shfl(m.inv, src);
-  c.add = __shfl(m.add, src);
   if (EXACT) {
+    c.add = __shfl(m.add, src);
     c.xt = __shfl(m.xt, src);
     c.tie = __shfl((int)m.tie, src) != 0;
+  } else {
+    c.addm = __shfl(m.addm, src);
   }
   return c;
 }

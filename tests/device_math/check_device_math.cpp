@@ -166,8 +166,8 @@ struct LnEstOff {
 template <typename E>
 static long ln_consts_same(int sx, int sxx, int s) {
   const LnRow a = ln_row_consts(sx, sxx, s, 2 * s - 32), b = ln_row_consts_e<E>(sx, sxx, s, 2 * s - 32);
-  const bool same = a.inv == b.inv && a.add == b.add && a.xt == b.xt && a.tie == b.tie &&
-                    a.neg_var == b.neg_var;
+  const bool same = a.inv == b.inv && a.add == b.add && a.addm == b.addm && a.xt == b.xt &&
+                    a.tie == b.tie && a.neg_var == b.neg_var;
   return same ? 0 : 1;
 }
 
