@@ -609,7 +609,7 @@ __host__ __device__ __forceinline__ LnRow ln_row_consts(int sx, int sxx, int s, 
   const u64 inv = recip48(sd);  // < 2^42
   const i128 C = ((i128)1 << 47) - (i128)mean * (i128)inv;
   const i128 c2 = C >> 48;
-  ln_row_fill(r, (double)mean, (double)inv, (i64)c2, (i64)(C - (c2 << 48)), s);
+  ln_row_fill(r, (double)mean, (double)inv, (i64)c2, (i64)(C - c2 * ((i128)1 << 48)), s);
   return r;
 }
 

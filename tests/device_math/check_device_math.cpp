@@ -324,7 +324,7 @@ static LnRow ln_row_exact(i64 mean, u64 inv, int s) {
   LnRow r;
   const i128 C = ((i128)1 << 47) - (i128)mean * (i128)inv;
   const i128 c2 = C >> 48;
-  ln_row_fill(r, (double)mean, (double)inv, (i64)c2, (i64)(C - (c2 << 48)), s);
+  ln_row_fill(r, (double)mean, (double)inv, (i64)c2, (i64)(C - c2 * ((i128)1 << 48)), s);
   r.neg_var = false;
   return r;
 }
