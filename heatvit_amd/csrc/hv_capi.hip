@@ -240,12 +240,12 @@ static constexpr int kFusedQkvMinBatch = 32;
 // LN1, QKV, attention, proj + residual, LN2, FFN1 + GELU, FFN2 + residual.
 // warnings (optional, [B]) receive the LayerNorms' negative-variance bit.
 // bias_max (optional, device): the largest |bias| of bqkv, bproj, b1 and b2.
-// rows32: the fused FFN in blocks of 32 rows (launch_ffn).
+// ffn_rows: the fused FFN's row blocking (FfnRows, launch_ffn).
 static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *offsets,
                          int batch, int max_rows, int8_t *z, const hv_block_ckpt *ck,
                          int32_t *warnings, const BlockWs &w, hipStream_t s,
                          const LnChain &chain = LnChain{}, const unsigned *bias_max = nullptr,
-                         bool rows32 = false) {
+                         int ffn_rows = FFN_ROWS64) {
   const int32_t *rows_dev = offsets + batch;
   const LnWarn lw{offsets, batch, warnings};
   int8_t *qkv = ck && ck->fused_qkv ? ck->fused_qkv : w.qkv;
@@ -343,7 +343,7 @@ static int block_forward(const hv_block_dev &p, const int8_t *x, const int32_t *
   if (ln2_in && !ck) {
     const LnPrologue fl{nullptr, ln, lw};
     ProfScope ps(HV_PROF_FFN, s);
-    rc = launch_ffn(g1, g2, s, &fl, chained ? &fe : nullptr, &g, rows32);
+    rc = launch_ffn(g1, g2, s, &fl, chained ? &fe : nullptr, &g, ffn_rows);
     if (rc != 1) {
       if (rc == HV_OK && chained && chain.next_done) *chain.next_done = true;
       return rc;
@@ -507,7 +507,8 @@ int hv_block_forward(const hv_block_dev *p, const int8_t *x, const int32_t *offs
   if ((rc = launch_image_check(offsets, batch, max_rows, status, warnings, (hipStream_t)stream)))
     return rc;
   return block_forward(*p, x, offsets, batch, max_rows, z, ck, warnings, w, (hipStream_t)stream,
-                       LnChain{}, nullptr, small_rows(max_rows));
+                       LnChain{}, nullptr,
+                       small_rows(max_rows) ? FFN_ROWS32 : FFN_ROWS64_BALANCED);
 }
 
 struct SelectorWs {
@@ -758,11 +759,14 @@ static int model_forward(const hv_model_dev *p, const void *images, bool float_i
     const LnChain chain{ln1_ready, chain_next ? (blk < 12 ? &p->blocks[blk] : &fin) : nullptr,
                         w.blk.ln, &next_done};
     // One forward at a time, 32-row FFN blocks once a selector has cut the
-    // rows (or for small batches); pipelined callers keep 64.
-    const bool rows32 =
-        !(options & HV_FWD_PIPELINED) && (sel > 0 || small_rows((long long)max_rows));
+    // rows (or for small batches), else 64-row blocks with the launch's last
+    // ones split where that evens out the CUs' work; pipelined callers,
+    // whose other batches fill the CUs a launch leaves idle, keep 64.
+    const int ffn_rows = (options & HV_FWD_PIPELINED)               ? FFN_ROWS64
+                         : (sel > 0 || small_rows((long long)max_rows)) ? FFN_ROWS32
+                                                                        : FFN_ROWS64_BALANCED;
     if ((rc = block_forward(p->blocks[blk - 1], w.xa, w.off_a, batch, max_rows, w.xb, nullptr,
-                            warnings, w.blk, s, chain, w.bias_max + 4 * (blk - 1), rows32)))
+                            warnings, w.blk, s, chain, w.bias_max + 4 * (blk - 1), ffn_rows)))
       return rc;
     ln1_ready = next_done ? w.blk.ln : nullptr;
     if (blk == 12) final_done = next_done;

@@ -822,15 +822,19 @@ static_assert(kFfnRows * kLnPrologueRow <= 4 * kGeluLutMaxWords, "output rows fi
 // report a negative variance to lw (the int32 form cannot produce one:
 // with x_scale >= -16 the sum of squares is exact and the rounding of the
 // mean moves mean^2 by less than the smallest nonzero variance).
+// When `two` is false the block holds 32 rows (rows 32..63 are neither
+// normalised nor stored, and their constants raise no exact pass).
 // ln_rows' output half: rows grp and grp + 32 with the constants of lanes
 // base + 0 and base + 1 of the 8-lane group.
 template <bool EXACT, int DS>
 __device__ __forceinline__ void ln_rows_out(const LnRow &mine, const int (&w)[2][6],
                                             const int (&gw)[6], const int (&bw)[6], const Ln32 &ln,
-                                            int8_t *dst, int store_rows, int grp, int sub) {
+                                            int8_t *dst, int store_rows, int grp, int sub,
+                                            bool two) {
   const int rnd = 1 << (ln.os - 1);
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
+    if (r == 1 && !two) break;  // uniform
     const LnRow c = ln_row_shfl<EXACT>(mine, (threadIdx.x & 63 & ~7) + r);
     int ov[24], out[6];
 #pragma unroll
@@ -857,7 +861,7 @@ __device__ __forceinline__ void ln_rows_out(const LnRow &mine, const int (&w)[2]
 template <int SS, int DS>
 __device__ __forceinline__ void ln_rows(const int8_t *src, int clamp, int8_t *dst, int store_rows,
                                         const Ln32 &ln, const LnWarn &lw, int r0,
-                                        int report_rows) {
+                                        int report_rows, bool two = true) {
   const int tid = threadIdx.x, sub = tid & 7, grp = tid >> 3;
   int w[2][6];
 #pragma unroll
@@ -901,13 +905,14 @@ __device__ __forceinline__ void ln_rows(const int8_t *src, int clamp, int8_t *ds
       sxx[r] += __shfl_xor(sxx[r], off);
     }
   const int mr = sub & 1;
-  const LnRow mine = ln_row_consts_e<LnEstHw>(mr ? sx[1] : sx[0], mr ? sxx[1] : sxx[0], ln.s, ln.t);
+  LnRow mine = ln_row_consts_e<LnEstHw>(mr ? sx[1] : sx[0], mr ? sxx[1] : sxx[0], ln.s, ln.t);
+  if (!two && mr) mine.tie = false;
   if (sub < 2 && mine.neg_var && lw.img_warn && grp + 32 * sub < report_rows)
     ln_warn_row(lw.offsets, lw.batch, lw.img_warn, r0 + grp + 32 * sub);
   if (__any(mine.tie))
-    ln_rows_out<true, DS>(mine, w, gw, bw, ln, dst, store_rows, grp, sub);
+    ln_rows_out<true, DS>(mine, w, gw, bw, ln, dst, store_rows, grp, sub, two);
   else
-    ln_rows_out<false, DS>(mine, w, gw, bw, ln, dst, store_rows, grp, sub);
+    ln_rows_out<false, DS>(mine, w, gw, bw, ln, dst, store_rows, grp, sub, two);
 }
 
 // Epilogue of one attention-projection tile in the fused FFN: lane l's 16
@@ -955,9 +960,13 @@ __device__ __forceinline__ v4i proj_epi(const GemmArgs &gp, const v16i &acc, con
 // produce y, which never leaves the CU: each wavefront computes the y tiles
 // of its phase-B tiles and keeps their bytes as phase B's residual, and the
 // y rows pass through LDS to LayerNorm 2.
+// Workgroups 0 .. nfull - 1 take 64-row blocks; the ones after them blocks
+// of 32 rows (one row tile: the steps of the second are skipped), so that a
+// launch whose last 64-row blocks would double up on a few CUs spreads that
+// work over twice as many.
 template <int DIRS1, int DIRS2, bool LN, bool LNE, bool PJ>
 __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologue fl,
-                                             LnPrologue fe, GemmArgs gp, int dirsp) {
+                                             LnPrologue fe, GemmArgs gp, int dirsp, int nfull) {
   static_assert(!PJ || LN, "the projection feeds the LayerNorm in front");
   __shared__ __attribute__((aligned(16))) int8_t hid[kFfnRows * kFfnHRow];
   // static, so its LDS address is a constant the table reads can fold
@@ -976,8 +985,12 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
   for (int i = 0; i < 8; ++i)
     tv[i] = reinterpret_cast<const v4i *>(kGeluLut + g1.lut_off)[min(tid + 256 * i, n4 - 1)];
   const int M = g1.m_dev ? min(*g1.m_dev, g1.m) : g1.m;
-  const int nrb = (M + kFfnRows - 1) / kFfnRows;
-  if ((int)blockIdx.x >= nrb) return;  // uniform: before any barrier
+  const int bid = blockIdx.x;
+  const int nrt = bid < nfull ? 2 : 1;  // row tiles of this block
+  const int r0 = bid < nfull ? bid * kFfnRows : nfull * kFfnRows + (bid - nfull) * 32;
+  if (r0 >= M) return;  // uniform: before any barrier
+  const bool two = nrt == 2;
+  const int live = min(M - r0, 32 * nrt);  // rows of this block
   auto write_lut = [&]() {
 #pragma unroll
     for (int i = 0; i < 8; ++i) reinterpret_cast<v4i *>(lut)[min(tid + 256 * i, n4 - 1)] = tv[i];
@@ -990,7 +1003,6 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
   asm("" : "+v"(qhi));  // the table clamp as one med3 (both bounds in VGPRs)
 
   {
-    const int r0 = blockIdx.x * kFfnRows;  // one row block per workgroup
     // Weight fragments single-buffered: the next column tile's load is
     // issued after the current tile's MFMAs and lands during its GELU
     // epilogues; the biases are double-buffered.
@@ -1006,13 +1018,14 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
     // Phase P (PJ): y tiles wave, wave + 4, wave + 8 of the 2 x 6 (phase B's
     // tiles), K = 192 from the ctx rows; their bytes stay in yres and go to
     // LDS (208-byte rows) for LayerNorm 2.
-    v4i yres[PJ ? 3 : 1];
+    v4i yres[PJ ? 3 : 1] = {};
     if constexpr (PJ) {
       const Rq rpa = rq_setup(gp.shift_a, -128, 127), rpb = rq_setup(gp.os, -128, 127);
       const bool allp = tensor_narrow(gp.bias_max, gp.acc_lim);
 #pragma unroll
       for (int ti = 0; ti < 3; ++ti) {
         const int t = wave + 4 * ti, rt = t / 6, ct = t - rt * 6;
+        if (rt >= nrt) break;  // uniform in the wavefront
         const int8_t *ap = gp.a + (size_t)min(r0 + 32 * rt + l32, M - 1) * 192 + 16 * h;
         const int8_t *bp = gp.b + (size_t)ct * 6 * 1024 + lane * 16;
         v4i pa[6], pw[6];
@@ -1049,7 +1062,7 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
       __syncthreads();
       load_w1(0, bs[0]);
       ln_rows<kLnPrologueRow, kLnPrologueRow>(hid, kFfnRows - 1, hid, kFfnRows, fl.ln, fl.lw, r0,
-                                              M - r0);
+                                              live, two);
       __syncthreads();
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt)
@@ -1063,7 +1076,7 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
       // pass through hid (free until phase A writes it)
       load_w1(0, bs[0]);
       ln_rows<192, kLnPrologueRow>(fl.x + (size_t)r0 * 192, M - 1 - r0, hid, kFfnRows, fl.ln,
-                                   fl.lw, r0, M - r0);
+                                   fl.lw, r0, live, two);
       write_lut();
       __syncthreads();
 #pragma unroll
@@ -1110,6 +1123,10 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
       }
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
+        // a 32-row block multiplies its second tile's (unused) rows too,
+        // keeping the two accumulator chains interleaved, but skips their
+        // epilogue
+        if (rt >= nrt) break;
         v4i ow;
         if (fast) {
           int qv[16];
@@ -1141,6 +1158,8 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
     v16i bsb;  // the tile's biases, the accumulator's start
     int rt, ct;
     tile_of(0, rt, ct);
+    // tiles of this wavefront: 3, or with one row tile those of row tile 0
+    const int nt = two ? 3 : (wave < 2 ? 2 : 1);
     // the tile's biases and residual bytes (PJ: the residual from yres)
     auto operands = [&]() {
       const int arow[1] = {min(r0 + 32 * rt + l32, M - 1)};
@@ -1166,11 +1185,11 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
     // chunks of 4 through a ring of three chunk buffers: the chunk two
     // ahead (within the tile or the next tile's first two) is in flight.
 #pragma unroll 1
-    for (int ti = 0; ti < 3; ++ti) {
+    for (int ti = 0; ti < nt; ++ti) {
       const int8_t *hp = &hid[(32 * rt + l32) * kFfnHRow + 16 * h];
       const int8_t *bp = g2.b + (size_t)ct * 24 * 1024 + lane * 16;
-      int nrt = rt, nct = ct;
-      if (ti + 1 < 3) tile_of(ti + 1, nrt, nct);
+      int nxrt = rt, nct = ct;
+      if (ti + 1 < nt) tile_of(ti + 1, nxrt, nct);
       v16i acc[1][1] = {{bsb}};
 #pragma unroll
       for (int c = 0; c < 6; ++c) {
@@ -1179,7 +1198,7 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
 #pragma unroll
           for (int j = 0; j < 4; ++j)
             wb[nxt][j] = *reinterpret_cast<const v4i *>(bp + ((c + 2) * 4 + j) * 1024);
-        } else if (ti + 1 < 3) {
+        } else if (ti + 1 < nt) {
 #pragma unroll
           for (int j = 0; j < 4; ++j)
             wb[nxt][j] = *reinterpret_cast<const v4i *>(
@@ -1196,8 +1215,8 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
           g2, acc, bias4, res4, r0 + 32 * rt, ct, M, h, l32, r2a, r2b, nullptr,
           LNE ? reinterpret_cast<int8_t *>(lut) + 32 * rt * kLnPrologueRow : nullptr,
           kLnPrologueRow);
-      if (ti + 1 < 3) {
-        rt = nrt;
+      if (ti + 1 < nt) {
+        rt = nxrt;
         ct = nct;
         if constexpr (PJ) {
           yres[0] = yres[1];
@@ -1209,8 +1228,8 @@ __global__ __launch_bounds__(256) void k_ffn(GemmArgs g1, GemmArgs g2, LnPrologu
     if constexpr (LNE) {
       __syncthreads();  // every output row is in zs
       const int8_t *zs = reinterpret_cast<const int8_t *>(lut);
-      ln_rows<kLnPrologueRow, 192>(zs, kFfnRows - 1, fe.ln.out + (size_t)r0 * 192, M - r0, fe.ln,
-                                   fe.lw, r0, M - r0);
+      ln_rows<kLnPrologueRow, 192>(zs, kFfnRows - 1, fe.ln.out + (size_t)r0 * 192, live, fe.ln,
+                                   fe.lw, r0, live, two);
     }
   }
 }
@@ -1483,21 +1502,51 @@ static void launch_ffn32_d(const GemmArgs &g1, const GemmArgs &g2, const LnProlo
 template <int DIRS1, bool LN, bool LNE, bool PJ>
 static void launch_ffn_d(const GemmArgs &g1, const GemmArgs &g2, const LnPrologue &fl,
                          const LnPrologue &fe, const GemmArgs &gp, int dirsp, int dirs2, dim3 grid,
-                         size_t lds, hipStream_t s) {
+                         int nfull, size_t lds, hipStream_t s) {
   const dim3 b(256);
+  const int nf = nfull;
   switch (dirs2) {
-    case 0: hv_launch(k_ffn<DIRS1, 0, LN, LNE, PJ>, grid, b, lds, s, g1, g2, fl, fe, gp, dirsp); break;
-    case 1: hv_launch(k_ffn<DIRS1, 1, LN, LNE, PJ>, grid, b, lds, s, g1, g2, fl, fe, gp, dirsp); break;
-    case 2: hv_launch(k_ffn<DIRS1, 2, LN, LNE, PJ>, grid, b, lds, s, g1, g2, fl, fe, gp, dirsp); break;
-    default: hv_launch(k_ffn<DIRS1, 3, LN, LNE, PJ>, grid, b, lds, s, g1, g2, fl, fe, gp, dirsp); break;
+    case 0: hv_launch(k_ffn<DIRS1, 0, LN, LNE, PJ>, grid, b, lds, s, g1, g2, fl, fe, gp, dirsp, nf); break;
+    case 1: hv_launch(k_ffn<DIRS1, 1, LN, LNE, PJ>, grid, b, lds, s, g1, g2, fl, fe, gp, dirsp, nf); break;
+    case 2: hv_launch(k_ffn<DIRS1, 2, LN, LNE, PJ>, grid, b, lds, s, g1, g2, fl, fe, gp, dirsp, nf); break;
+    default: hv_launch(k_ffn<DIRS1, 3, LN, LNE, PJ>, grid, b, lds, s, g1, g2, fl, fe, gp, dirsp, nf); break;
   }
+}
+
+// CUs of the current device (cached per device).
+static int device_cus() {
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// The 64-row blocks of a k_ffn launch over m rows, the first nfull of them
+// whole and the rest split in two: with q whole rounds of one block per CU
+// and r blocks over them (1 <= r <= CUs / 2), the CUs that would run a block
+// more than the others (two at once, or one after their last pair) instead
+// share its rows with another CU, in 32-row blocks that run beside the
+// other CUs' last 64-row block.
+static int ffn_full_blocks(int m, bool balanced) {
+  const int nrb = (m + kFfnRows - 1) / kFfnRows;
+  if (!balanced) return nrb;
+  const int cus = device_cus(), q = nrb / cus, r = nrb % cus;
+  return q >= 1 && r >= 1 && 2 * r <= cus ? nrb - r : nrb;
 }
 
 // Returns HV_OK when the fused kernel was launched, 1 when the shapes or
 // exponents need the two GEMM launches instead.
 int launch_ffn(const GemmArgs &g1_in, const GemmArgs &g2_in, hipStream_t s,
                const LnPrologue *ln, const LnPrologue *ln_next, const GemmArgs *proj,
-               bool rows32) {
+               int rows) {
+  const bool rows32 = rows == FFN_ROWS32;
   GemmArgs g1 = g1_in, g2 = g2_in;
   GemmArgs gp = proj ? *proj : GemmArgs{};
   if (proj) {
@@ -1535,7 +1584,9 @@ int launch_ffn(const GemmArgs &g1_in, const GemmArgs &g2_in, hipStream_t s,
   const size_t lds = 0;  // the table's LDS is static in k_ffn
   // One workgroup per row block (the dispatcher balances them; a persistent
   // grid left half the workgroups with one block more than the others).
-  const dim3 grid((g1.m + kFfnRows - 1) / kFfnRows);
+  const int nfull = ffn_full_blocks(g1.m, proj && rows == FFN_ROWS64_BALANCED);
+  const int rest = g1.m - nfull * kFfnRows;  // rows of the 32-row blocks
+  const dim3 grid(nfull + (rest > 0 ? (rest + 31) / 32 : 0));
   const int d1 = epilogue_dirs(g1, EPI_GELU) & 1, d2 = epilogue_dirs(g2, EPI_RES);
   const LnPrologue fl = ln ? *ln : LnPrologue{}, fe = ln_next ? *ln_next : LnPrologue{};
   const int dp = proj ? epilogue_dirs(gp, EPI_RES) : 0;
@@ -1552,22 +1603,22 @@ int launch_ffn(const GemmArgs &g1_in, const GemmArgs &g2_in, hipStream_t s,
   }
   if (proj) {
     switch (mode) {
-      case 1: launch_ffn_d<4, true, false, true>(g1, g2, fl, fe, gp, dp, d2, grid, lds, s); break;
-      case 3: launch_ffn_d<4, true, true, true>(g1, g2, fl, fe, gp, dp, d2, grid, lds, s); break;
-      case 5: launch_ffn_d<5, true, false, true>(g1, g2, fl, fe, gp, dp, d2, grid, lds, s); break;
-      default: launch_ffn_d<5, true, true, true>(g1, g2, fl, fe, gp, dp, d2, grid, lds, s); break;
+      case 1: launch_ffn_d<4, true, false, true>(g1, g2, fl, fe, gp, dp, d2, grid, nfull, lds, s); break;
+      case 3: launch_ffn_d<4, true, true, true>(g1, g2, fl, fe, gp, dp, d2, grid, nfull, lds, s); break;
+      case 5: launch_ffn_d<5, true, false, true>(g1, g2, fl, fe, gp, dp, d2, grid, nfull, lds, s); break;
+      default: launch_ffn_d<5, true, true, true>(g1, g2, fl, fe, gp, dp, d2, grid, nfull, lds, s); break;
     }
     return check_hip(hipGetLastError(), "k_ffn launch");
   }
   switch (mode) {
-    case 0: launch_ffn_d<4, false, false, false>(g1, g2, fl, fe, gp, 0, d2, grid, lds, s); break;
-    case 1: launch_ffn_d<4, true, false, false>(g1, g2, fl, fe, gp, 0, d2, grid, lds, s); break;
-    case 2: launch_ffn_d<4, false, true, false>(g1, g2, fl, fe, gp, 0, d2, grid, lds, s); break;
-    case 3: launch_ffn_d<4, true, true, false>(g1, g2, fl, fe, gp, 0, d2, grid, lds, s); break;
-    case 4: launch_ffn_d<5, false, false, false>(g1, g2, fl, fe, gp, 0, d2, grid, lds, s); break;
-    case 5: launch_ffn_d<5, true, false, false>(g1, g2, fl, fe, gp, 0, d2, grid, lds, s); break;
-    case 6: launch_ffn_d<5, false, true, false>(g1, g2, fl, fe, gp, 0, d2, grid, lds, s); break;
-    default: launch_ffn_d<5, true, true, false>(g1, g2, fl, fe, gp, 0, d2, grid, lds, s); break;
+    case 0: launch_ffn_d<4, false, false, false>(g1, g2, fl, fe, gp, 0, d2, grid, nfull, lds, s); break;
+    case 1: launch_ffn_d<4, true, false, false>(g1, g2, fl, fe, gp, 0, d2, grid, nfull, lds, s); break;
+    case 2: launch_ffn_d<4, false, true, false>(g1, g2, fl, fe, gp, 0, d2, grid, nfull, lds, s); break;
+    case 3: launch_ffn_d<4, true, true, false>(g1, g2, fl, fe, gp, 0, d2, grid, nfull, lds, s); break;
+    case 4: launch_ffn_d<5, false, false, false>(g1, g2, fl, fe, gp, 0, d2, grid, nfull, lds, s); break;
+    case 5: launch_ffn_d<5, true, false, false>(g1, g2, fl, fe, gp, 0, d2, grid, nfull, lds, s); break;
+    case 6: launch_ffn_d<5, false, true, false>(g1, g2, fl, fe, gp, 0, d2, grid, nfull, lds, s); break;
+    default: launch_ffn_d<5, true, true, false>(g1, g2, fl, fe, gp, 0, d2, grid, nfull, lds, s); break;
   }
   return check_hip(hipGetLastError(), "k_ffn launch");
 }

@@ -93,11 +93,17 @@ struct LnPrologue {
   Ln32 ln;
   LnWarn lw;
 };
-// rows32 (with proj): blocks of 32 rows by eight wavefronts (k_ffn32), for
-// batches whose 64-row blocks leave CUs idle; the same outputs.
+// Row blocking of the fused FFN with proj (the same outputs in each):
+//   FFN_ROWS64           blocks of 64 rows by four wavefronts (k_ffn);
+//   FFN_ROWS32           blocks of 32 rows by eight wavefronts (k_ffn32), for
+//                        batches whose 64-row blocks leave CUs idle;
+//   FFN_ROWS64_BALANCED  k_ffn, with the last 64-row blocks split into
+//                        32-row ones when the blocks exceed a whole number
+//                        of blocks per CU by at most half the CUs.
+enum FfnRows { FFN_ROWS64 = 0, FFN_ROWS32 = 1, FFN_ROWS64_BALANCED = 2 };
 int launch_ffn(const GemmArgs &g1, const GemmArgs &g2, hipStream_t s,
                const LnPrologue *ln = nullptr, const LnPrologue *ln_next = nullptr,
-               const GemmArgs *proj = nullptr, bool rows32 = false);
+               const GemmArgs *proj = nullptr, int rows = FFN_ROWS64);
 // Fills acc_lim / narrow_ok / da / db / os of the int32 epilogue paths.
 void epilogue_limits_pub(GemmArgs &g, int epilogue);
 

@@ -72,6 +72,30 @@ def test_fused_ffn_wide_biases_and_ragged_rows_vs_oracle(oracle, wide):
         assert np.array_equal(zs[i], z), i
 
 
+@pytest.mark.parametrize("blk,tail", [(0, 0), (5, 1), (10, 2)])
+def test_fused_ffn_split_last_blocks_vs_oracle(oracle, blk, tail):
+    """A block over 32,768 rows or more runs the fused FFN in 64-row blocks
+    whose last few, beyond whole rounds of one block per CU, are split into
+    32-row blocks (the second row tile's steps skipped): 168 images of 197
+    rows are 33,096 rows, 512 whole blocks and 11 halves, the last of 8 rows;
+    `tail` trims the last images so the final half ends mid-tile."""
+    from heatvit_amd.transformer import transformer_block_batch
+    _, params = synth.throughput_workload(1)
+    bp = params.blocks[blk]
+    rng = np.random.default_rng(40 + blk)
+    lens = [197] * 168
+    if tail == 1:
+        lens[-1] = 150  # 33,049 rows: 512 whole blocks, 9 halves, the last of 25 rows
+    elif tail == 2:
+        lens[-1:] = [1, 30, 64]  # 32,994 rows: 8 halves, the last of 2 rows
+    xs = [rng.integers(-128, 128, (n, 192)).astype(np.int8) for n in lens]
+    assert sum(lens) >= 32768
+    zs = transformer_block_batch(xs, bp)
+    for i, x in enumerate(xs):
+        z, _ = oracle.transformer_block(x, bp, checkpoints=False)
+        assert np.array_equal(zs[i], z), (blk, i, len(x))
+
+
 # Ragged token counts of a pruned stage: partial 32-row tiles and 64-row
 # FFN blocks, images of one and two key tiles, many small images; 32 images,
 # so the attention kernel runs the QKV GEMM.
