@@ -96,6 +96,39 @@ def test_fused_ffn_split_last_blocks_vs_oracle(oracle, blk, tail):
         assert np.array_equal(zs[i], z), (blk, i, len(x))
 
 
+def test_fused_ffn_split_blocks_past_the_live_rows_vs_oracle(oracle):
+    """The row capacity sizes the launch (33,096 rows: 512 whole blocks and
+    11 halves) while the batch's offsets hold 32,900 live rows: the fifth
+    half keeps 4 live rows, the last six exit before any work, and the rows
+    past the live count are never written."""
+    import torch
+    from heatvit_amd import _lib
+    from heatvit_amd.device import DeviceBlock
+    _, params = synth.throughput_workload(1)
+    bp = params.blocks[3]
+    rng = np.random.default_rng(77)
+    lens = [197] * 167 + [1]
+    live, cap = sum(lens), 33096
+    assert live == 32900
+    xs = [rng.integers(-128, 128, (n, 192)).astype(np.int8) for n in lens]
+    x = np.concatenate(xs + [rng.integers(-128, 128, (cap - live, 192)).astype(np.int8)])
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    L = _lib.lib()
+    db = DeviceBlock(bp)
+    xd = torch.from_numpy(x).cuda()
+    off = torch.from_numpy(offsets).cuda()
+    z = torch.full((cap, 192), 55, dtype=torch.int8, device="cuda")
+    ws = torch.empty(L.hv_block_workspace_bytes(len(lens), cap), dtype=torch.uint8, device="cuda")
+    _lib.check(L.hv_block_forward(db.struct, xd.data_ptr(), off.data_ptr(), len(lens), cap,
+                                  z.data_ptr(), None, None, None, ws.data_ptr(), ws.numel(),
+                                  torch.cuda.current_stream().cuda_stream), "block")
+    zs = z.cpu().numpy()
+    assert (zs[live:] == 55).all()
+    for i, xi in enumerate(xs):
+        want, _ = oracle.transformer_block(xi, bp, checkpoints=False)
+        assert np.array_equal(zs[offsets[i]:offsets[i + 1]], want), (i, len(xi))
+
+
 # Ragged token counts of a pruned stage: partial 32-row tiles and 64-row
 # FFN blocks, images of one and two key tiles, many small images; 32 images,
 # so the attention kernel runs the QKV GEMM.
