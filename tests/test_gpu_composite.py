@@ -378,6 +378,20 @@ def test_throughput_batch_vs_oracle_and_deterministic(oracle):
     assert np.array_equal(r3.logits, r1.logits[100:103])
 
 
+def test_model_split_ffn_blocks_at_200_images_vs_oracle(oracle):
+    """200 images: stage 0's 39,400 rows are 616 blocks of 64 rows on 256
+    CUs, 104 past two per CU, so the fused FFN runs 512 whole blocks and 208
+    of 32 rows (the last of 8 rows), with and without the next LayerNorm 1."""
+    from heatvit_amd.model import HeatViTModel
+    imgs, params = synth.throughput_workload(200)
+    r = HeatViTModel().infer_batch(imgs, params)
+    logits, counts, status, warnings = oracle.model_infer_batch(imgs, params)
+    assert not status.any()
+    assert np.array_equal(r.logits, logits)
+    assert np.array_equal(r.token_counts, counts)
+    assert np.array_equal(r.warnings, warnings)
+
+
 def test_unpruned_control_vs_oracle(oracle):
     from heatvit_amd.model import HeatViTModel
     imgs, params = synth.throughput_workload()  # all 256 images of the control
