@@ -43,6 +43,7 @@
 // first requant shifts left by k, |bias| <= ((2^31 - 1) >> k) - K*2^14 (so
 // v << k stays inside int32); the other cases call the exact 64/128-bit
 // form, kept out of line.
+#include <atomic>
 #include "hv_device.h"
 #include "hv_internal.h"
 #include "gelu_lut.inc"  // generated at build time by gen_gelu_lut.py
@@ -1513,19 +1514,20 @@ static void launch_ffn_d(const GemmArgs &g1, const GemmArgs &g2, const LnPrologu
   }
 }
 
-// CUs of the current device (cached per device).
+// CUs of the current device (cached per device; host threads may race to
+// fill an entry, all with the same value).
 static int device_cus() {
-  static int cus[64];
+  static std::atomic<int> cus[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cus[dev]) {
-    int n = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (!n) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         n <= 0)
       n = 256;
-    cus[dev] = n;
+    cus[dev].store(n, std::memory_order_relaxed);
   }
-  return cus[dev];
+  return n;
 }
 
 // The 64-row blocks of a k_ffn launch over m rows, the first nfull of them
