@@ -382,7 +382,7 @@ def main():
                     help="skip the float-image front-end measurement")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the per-config lines and the standalone softmax")
-    ap.add_argument("--sustained-seconds", type=float, default=2.5,
+    ap.add_argument("--sustained-seconds", type=float, default=5.0,
                     help="length of the sustained pipelined run reported beside `value` "
                          "(0 skips it)")
     ap.add_argument("--copy-calibration", action="store_true",
