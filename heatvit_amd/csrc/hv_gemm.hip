@@ -1515,7 +1515,8 @@ static void launch_ffn_d(const GemmArgs &g1, const GemmArgs &g2, const LnPrologu
 }
 
 // CUs of the current device (cached per device; host threads may race to
-// fill an entry, all with the same value).
+// fill an entry, all with the same value).  It only places the split of
+// ffn_full_blocks: any split gives the same outputs.
 static int device_cus() {
   static std::atomic<int> cus[64];
   int dev = 0;
